@@ -1,0 +1,104 @@
+// Shared helpers for the eth_amd HIP kernels (gfx950 / CDNA4 only).
+//
+// Every exported entry point returns an int status (ETH_OK on success) and
+// records a message retrievable through eth_last_error().  Kernels are
+// launched on the caller's stream; nothing here allocates device memory on a
+// hot path.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string>
+
+#include "../../include/eth_amd.h"
+
+namespace eth {
+
+void set_error(const char* fmt, ...);
+
+#define ETH_CHECK_ARG(cond, ...)              \
+  do {                                        \
+    if (!(cond)) {                            \
+      ::eth::set_error(__VA_ARGS__);          \
+      return ETH_ERR_INVALID;                 \
+    }                                         \
+  } while (0)
+
+#define ETH_CHECK_LAUNCH(what)                                              \
+  do {                                                                      \
+    hipError_t _e = hipGetLastError();                                      \
+    if (_e != hipSuccess) {                                                 \
+      ::eth::set_error("%s: launch failed: %s", what, hipGetErrorString(_e)); \
+      return ETH_ERR_HIP;                                                   \
+    }                                                                       \
+  } while (0)
+
+typedef uint16_t bf16_t;
+typedef _Float16 f16_t;
+
+// float -> bfloat16, round to nearest even; NaN stays a quiet NaN.
+__device__ __forceinline__ bf16_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (bf16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (bf16_t)(u >> 16);
+}
+__device__ __forceinline__ float bf2f(bf16_t h) {
+  return __uint_as_float(((uint32_t)h) << 16);
+}
+__device__ __forceinline__ uint16_t f2h_bits(float f) {
+  f16_t h = (f16_t)f;
+  return *reinterpret_cast<uint16_t*>(&h);
+}
+__device__ __forceinline__ float h2f_bits(uint16_t b) {
+  f16_t h = *reinterpret_cast<f16_t*>(&b);
+  return (float)h;
+}
+
+// Load/store one element of a tensor whose dtype is chosen at run time.
+__device__ __forceinline__ float load_elem(const void* p, int64_t i, int dtype) {
+  if (dtype == ETH_F32) return reinterpret_cast<const float*>(p)[i];
+  uint16_t b = reinterpret_cast<const uint16_t*>(p)[i];
+  return dtype == ETH_BF16 ? bf2f(b) : h2f_bits(b);
+}
+__device__ __forceinline__ void store_elem(void* p, int64_t i, int dtype, float v) {
+  if (dtype == ETH_F32) {
+    reinterpret_cast<float*>(p)[i] = v;
+  } else {
+    reinterpret_cast<uint16_t*>(p)[i] = dtype == ETH_BF16 ? f2bf(v) : f2h_bits(v);
+  }
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+// Block-wide sum for blockDim.x == NT (multiple of 64).  `red` must hold
+// NT/64 floats of shared memory.  Every thread receives the total.
+template <int NT>
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  if (lane == 0) red[wid] = v;
+  __syncthreads();
+  float t = 0.f;
+#pragma unroll
+  for (int w = 0; w < NT / 64; ++w) t += red[w];
+  __syncthreads();
+  return t;
+}
+
+inline int dtype_size(int dtype) { return dtype == ETH_F32 ? 4 : 2; }
+inline bool valid_dtype(int dtype) {
+  return dtype == ETH_F32 || dtype == ETH_F16 || dtype == ETH_BF16;
+}
+
+}  // namespace eth

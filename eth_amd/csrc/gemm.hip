@@ -1,0 +1,308 @@
+// bf16/fp16 GEMM on CDNA4 matrix cores (v_mfma_f32_32x32x16_{bf16,f16}),
+// fp32 accumulation, LDS-staged double-buffered tiles.
+//
+//   C[m, n] (+)= alpha * sum_k A(m, k) * B(k, n)  (+ bias[n])
+//
+// A(m, k) is read K-contiguous (A[m*lda + k]) or M-contiguous (A[k*lda + m]);
+// B(k, n) is read K-contiguous (B[n*ldb + k]) or N-contiguous (B[k*ldb + n]).
+// The three GPT linear-layer products are
+//   forward  Y = X W^T      : A K-contiguous, B K-contiguous
+//   dgrad    dX = dY W      : A K-contiguous, B N-contiguous
+//   wgrad    dW += dY^T X   : A M-contiguous, B N-contiguous, fp32 C += (the
+//                             Megatron main_grad accumulation, fused)
+// M-contiguous / N-contiguous operands are transposed in registers on their
+// way into LDS (4 k-rows x 8 columns per thread), so every LDS tile is stored
+// K-contiguous and each MFMA operand is one 16-byte LDS read.
+//
+// Workgroup: 256 threads = 4 waves in a 2x2 grid; each wave owns a
+// (BM/2) x (BN/2) sub-tile made of 32x32 MFMA blocks.  Tiles are assigned
+// XCD-aware (consecutive workgroups land on different XCDs, so the tile id
+// is remapped to give each XCD a contiguous range) and in GROUP_M-row
+// groups so neighbouring workgroups share A and B tiles in L2.
+//
+// Replaces the F.linear / cuBLAS calls of mpu/layers.py:357-370,452-470 and
+// the main_grad.add_ hook of model/distributed.py:116-123.
+#include "common.h"
+
+namespace eth {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+template <bool FP16>
+__device__ __forceinline__ f32x16_t mfma32(const uint4& a, const uint4& b, const f32x16_t& c) {
+  if constexpr (FP16) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  }
+}
+
+constexpr int kGemmThreads = 256;
+constexpr int kPad = 8;  // LDS row padding (elements): 16 B breaks bank aliasing
+
+// Map a linear workgroup id to (tile_m, tile_n): XCD-contiguous, then
+// GROUP_M-row grouped.
+__device__ __forceinline__ void tile_coords(int pid, int tiles_m, int tiles_n, int& tm, int& tn) {
+  constexpr int kXcds = 8, kGroupM = 8;
+  const int total = tiles_m * tiles_n;
+  const int per = (total + kXcds - 1) / kXcds;
+  const int tall = total % kXcds == 0 ? kXcds : total % kXcds;
+  const int xcd = pid % kXcds, local = pid / kXcds;
+  pid = xcd < tall ? xcd * per + local : tall * per + (xcd - tall) * (per - 1) + local;
+  const int in_group = kGroupM * tiles_n;
+  const int first_m = (pid / in_group) * kGroupM;
+  const int gm = min(tiles_m - first_m, kGroupM);
+  tm = first_m + (pid % in_group) % gm;
+  tn = (pid % in_group) / gm;
+}
+
+// Load a ROWS x BK tile of a K-contiguous operand (row r at P[(r0+r)*ld + k])
+// into registers: CPT 16-byte chunks per thread.
+template <int ROWS, int BK>
+struct KTile {
+  static constexpr int CPR = BK / 8;
+  static constexpr int CPT = ROWS * CPR / kGemmThreads;
+  uint4 v[CPT];
+  __device__ __forceinline__ void load(const uint16_t* __restrict__ P, int64_t ld, int r0, int rows,
+                                       int k0, int K) {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int c = threadIdx.x + i * kGemmThreads;
+      const int r = c / CPR, kc = (c % CPR) * 8;
+      if (r0 + r < rows && k0 + kc < K)
+        v[i] = *reinterpret_cast<const uint4*>(P + (int64_t)(r0 + r) * ld + k0 + kc);
+      else
+        v[i] = make_uint4(0, 0, 0, 0);
+    }
+  }
+  __device__ __forceinline__ void store(uint16_t* S) const {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int c = threadIdx.x + i * kGemmThreads;
+      const int r = c / CPR, kc = (c % CPR) * 8;
+      *reinterpret_cast<uint4*>(S + r * (BK + kPad) + kc) = v[i];
+    }
+  }
+};
+
+// Load a BK x ROWS tile of an operand contiguous along the row index
+// (element (r, k) at P[k*ld + r0 + r]): each thread reads 4 k-rows of 8
+// consecutive r and writes them transposed (8 rows of 4 k) into LDS.
+template <int ROWS, int BK>
+struct RTile {
+  static constexpr int RG = ROWS / 8, KG = BK / 4;
+  static constexpr int BPT = RG * KG / kGemmThreads;
+  uint4 v[BPT][4];
+  __device__ __forceinline__ void load(const uint16_t* __restrict__ P, int64_t ld, int r0, int rows,
+                                       int k0, int K) {
+#pragma unroll
+    for (int b = 0; b < BPT; ++b) {
+      const int blk = threadIdx.x + b * kGemmThreads;
+      const int rg = blk % RG, kg = blk / RG;
+      const int r = r0 + rg * 8;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int k = k0 + kg * 4 + j;
+        if (r < rows && k < K)
+          v[b][j] = *reinterpret_cast<const uint4*>(P + (int64_t)k * ld + r);
+        else
+          v[b][j] = make_uint4(0, 0, 0, 0);
+      }
+    }
+  }
+  __device__ __forceinline__ void store(uint16_t* S) const {
+#pragma unroll
+    for (int b = 0; b < BPT; ++b) {
+      const int blk = threadIdx.x + b * kGemmThreads;
+      const int rg = blk % RG, kg = blk / RG;
+      const uint32_t* w0 = reinterpret_cast<const uint32_t*>(&v[b][0]);
+      const uint32_t* w1 = reinterpret_cast<const uint32_t*>(&v[b][1]);
+      const uint32_t* w2 = reinterpret_cast<const uint32_t*>(&v[b][2]);
+      const uint32_t* w3 = reinterpret_cast<const uint32_t*>(&v[b][3]);
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        // rows 2p and 2p+1 of the 8-row group
+        const uint32_t a0 = w0[p], a1 = w1[p], a2 = w2[p], a3 = w3[p];
+        uint2 lo, hi;
+        lo.x = (a0 & 0xffffu) | (a1 << 16);
+        lo.y = (a2 & 0xffffu) | (a3 << 16);
+        hi.x = (a0 >> 16) | (a1 & 0xffff0000u);
+        hi.y = (a2 >> 16) | (a3 & 0xffff0000u);
+        uint16_t* row = S + (rg * 8 + 2 * p) * (BK + kPad) + kg * 4;
+        *reinterpret_cast<uint2*>(row) = lo;
+        *reinterpret_cast<uint2*>(row + (BK + kPad)) = hi;
+      }
+    }
+  }
+};
+
+template <int ROWS, int BK, bool KCONTIG>
+struct TileLoader;
+template <int ROWS, int BK>
+struct TileLoader<ROWS, BK, true> : KTile<ROWS, BK> {};
+template <int ROWS, int BK>
+struct TileLoader<ROWS, BK, false> : RTile<ROWS, BK> {};
+
+struct GemmArgs {
+  const uint16_t* A;
+  const uint16_t* B;
+  void* C;
+  const uint16_t* bias;
+  int M, N, K;
+  int64_t lda, ldb, ldc;
+  int c_dtype;
+  int flags;
+  float alpha;
+};
+
+template <int BM, int BN, int BK, bool A_K, bool B_K, bool FP16>
+__global__ void __launch_bounds__(kGemmThreads) gemm_kernel(GemmArgs g) {
+  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int TM = WM / 32, TN = WN / 32;
+  constexpr int LDS_ROW = BK + kPad;
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * LDS_ROW];
+  __shared__ __attribute__((aligned(16))) uint16_t Bs[2][BN * LDS_ROW];
+
+  const int tiles_m = (g.M + BM - 1) / BM, tiles_n = (g.N + BN - 1) / BN;
+  int tm, tn;
+  tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int wm = wid >> 1, wn = wid & 1;
+  const int lr = lane & 31, lk = (lane >> 5) * 8;
+
+  f32x16_t acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  TileLoader<BM, BK, A_K> la;
+  TileLoader<BN, BK, B_K> lb;
+  const int nk = (g.K + BK - 1) / BK;
+  la.load(g.A, g.lda, m0, g.M, 0, g.K);
+  lb.load(g.B, g.ldb, n0, g.N, 0, g.K);
+  la.store(As[0]);
+  lb.store(Bs[0]);
+  __syncthreads();
+
+  for (int kt = 0; kt < nk; ++kt) {
+    const int st = kt & 1;
+    const bool more = kt + 1 < nk;
+    if (more) {
+      la.load(g.A, g.lda, m0, g.M, (kt + 1) * BK, g.K);
+      lb.load(g.B, g.ldb, n0, g.N, (kt + 1) * BK, g.K);
+    }
+    const uint16_t* as = As[st] + (wm * WM + lr) * LDS_ROW + lk;
+    const uint16_t* bs = Bs[st] + (wn * WN + lr) * LDS_ROW + lk;
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ++ks) {
+      uint4 af[TM], bfr[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+        af[i] = *reinterpret_cast<const uint4*>(as + i * 32 * LDS_ROW + ks * 16);
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        bfr[j] = *reinterpret_cast<const uint4*>(bs + j * 32 * LDS_ROW + ks * 16);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = mfma32<FP16>(af[i], bfr[j], acc[i][j]);
+    }
+    if (more) {
+      la.store(As[st ^ 1]);
+      lb.store(Bs[st ^ 1]);
+    }
+    __syncthreads();
+  }
+
+  // epilogue: lane holds column n = lane%32 and rows (r/4)*8 + (lane/32)*4 + r%4
+  const bool accumulate = g.flags & ETH_GEMM_ACCUMULATE;
+  const bool has_bias = (g.flags & ETH_GEMM_BIAS) && g.bias;
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int n = n0 + wn * WN + j * 32 + lr;
+    if (n >= g.N) continue;
+    float bn = 0.f;
+    if (has_bias) bn = FP16 ? h2f_bits(g.bias[n]) : bf2f(g.bias[n]);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + wm * WM + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+        if (m >= g.M) continue;
+        const float v = acc[i][j][r] * g.alpha + bn;
+        const int64_t off = (int64_t)m * g.ldc + n;
+        if (g.c_dtype == ETH_F32) {
+          float* c = reinterpret_cast<float*>(g.C) + off;
+          *c = accumulate ? *c + v : v;
+        } else if (g.c_dtype == ETH_BF16) {
+          reinterpret_cast<uint16_t*>(g.C)[off] = f2bf(v);
+        } else {
+          reinterpret_cast<uint16_t*>(g.C)[off] = f2h_bits(v);
+        }
+      }
+    }
+  }
+}
+
+template <int BM, int BN, int BK, bool FP16>
+static int launch_layout(const GemmArgs& a, int a_k, int b_k, hipStream_t s) {
+  const int tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
+  if (a_k && b_k)
+    gemm_kernel<BM, BN, BK, true, true, FP16><<<tiles, kGemmThreads, 0, s>>>(a);
+  else if (a_k && !b_k)
+    gemm_kernel<BM, BN, BK, true, false, FP16><<<tiles, kGemmThreads, 0, s>>>(a);
+  else if (!a_k && !b_k)
+    gemm_kernel<BM, BN, BK, false, false, FP16><<<tiles, kGemmThreads, 0, s>>>(a);
+  else
+    gemm_kernel<BM, BN, BK, false, true, FP16><<<tiles, kGemmThreads, 0, s>>>(a);
+  ETH_CHECK_LAUNCH("eth_gemm");
+  return ETH_OK;
+}
+
+}  // namespace eth
+
+using namespace eth;
+
+extern "C" int eth_gemm(const void* A, int64_t lda, int a_kcontig, const void* B, int64_t ldb,
+                        int b_kcontig, void* C, int64_t ldc, int c_dtype, const void* bias,
+                        int64_t M, int64_t N, int64_t K, int in_dtype, int flags, float alpha,
+                        void* stream) {
+  ETH_CHECK_ARG(in_dtype == ETH_BF16 || in_dtype == ETH_F16, "eth_gemm: inputs must be bf16 or fp16");
+  ETH_CHECK_ARG(valid_dtype(c_dtype), "eth_gemm: bad output dtype %d", c_dtype);
+  ETH_CHECK_ARG(M > 0 && N > 0 && K > 0 && M < (1LL << 31) && N < (1LL << 31) && K < (1LL << 31),
+                "eth_gemm: bad shape %lld x %lld x %lld", (long long)M, (long long)N, (long long)K);
+  ETH_CHECK_ARG(A && B && C, "eth_gemm: null operand");
+  ETH_CHECK_ARG(K % 8 == 0, "eth_gemm: K (%lld) must be a multiple of 8", (long long)K);
+  ETH_CHECK_ARG(lda % 8 == 0 && ldb % 8 == 0, "eth_gemm: lda/ldb must be multiples of 8");
+  ETH_CHECK_ARG(((uintptr_t)A & 15) == 0 && ((uintptr_t)B & 15) == 0, "eth_gemm: A/B must be 16-byte aligned");
+  ETH_CHECK_ARG(a_kcontig ? lda >= K : (M % 8 == 0 && lda >= M), "eth_gemm: bad A layout");
+  ETH_CHECK_ARG(b_kcontig ? ldb >= K : (N % 8 == 0 && ldb >= N), "eth_gemm: bad B layout");
+  ETH_CHECK_ARG(ldc >= N, "eth_gemm: ldc < N");
+  ETH_CHECK_ARG(!(flags & ETH_GEMM_ACCUMULATE) || c_dtype == ETH_F32, "eth_gemm: accumulate needs fp32 C");
+  ETH_CHECK_ARG(!(flags & ETH_GEMM_BIAS) || bias, "eth_gemm: bias flag without bias");
+  GemmArgs a;
+  a.A = (const uint16_t*)A;
+  a.B = (const uint16_t*)B;
+  a.C = C;
+  a.bias = (const uint16_t*)bias;
+  a.M = (int)M;
+  a.N = (int)N;
+  a.K = (int)K;
+  a.lda = lda;
+  a.ldb = ldb;
+  a.ldc = ldc;
+  a.c_dtype = c_dtype;
+  a.flags = flags;
+  a.alpha = alpha;
+  hipStream_t s = (hipStream_t)stream;
+  if (in_dtype == ETH_BF16) return launch_layout<128, 128, 64, false>(a, a_kcontig, b_kcontig, s);
+  return launch_layout<128, 128, 64, true>(a, a_kcontig, b_kcontig, s);
+}

@@ -1,0 +1,308 @@
+// Block-wise gradient synchronization, local half: bucket pack, fused
+// unpack / normalization / unscale / inf-nan flag / L2 partials, and the
+// norm finalize.  One workgroup per chunk (<= ETH_CHUNK_ELEMS elements); a
+// chunk is a strided 2-D block of one main_grad tensor.  The payload side is
+// always contiguous, so contiguous chunks stream with 16-byte accesses.
+//
+// Semantics follow eth/runtime/megatron/grad_sync/executor.py:199-261 (pack,
+// mul_, unpack), optimizer/optimizer.py:436-461 (unscale + found_inf) and
+// grad_sync/optimizer_semantics.py:563-595 (L2 statistic + coefficient).
+#include <stdarg.h>
+
+#include "common.h"
+
+namespace eth {
+
+static thread_local std::string g_last_error;
+
+void set_error(const char* fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+}
+
+constexpr int kThreads = 256;
+
+template <typename T>
+struct Elem;
+template <>
+struct Elem<float> {
+  static constexpr int kVec = 4;
+  typedef float4 V;
+  __device__ static float get(float x, int) { return x; }
+  __device__ static float put(float v, int) { return v; }
+};
+template <>
+struct Elem<uint16_t> {
+  static constexpr int kVec = 8;
+  typedef uint4 V;
+  __device__ static float get(uint16_t x, int dt) { return dt == ETH_BF16 ? bf2f(x) : h2f_bits(x); }
+  __device__ static uint16_t put(float v, int dt) { return dt == ETH_BF16 ? f2bf(v) : f2h_bits(v); }
+};
+
+template <typename T>
+__device__ __forceinline__ bool aligned16(const T* p) {
+  return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+}
+
+// ---------------------------------------------------------------- pack ---
+template <typename T>
+__global__ void __launch_bounds__(kThreads) pack_kernel(const eth_chunk_t* __restrict__ chunks,
+                                                        T* __restrict__ payload, int dtype) {
+  const eth_chunk_t c = chunks[blockIdx.x];
+  const T* src = reinterpret_cast<const T*>(c.src);
+  T* dst = payload + c.dst;
+  const float scale = c.scale;
+  const bool scaled = scale != 1.0f;
+  const int64_t n = (int64_t)c.rows * c.row_len;
+  constexpr int VW = Elem<T>::kVec;
+  typedef typename Elem<T>::V V;
+  if (c.rows == 1 && aligned16(src) && aligned16(dst)) {
+    const int64_t nv = n / VW;
+    const V* s = reinterpret_cast<const V*>(src);
+    V* d = reinterpret_cast<V*>(dst);
+    for (int64_t i = threadIdx.x; i < nv; i += kThreads) {
+      V x = s[i];
+      if (scaled) {
+        T* e = reinterpret_cast<T*>(&x);
+#pragma unroll
+        for (int j = 0; j < VW; ++j) e[j] = Elem<T>::put(Elem<T>::get(e[j], dtype) * scale, dtype);
+      }
+      d[i] = x;
+    }
+    for (int64_t i = nv * VW + threadIdx.x; i < n; i += kThreads) {
+      T x = src[i];
+      dst[i] = scaled ? Elem<T>::put(Elem<T>::get(x, dtype) * scale, dtype) : x;
+    }
+  } else {
+    for (int64_t i = threadIdx.x; i < n; i += kThreads) {
+      const int64_t r = i / c.row_len, col = i - r * c.row_len;
+      T x = src[r * c.src_stride + col];
+      dst[i] = scaled ? Elem<T>::put(Elem<T>::get(x, dtype) * scale, dtype) : x;
+    }
+  }
+}
+
+// -------------------------------------------------------------- unpack ---
+// One element of the fused unpack; returns g*g for the norm statistic.
+template <typename T>
+__device__ __forceinline__ float unpack_one(T& pay, T& out, float norm, float inv, int flags,
+                                            int dtype, bool& bad) {
+  float v = Elem<T>::get(pay, dtype);
+  if (norm != 1.0f) {
+    T r = Elem<T>::put(v * norm, dtype);
+    v = Elem<T>::get(r, dtype);
+    if (flags & ETH_UNPACK_WRITEBACK) pay = r;
+  }
+  float g = v;
+  if (flags & ETH_UNPACK_UNSCALE) g = v * inv;  // fp32 only (checked on host)
+  bad |= !isfinite(v);
+  out = Elem<T>::put(g, dtype);
+  return g * g;
+}
+
+template <typename T>
+__global__ void __launch_bounds__(kThreads) unpack_kernel(const eth_chunk_t* __restrict__ chunks,
+                                                          T* __restrict__ payload, int dtype,
+                                                          float norm, float inv, int flags,
+                                                          float* __restrict__ found_inf,
+                                                          double* __restrict__ partials,
+                                                          int64_t partial_base) {
+  __shared__ float red[kThreads / 64];
+  const eth_chunk_t c = chunks[blockIdx.x];
+  T* dstp = reinterpret_cast<T*>(c.src);
+  T* pay = payload + c.dst;
+  const int64_t n = (int64_t)c.rows * c.row_len;
+  constexpr int VW = Elem<T>::kVec;
+  typedef typename Elem<T>::V V;
+  float sq = 0.f;
+  bool bad = false;
+  if (c.rows == 1 && aligned16(dstp) && aligned16(pay)) {
+    const int64_t nv = n / VW;
+    V* p = reinterpret_cast<V*>(pay);
+    V* d = reinterpret_cast<V*>(dstp);
+    for (int64_t i = threadIdx.x; i < nv; i += kThreads) {
+      V x = p[i], y;
+      T* xe = reinterpret_cast<T*>(&x);
+      T* ye = reinterpret_cast<T*>(&y);
+#pragma unroll
+      for (int j = 0; j < VW; ++j) sq += unpack_one<T>(xe[j], ye[j], norm, inv, flags, dtype, bad);
+      if ((flags & ETH_UNPACK_WRITEBACK) && norm != 1.0f) p[i] = x;
+      d[i] = y;
+    }
+    for (int64_t i = nv * VW + threadIdx.x; i < n; i += kThreads)
+      sq += unpack_one<T>(pay[i], dstp[i], norm, inv, flags, dtype, bad);
+  } else {
+    for (int64_t i = threadIdx.x; i < n; i += kThreads) {
+      const int64_t r = i / c.row_len, col = i - r * c.row_len;
+      sq += unpack_one<T>(pay[i], dstp[r * c.src_stride + col], norm, inv, flags, dtype, bad);
+    }
+  }
+  if (flags & ETH_UNPACK_STATS) {
+    if (bad) *found_inf = 1.0f;
+    float tot = block_sum<kThreads>(sq, red);
+    if (threadIdx.x == 0)
+      partials[partial_base + blockIdx.x] = (c.flags & ETH_CHUNK_NORM) ? (double)tot : 0.0;
+  }
+}
+
+// ------------------------------------------------- standalone statistics ---
+__global__ void __launch_bounds__(kThreads) stats_kernel(const eth_chunk_t* __restrict__ chunks,
+                                                         float inv, int flags,
+                                                         float* __restrict__ found_inf,
+                                                         double* __restrict__ partials,
+                                                         int64_t partial_base) {
+  __shared__ float red[kThreads / 64];
+  const eth_chunk_t c = chunks[blockIdx.x];
+  float* g = reinterpret_cast<float*>(c.src);
+  const int64_t n = (int64_t)c.rows * c.row_len;
+  const bool unscale = flags & ETH_UNPACK_UNSCALE;
+  float sq = 0.f;
+  bool bad = false;
+  if (c.rows == 1 && aligned16(g)) {
+    const int64_t nv = n / 4;
+    float4* gv = reinterpret_cast<float4*>(g);
+    for (int64_t i = threadIdx.x; i < nv; i += kThreads) {
+      float4 x = gv[i];
+      bad |= !isfinite(x.x) | !isfinite(x.y) | !isfinite(x.z) | !isfinite(x.w);
+      if (unscale) {
+        x.x *= inv; x.y *= inv; x.z *= inv; x.w *= inv;
+        gv[i] = x;
+      }
+      sq += x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w;
+    }
+    for (int64_t i = nv * 4 + threadIdx.x; i < n; i += kThreads) {
+      float x = g[i];
+      bad |= !isfinite(x);
+      if (unscale) g[i] = x = x * inv;
+      sq += x * x;
+    }
+  } else {
+    for (int64_t i = threadIdx.x; i < n; i += kThreads) {
+      const int64_t r = i / c.row_len, col = i - r * c.row_len;
+      float* e = g + r * c.src_stride + col;
+      float x = *e;
+      bad |= !isfinite(x);
+      if (unscale) *e = x = x * inv;
+      sq += x * x;
+    }
+  }
+  if (bad) *found_inf = 1.0f;
+  float tot = block_sum<kThreads>(sq, red);
+  if (threadIdx.x == 0)
+    partials[partial_base + blockIdx.x] = (c.flags & ETH_CHUNK_NORM) ? (double)tot : 0.0;
+}
+
+// ---------------------------------------------------------- finalize ---
+__global__ void __launch_bounds__(1024) finalize_kernel(const double* __restrict__ partials,
+                                                        int64_t n, double max_norm,
+                                                        double* __restrict__ stats) {
+  __shared__ double red[1024];
+  double s = 0.0;
+  for (int64_t i = threadIdx.x; i < n; i += 1024) s += partials[i];
+  red[threadIdx.x] = s;
+  __syncthreads();
+  for (int w = 512; w > 0; w >>= 1) {
+    if (threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    const double tot = red[0];
+    const double norm = sqrt(tot);
+    stats[0] = tot;
+    stats[1] = norm;
+    stats[2] = max_norm > 0.0 ? max_norm / (norm + 1.0e-6) : 1.0;
+  }
+}
+
+__global__ void fill_kernel(float* dst, int64_t n, float v) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    dst[i] = v;
+}
+
+}  // namespace eth
+
+using namespace eth;
+
+extern "C" {
+
+int eth_abi_version(void) { return 1; }
+
+const char* eth_last_error(void) { return g_last_error.c_str(); }
+
+int eth_fill_f32(float* dst, int64_t n, float value, void* stream) {
+  ETH_CHECK_ARG(n >= 0 && (n == 0 || dst), "eth_fill_f32: bad arguments");
+  if (n == 0) return ETH_OK;
+  int64_t blocks = (n + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  fill_kernel<<<(int)blocks, 256, 0, (hipStream_t)stream>>>(dst, n, value);
+  ETH_CHECK_LAUNCH("eth_fill_f32");
+  return ETH_OK;
+}
+
+int eth_bucket_pack(const eth_chunk_t* chunks, int64_t n_chunks, void* payload, int dtype,
+                    void* stream) {
+  ETH_CHECK_ARG(valid_dtype(dtype), "eth_bucket_pack: unsupported dtype %d", dtype);
+  ETH_CHECK_ARG(n_chunks >= 0 && n_chunks < (1LL << 31), "eth_bucket_pack: bad chunk count %lld",
+                (long long)n_chunks);
+  if (n_chunks == 0) return ETH_OK;
+  ETH_CHECK_ARG(chunks && payload, "eth_bucket_pack: null pointer");
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == ETH_F32)
+    pack_kernel<float><<<(int)n_chunks, kThreads, 0, s>>>(chunks, (float*)payload, dtype);
+  else
+    pack_kernel<uint16_t><<<(int)n_chunks, kThreads, 0, s>>>(chunks, (uint16_t*)payload, dtype);
+  ETH_CHECK_LAUNCH("eth_bucket_pack");
+  return ETH_OK;
+}
+
+int eth_bucket_unpack(const eth_chunk_t* chunks, int64_t n_chunks, void* payload, int dtype,
+                      float normalization_scale, float inv_loss_scale, int flags,
+                      float* found_inf, double* partials, int64_t partial_base, void* stream) {
+  ETH_CHECK_ARG(valid_dtype(dtype), "eth_bucket_unpack: unsupported dtype %d", dtype);
+  ETH_CHECK_ARG(n_chunks >= 0 && n_chunks < (1LL << 31), "eth_bucket_unpack: bad chunk count");
+  ETH_CHECK_ARG(!(flags & ETH_UNPACK_UNSCALE) || dtype == ETH_F32,
+                "eth_bucket_unpack: unscale requires fp32 gradients");
+  ETH_CHECK_ARG(!(flags & ETH_UNPACK_STATS) || (found_inf && partials && partial_base >= 0),
+                "eth_bucket_unpack: statistics requested without buffers");
+  if (n_chunks == 0) return ETH_OK;
+  ETH_CHECK_ARG(chunks && payload, "eth_bucket_unpack: null pointer");
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == ETH_F32)
+    unpack_kernel<float><<<(int)n_chunks, kThreads, 0, s>>>(chunks, (float*)payload, dtype,
+                                                            normalization_scale, inv_loss_scale,
+                                                            flags, found_inf, partials,
+                                                            partial_base);
+  else
+    unpack_kernel<uint16_t><<<(int)n_chunks, kThreads, 0, s>>>(
+        chunks, (uint16_t*)payload, dtype, normalization_scale, inv_loss_scale, flags, found_inf,
+        partials, partial_base);
+  ETH_CHECK_LAUNCH("eth_bucket_unpack");
+  return ETH_OK;
+}
+
+int eth_grad_stats(const eth_chunk_t* chunks, int64_t n_chunks, float inv_loss_scale, int flags,
+                   float* found_inf, double* partials, int64_t partial_base, void* stream) {
+  ETH_CHECK_ARG(n_chunks >= 0 && n_chunks < (1LL << 31), "eth_grad_stats: bad chunk count");
+  ETH_CHECK_ARG(found_inf && partials && partial_base >= 0, "eth_grad_stats: null buffers");
+  if (n_chunks == 0) return ETH_OK;
+  ETH_CHECK_ARG(chunks, "eth_grad_stats: null chunk table");
+  stats_kernel<<<(int)n_chunks, kThreads, 0, (hipStream_t)stream>>>(
+      chunks, inv_loss_scale, flags, found_inf, partials, partial_base);
+  ETH_CHECK_LAUNCH("eth_grad_stats");
+  return ETH_OK;
+}
+
+int eth_grad_norm_finalize(const double* partials, int64_t n, double max_norm, double* stats,
+                           void* stream) {
+  ETH_CHECK_ARG(n >= 0 && stats && (n == 0 || partials), "eth_grad_norm_finalize: bad arguments");
+  finalize_kernel<<<1, 1024, 0, (hipStream_t)stream>>>(partials, n, max_norm, stats);
+  ETH_CHECK_LAUNCH("eth_grad_norm_finalize");
+  return ETH_OK;
+}
+
+}  // extern "C"

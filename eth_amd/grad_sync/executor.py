@@ -1,0 +1,327 @@
+"""Execution of an immutable gradient synchronization plan on the GPU.
+
+Drop-in for eth/runtime/megatron/grad_sync/executor.py:24-261
+(GradientBucketExecutor): same constructor, `execute(normalization_scale)`,
+`scratch(dtype)`, `scratch_dtypes`, same validation errors carrying
+`bucket {id} rank {r} logical_param_id {id} fragment {id}` context.
+
+What differs is how a bucket is moved.  Instead of one `copy_` per segment
+plus a `mul_` per bucket, every segment of every bucket is resolved once, at
+construction, into a device table of chunks (2-D strided blocks of at most
+ETH_CHUNK_ELEMS elements).  Per bucket and step the executor then issues one
+pack launch, the unchanged `all_reduce_sum(payload, handle)` collective seam,
+and one unpack launch that also applies the normalization scale.  When an
+optimizer binds a GradientStatistics object, the same unpack launch also
+unscales the gradients, raises the inf/nan flag and writes per-chunk sums of
+squares for the global L2 norm, so the optimizer does not re-read them.
+"""
+
+import math
+
+import numpy as np
+import torch
+
+from .. import _native as nat
+
+
+def _dtype_name(dtype):
+    return str(dtype).removeprefix("torch.")
+
+
+def _normalize_axis(axis, shape, logical_param_id):
+    if axis < 0:
+        axis += len(shape)
+    if not 0 <= axis < len(shape):
+        raise ValueError(f"logical_param_id {logical_param_id} has invalid partition axis {axis}")
+    return axis
+
+
+def split_block(base, elem_size, rows, row_len, stride, dst, scale, flags, out):
+    """Append chunks covering a rows x row_len block (row stride `stride`)."""
+    cap = nat.CHUNK_ELEMS
+    if rows == 1 or row_len == stride:
+        total = rows * row_len
+        for start in range(0, total, cap):
+            n = min(cap, total - start)
+            out.append((base + start * elem_size, dst + start, n, 1, n, scale, flags))
+        return
+    if row_len >= cap:
+        for r in range(rows):
+            for start in range(0, row_len, cap):
+                n = min(cap, row_len - start)
+                out.append((base + (r * stride + start) * elem_size, dst + r * row_len + start, stride, 1, n, scale, flags))
+        return
+    per = max(1, cap // row_len)
+    for r0 in range(0, rows, per):
+        nr = min(per, rows - r0)
+        out.append((base + r0 * stride * elem_size, dst + r0 * row_len, stride, nr, row_len, scale, flags))
+
+
+def chunk_table(entries):
+    table = np.zeros(len(entries), dtype=nat.CHUNK_DTYPE)
+    if entries:
+        cols = list(zip(*entries))
+        table["src"] = np.asarray(cols[0], dtype=np.uint64)
+        table["dst"] = cols[1]
+        table["src_stride"] = cols[2]
+        table["rows"] = cols[3]
+        table["row_len"] = cols[4]
+        table["scale"] = cols[5]
+        table["flags"] = cols[6]
+    return table
+
+
+class GradientStatistics:
+    """Device-side found_inf flag, per-chunk L2 partials and the finalized
+    [sum of squares, norm, clip coefficient] of one optimizer step."""
+
+    def __init__(self, n_partials, device):
+        self.device = torch.device(device)
+        self.found_inf = torch.zeros(1, dtype=torch.float32, device=self.device)
+        self.partials = torch.zeros(max(1, n_partials), dtype=torch.float64, device=self.device)
+        self.stats = torch.zeros(3, dtype=torch.float64, device=self.device)
+        self.n_partials = n_partials
+        self.n_partials_used = n_partials
+        self.fresh = False
+        self.inv_scale_used = None
+
+    def reset(self):
+        nat.call("eth_fill_f32", nat.ptr(self.found_inf), 1, 0.0, nat.stream_ptr(self.device))
+
+    def finalize(self, max_norm):
+        nat.call(
+            "eth_grad_norm_finalize",
+            nat.ptr(self.partials),
+            self.n_partials_used,
+            float(max_norm),
+            nat.ptr(self.stats),
+            nat.stream_ptr(self.device),
+        )
+
+
+class GradientBucketExecutor:
+    def __init__(
+        self,
+        plan,
+        global_rank,
+        local_descriptors,
+        local_runtime_bindings,
+        process_group_registry,
+        all_reduce_sum,
+        runtime_evidence_dir=None,
+    ):
+        self.plan = plan
+        self.global_rank = global_rank
+        self._registry = process_group_registry
+        self._all_reduce_sum = all_reduce_sum
+        self._fragments = {f.fragment_id: f for f in plan.canonical_fragments}
+        self._groups = {g.process_group_id: g for g in plan.process_groups}
+        self._descriptors = self._unique_by_logical_id(local_descriptors, "descriptor")
+        self._runtime_bindings = self._unique_by_logical_id(local_runtime_bindings, "runtime binding")
+        self._binding_specs = {
+            b.fragment_id: b
+            for rank, bindings in plan.local_fragment_bindings_by_rank
+            if rank == global_rank
+            for b in bindings
+        }
+        if runtime_evidence_dir:
+            raise ValueError("runtime evidence recording is not supported by the eth_amd executor")
+        self._validate_local_contract()
+        self._scratch = self._allocate_scratch()
+        self._tables = self._build_tables()
+        self._statistics = None
+        self._inv_scale = 1.0
+
+    # ------------------------------------------------------------ contract --
+    @staticmethod
+    def _unique_by_logical_id(items, kind):
+        out = {}
+        for item in items:
+            if item.logical_param_id in out:
+                raise ValueError(f"duplicate {kind} for logical_param_id {item.logical_param_id}")
+            out[item.logical_param_id] = item
+        return out
+
+    def _rank_buckets(self):
+        for bucket in self.plan.global_bucket_order:
+            if self.global_rank in self._groups[bucket.process_group_id].ranks:
+                yield bucket
+
+    def _bucket_error(self, bucket, message, binding=None):
+        context = f"bucket {bucket.bucket_id} rank {self.global_rank}"
+        if binding is not None:
+            context += f" logical_param_id {binding.logical_param_id} fragment {binding.fragment_id}"
+        return ValueError(f"{context}: {message}")
+
+    def _validate_local_contract(self):
+        devices = set()
+        for bucket in self._rank_buckets():
+            for placement in bucket.placements:
+                binding = self._binding_specs.get(placement.fragment_id)
+                if binding is None:
+                    frag = self._fragments[placement.fragment_id]
+
+                    class _Missing:
+                        logical_param_id = frag.logical_param_id
+                        fragment_id = frag.fragment_id
+
+                    raise self._bucket_error(bucket, "missing local binding", _Missing)
+                runtime = self._runtime_bindings.get(binding.logical_param_id)
+                descriptor = self._descriptors.get(binding.logical_param_id)
+                if runtime is None or descriptor is None:
+                    raise self._bucket_error(bucket, "missing descriptor or main_grad binding", binding)
+                if tuple(runtime.main_grad.shape) != tuple(binding.source_segments[0].source_shape):
+                    raise self._bucket_error(bucket, "main_grad shape mismatch", binding)
+                if _dtype_name(runtime.main_grad.dtype) != bucket.grad_dtype.removeprefix("torch."):
+                    raise self._bucket_error(bucket, "main_grad dtype mismatch", binding)
+                if torch.device(runtime.main_grad.device) != torch.device(runtime.device):
+                    raise self._bucket_error(bucket, "main_grad device mismatch", binding)
+                devices.add(torch.device(runtime.main_grad.device))
+        if len(devices) > 1:
+            raise ValueError(
+                f"rank {self.global_rank} has multiple gradient execution devices: {sorted(map(str, devices))}"
+            )
+        self._device = next(iter(devices), None)
+        if self._device is not None and self._device.type != "cuda":
+            raise ValueError(
+                f"rank {self.global_rank}: the eth_amd executor runs on the GPU only, got {self._device}"
+            )
+
+    def _allocate_scratch(self):
+        wanted = {
+            dtype: numel
+            for (rank, dtype), numel in self.plan.max_scratch_numel_by_rank_and_dtype
+            if rank == self.global_rank
+        }
+        if not wanted:
+            return {}
+        if self._device is None:
+            raise ValueError(f"rank {self.global_rank} participates in gradient buckets without a device")
+        by_name = {_dtype_name(r.main_grad.dtype): r.main_grad.dtype for r in self._runtime_bindings.values()}
+        scratch = {}
+        for name, numel in wanted.items():
+            dtype = by_name.get(name.removeprefix("torch."))
+            if dtype is None:
+                raise ValueError(f"rank {self.global_rank} has no main_grad with dtype {name}")
+            scratch[name] = torch.empty(numel, dtype=dtype, device=self._device)
+        return scratch
+
+    @property
+    def scratch_dtypes(self):
+        return tuple(sorted(self._scratch))
+
+    def scratch(self, dtype_name):
+        return self._scratch[dtype_name]
+
+    # -------------------------------------------------------- chunk tables --
+    def _segment_block(self, binding, segment):
+        """(address, rows, row_len, stride) of one segment of main_grad."""
+        runtime = self._runtime_bindings[binding.logical_param_id]
+        descriptor = self._descriptors[binding.logical_param_id]
+        grad = runtime.main_grad
+        if not grad.is_contiguous():
+            raise ValueError(f"logical_param_id {binding.logical_param_id} main_grad must be contiguous")
+        esize = grad.element_size()
+        tensor_parallel = getattr(descriptor, "tensor_parallel", descriptor.partition_dim >= 0)
+        if not tensor_parallel:
+            if segment.flattened_numel != grad.numel():
+                raise ValueError(f"logical_param_id {binding.logical_param_id} replicated source numel mismatch")
+            return grad.data_ptr(), 1, grad.numel(), grad.numel()
+        shape = tuple(grad.shape)
+        axis = _normalize_axis(descriptor.partition_dim, shape, binding.logical_param_id)
+        if math.prod(segment.source_shape) != grad.numel():
+            raise ValueError(f"logical_param_id {binding.logical_param_id} source shape mismatch")
+        if segment.source_dim_offset + segment.source_dim_length > shape[axis] or segment.source_dim_offset < 0:
+            raise ValueError(f"logical_param_id {binding.logical_param_id} segment outside the tensor")
+        outer = math.prod(shape[:axis])
+        inner = math.prod(shape[axis + 1 :])
+        addr = grad.data_ptr() + segment.source_dim_offset * inner * esize
+        return addr, outer, segment.source_dim_length * inner, shape[axis] * inner
+
+    def _build_tables(self):
+        tables = []
+        partial_base = 0
+        for bucket in self._rank_buckets():
+            entries = []
+            for placement in bucket.placements:
+                fragment = self._fragments[placement.fragment_id]
+                binding = self._binding_specs[placement.fragment_id]
+                owned = fragment.include_in_optimizer_norm and fragment.norm_owner_rank == self.global_rank
+                flags = nat.CHUNK_NORM if owned else 0
+                esize = self._runtime_bindings[binding.logical_param_id].main_grad.element_size()
+                dst = placement.destination_offset
+                copied = 0
+                for segment in binding.source_segments:
+                    addr, rows, row_len, stride = self._segment_block(binding, segment)
+                    n = rows * row_len
+                    if n != segment.flattened_numel:
+                        raise self._bucket_error(bucket, "source segment numel mismatch", binding)
+                    if dst + n > bucket.exact_numel:
+                        raise self._bucket_error(bucket, "placement exceeds exact_numel", binding)
+                    split_block(addr, esize, rows, row_len, stride, dst, float(binding.contribution_scale), flags, entries)
+                    dst += n
+                    copied += n
+                if copied != fragment.numel:
+                    raise self._bucket_error(bucket, f"packed {copied} elements, expected {fragment.numel}", binding)
+            table = chunk_table(entries)
+            dev = nat.table_to_device(table, self._device) if len(table) else None
+            tables.append((bucket, dev, len(table), partial_base))
+            partial_base += len(table)
+        self._n_partials = partial_base
+        return tables
+
+    # ----------------------------------------------------------- statistics --
+    @property
+    def n_partials(self):
+        return self._n_partials
+
+    def covered_gradients(self):
+        """main_grad tensors this executor writes, by logical id."""
+        return {lid: r.main_grad for lid, r in self._runtime_bindings.items()}
+
+    def bind_statistics(self, statistics):
+        """Let execute() also unscale, flag inf/nan and collect L2 partials."""
+        if statistics is not None and statistics.n_partials < self._n_partials:
+            raise ValueError("statistics buffer is smaller than the executor's chunk count")
+        self._statistics = statistics
+
+    def set_inv_loss_scale(self, inv_scale):
+        self._inv_scale = float(inv_scale)
+
+    # ------------------------------------------------------------ execute --
+    def execute(self, normalization_scale=1.0):
+        stats = self._statistics
+        stream = nat.stream_ptr(self._device) if self._device is not None else None
+        flags = 0
+        if stats is not None:
+            stats.reset()
+            flags |= nat.UNPACK_STATS
+            if self._inv_scale != 1.0:
+                flags |= nat.UNPACK_UNSCALE
+        if normalization_scale != 1.0:
+            flags |= nat.UNPACK_WRITEBACK
+        for bucket, table, n_chunks, base in self._tables:
+            payload = self._scratch[bucket.grad_dtype][: bucket.exact_numel]
+            dcode = nat.dtype_code(payload.dtype)
+            if n_chunks:
+                nat.call("eth_bucket_pack", nat.ptr(table), n_chunks, nat.ptr(payload), dcode, stream)
+            self._all_reduce_sum(payload, self._registry.handle(bucket.process_group_id))
+            if n_chunks:
+                f = flags if (dcode == nat.ETH_F32 or not (flags & nat.UNPACK_UNSCALE)) else flags & ~nat.UNPACK_UNSCALE
+                nat.call(
+                    "eth_bucket_unpack",
+                    nat.ptr(table),
+                    n_chunks,
+                    nat.ptr(payload),
+                    dcode,
+                    float(normalization_scale),
+                    float(self._inv_scale),
+                    f,
+                    nat.ptr(stats.found_inf) if stats is not None else None,
+                    nat.ptr(stats.partials) if stats is not None else None,
+                    base,
+                    stream,
+                )
+        if stats is not None:
+            stats.fresh = True
+            stats.inv_scale_used = self._inv_scale

@@ -1,0 +1,172 @@
+"""FusedAdamW: torch.optim-compatible AdamW whose step is one HIP launch.
+
+Drop-in for the optimizer built by
+eth/runtime/megatron/optimizer/__init__.py:61-72 (apex FusedAdam in AdamW
+mode, falling back to torch.optim.AdamW): same param_groups keys
+(params, lr, betas, eps, weight_decay) and the same per-parameter state
+(`step`, `exp_avg`, `exp_avg_sq`) that evidence and checkpoints read.
+
+Moment buffers of all parameters live in two flat fp32 allocations (one
+view per parameter), and the per-step launch walks a device table of
+(tensor, chunk) records built once; the table is rebuilt only when a
+parameter's or gradient's storage changes.
+"""
+
+import numpy as np
+import torch
+
+from .. import _native as nat
+
+
+class FusedAdamW(torch.optim.Optimizer):
+    def __init__(self, params, lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=1e-2):
+        if lr < 0.0 or eps < 0.0 or weight_decay < 0.0:
+            raise ValueError("invalid AdamW hyper-parameter")
+        if not (0.0 <= betas[0] < 1.0 and 0.0 <= betas[1] < 1.0):
+            raise ValueError(f"invalid betas {betas}")
+        defaults = dict(lr=lr, betas=tuple(betas), eps=eps, weight_decay=weight_decay)
+        super().__init__(params, defaults)
+        self._table_key = None
+        self._tables = None
+        self._model_copies = {}
+        self._model_dtype = nat.ETH_F32
+        self._allocate_state()
+
+    # ---------------------------------------------------------------- state --
+    def _all_params(self):
+        return [p for g in self.param_groups for p in g["params"]]
+
+    def _allocate_state(self):
+        params = self._all_params()
+        for p in params:
+            if p.dtype != torch.float32:
+                raise ValueError("FusedAdamW keeps fp32 parameters (masters); got " + str(p.dtype))
+            if not p.is_contiguous():
+                raise ValueError("FusedAdamW parameters must be contiguous")
+        if not params:
+            return
+        device = params[0].device
+        # 16-byte aligned views: pad every tensor to a multiple of 4 elements
+        sizes = [(p.numel() + 3) // 4 * 4 for p in params]
+        total = sum(sizes)
+        self._exp_avg_flat = torch.zeros(total, dtype=torch.float32, device=device)
+        self._exp_avg_sq_flat = torch.zeros(total, dtype=torch.float32, device=device)
+        off = 0
+        for p, n in zip(params, sizes):
+            st = self.state[p]
+            st["step"] = torch.tensor(0.0)
+            st["exp_avg"] = self._exp_avg_flat[off : off + p.numel()].view_as(p)
+            st["exp_avg_sq"] = self._exp_avg_sq_flat[off : off + p.numel()].view_as(p)
+            off += n
+
+    def set_model_copies(self, mapping, model_dtype):
+        """Master parameter -> 16-bit model parameter written by every step."""
+        self._model_copies = dict(mapping)
+        self._model_dtype = nat.dtype_code(model_dtype)
+        self._table_key = None
+
+    # ---------------------------------------------------------------- table --
+    def _key(self):
+        return tuple(
+            (p.data_ptr(), p.grad.data_ptr() if p.grad is not None else 0, g["lr"], g["weight_decay"])
+            for g in self.param_groups
+            for p in g["params"]
+        )
+
+    def _build_tables(self):
+        tensors = []
+        chunks = []
+        cap = nat.CHUNK_ELEMS
+        for g in self.param_groups:
+            for p in g["params"]:
+                if p.grad is None:
+                    continue
+                if p.grad.dtype != torch.float32 or not p.grad.is_contiguous() or p.grad.shape != p.shape:
+                    raise ValueError("FusedAdamW needs contiguous fp32 gradients shaped like the parameter")
+                st = self.state[p]
+                model = self._model_copies.get(p)
+                idx = len(tensors)
+                tensors.append(
+                    (
+                        p.data_ptr(),
+                        p.grad.data_ptr(),
+                        st["exp_avg"].data_ptr(),
+                        st["exp_avg_sq"].data_ptr(),
+                        model.data_ptr() if model is not None else 0,
+                        p.numel(),
+                        float(g["lr"]),
+                        float(g["weight_decay"]),
+                    )
+                )
+                for start in range(0, p.numel(), cap):
+                    chunks.append((idx, min(cap, p.numel() - start), start))
+        ttab = np.zeros(len(tensors), dtype=nat.ADAM_TENSOR_DTYPE)
+        for i, name in enumerate(nat.ADAM_TENSOR_DTYPE.names):
+            ttab[name] = [t[i] for t in tensors]
+        ctab = np.zeros(len(chunks), dtype=nat.ADAM_CHUNK_DTYPE)
+        if chunks:
+            arr = np.asarray(chunks, dtype=np.int64)
+            ctab["tensor"] = arr[:, 0]
+            ctab["n"] = arr[:, 1]
+            ctab["start"] = arr[:, 2]
+        device = self._all_params()[0].device
+        self._tables = (
+            nat.table_to_device(ttab, device) if len(ttab) else None,
+            nat.table_to_device(ctab, device) if len(ctab) else None,
+            len(ctab),
+        )
+
+    # ----------------------------------------------------------------- step --
+    @torch.no_grad()
+    def step(self, closure=None, stats=None, found_inf=None):
+        """One AdamW step.  `stats` (device double[3], clip coefficient at
+        index 2) and `found_inf` (device float[1]) are optional; with
+        found_inf set to non-zero the launch leaves every tensor unchanged."""
+        loss = closure() if closure is not None else None
+        params = self._all_params()
+        if not params:
+            return loss
+        key = self._key()
+        if key != self._table_key:
+            self._build_tables()
+            self._table_key = key
+        ttab, ctab, n_chunks = self._tables
+        if n_chunks == 0:
+            return loss
+        groups = {(g["betas"], g["eps"]) for g in self.param_groups}
+        if len(groups) != 1:
+            raise ValueError("FusedAdamW needs identical betas/eps across parameter groups")
+        (beta1, beta2), eps = next(iter(groups))
+        # all parameters step together; the state mirrors torch's per-param step
+        step = int(self.state[params[0]]["step"].item()) + 1
+        nat.call(
+            "eth_adam_step",
+            nat.ptr(ttab),
+            nat.ptr(ctab),
+            n_chunks,
+            float(beta1),
+            float(beta2),
+            float(eps),
+            step,
+            self._model_dtype,
+            nat.ptr(stats),
+            nat.ptr(found_inf),
+            nat.stream_ptr(params[0].device),
+        )
+        self._pending_step = step
+        if found_inf is None:
+            self.commit_step(True)
+        return loss
+
+    def commit_step(self, applied=True):
+        """Advance the per-parameter step counters after a launched step
+        (skipped steps on overflow leave them unchanged, as torch does when
+        step() is not called)."""
+        step = getattr(self, "_pending_step", None)
+        if step is None:
+            return
+        if applied:
+            for p in self._all_params():
+                if p.grad is not None:
+                    self.state[p]["step"].fill_(float(step))
+        self._pending_step = None

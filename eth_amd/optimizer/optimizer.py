@@ -1,0 +1,373 @@
+"""Megatron optimizer wrappers on the fused HIP path.
+
+Step contract of eth/runtime/megatron/optimizer/optimizer.py:493-531:
+`step() -> (update_successful, grad_norm, num_zeros)`; copy model grads to
+main grads, unscale + inf/nan check (fp16 loss scaling), skip the step and
+back off the scale on overflow, clip to `clip_grad` by the global L2 norm,
+AdamW on fp32 masters, copy masters to the 16-bit model parameters.
+
+How it runs here: the unscale / flag / sum of squares are either already
+done by the gradient-sync unpack (when an executor is bound with
+`bind_gradient_sync`) or done by one standalone statistics launch; the norm
+and clip coefficient are finalized on the device; the AdamW launch reads the
+coefficient and the overflow flag from device memory and writes the model
+copy itself.  The host reads the flag and the norm once, after everything is
+queued.
+"""
+
+import numpy as np
+import torch
+
+from .. import _native as nat
+from ..grad_sync.executor import GradientStatistics, chunk_table, split_block
+from .fused_adam import FusedAdamW
+
+
+def _flat_master_copies(model_params):
+    """fp32 master copies of `model_params`, views of one 16-byte aligned buffer."""
+    sizes = [(p.numel() + 3) // 4 * 4 for p in model_params]
+    device = model_params[0].device
+    flat = torch.empty(sum(sizes), dtype=torch.float32, device=device)
+    masters, off = [], 0
+    for p, n in zip(model_params, sizes):
+        m = flat[off : off + p.numel()].view_as(p)
+        m.copy_(p.detach())
+        m.requires_grad_(True)
+        for attr in ("tensor_model_parallel", "partition_dim", "partition_stride", "shared"):
+            if hasattr(p, attr):
+                setattr(m, attr, getattr(p, attr))
+        masters.append(m)
+        off += n
+    return flat, masters
+
+
+class MegatronOptimizer:
+    def __init__(self, optimizer, clip_grad, log_num_zeros_in_grad, params_have_main_grad):
+        self.optimizer = optimizer
+        self.clip_grad = float(clip_grad)
+        self.log_num_zeros_in_grad = log_num_zeros_in_grad
+        self.params_have_main_grad = params_have_main_grad
+        self.grad_scaler = None
+        self._executor = None
+        self._statistics = None
+        self._stats_tables = None
+        self._stats_key = None
+        self._model_to_optimizer_param = {}
+
+    # ----------------------------------------------------------- plumbing --
+    @property
+    def param_groups(self):
+        return self.optimizer.param_groups
+
+    def get_parameters(self):
+        return [p for g in self.optimizer.param_groups for p in g["params"]]
+
+    def get_loss_scale(self):
+        if self.grad_scaler is None:
+            return torch.ones(1, dtype=torch.float32, device=self._device())
+        return self.grad_scaler.scale
+
+    def scale_loss(self, loss):
+        return self.get_loss_scale() * loss
+
+    def _device(self):
+        return self.get_parameters()[0].device
+
+    def state_for_model_parameter(self, model_parameter):
+        p = self._model_to_optimizer_param.get(id(model_parameter))
+        if p is None:
+            raise ValueError("model parameter is not owned by this optimizer")
+        return self.optimizer.state.get(p, {})
+
+    def optimizer_parameter_for_model_parameter(self, model_parameter):
+        p = self._model_to_optimizer_param.get(id(model_parameter))
+        if p is None:
+            raise ValueError("model parameter is not owned by this optimizer")
+        return p
+
+    def bind_gradient_sync(self, executor):
+        """Fuse unscale / inf-nan flag / L2 partials into `executor`'s unpack.
+
+        Only valid when every optimizer gradient is an fp32 main_grad the
+        executor writes (bf16 or fp32 training)."""
+        covered = {g.data_ptr() for g in executor.covered_gradients().values()}
+        grads = self._bound_main_grads()
+        if any(g is None or g.dtype != torch.float32 or g.data_ptr() not in covered for g in grads):
+            raise ValueError("fused gradient statistics need fp32 main grads written by the executor")
+        self._executor = executor
+        self._statistics = GradientStatistics(executor.n_partials, self._device())
+        executor.bind_statistics(self._statistics)
+        executor.set_inv_loss_scale(self._inv_scale())
+
+    def _bound_main_grads(self):
+        raise NotImplementedError
+
+    def _inv_scale(self):
+        return self.grad_scaler.inv_scale_value if self.grad_scaler is not None else 1.0
+
+    # --------------------------------------------------------- statistics --
+    def _norm_owned(self, param):
+        return not getattr(param, "shared", False) or getattr(param, "shared_root", False)
+
+    def _standalone_statistics(self, unscale):
+        params = [p for p in self.get_parameters() if p.grad is not None]
+        key = tuple((p.grad.data_ptr(), p.grad.numel()) for p in params)
+        if key != self._stats_key:
+            entries = []
+            for p in params:
+                g = p.grad
+                if g.dtype != torch.float32 or not g.is_contiguous():
+                    raise ValueError("optimizer gradients must be contiguous fp32")
+                flags = nat.CHUNK_NORM if self._norm_owned(p) else 0
+                split_block(g.data_ptr(), 4, 1, g.numel(), g.numel(), 0, 1.0, flags, entries)
+            table = chunk_table(entries)
+            self._stats_tables = (nat.table_to_device(table, self._device()) if len(table) else None, len(table))
+            self._stats_key = key
+            if self._statistics is None or self._statistics.n_partials < len(table):
+                self._statistics = GradientStatistics(len(table), self._device())
+                if self._executor is not None:
+                    self._executor.bind_statistics(None)
+                    self._executor = None
+        table, n = self._stats_tables
+        st = self._statistics
+        st.reset()
+        flags = nat.UNPACK_UNSCALE if unscale else 0
+        nat.call(
+            "eth_grad_stats",
+            nat.ptr(table),
+            n,
+            float(self._inv_scale()),
+            flags,
+            nat.ptr(st.found_inf),
+            nat.ptr(st.partials),
+            0,
+            nat.stream_ptr(self._device()),
+        )
+        # partials past this table's chunks must not leak into the norm
+        st.n_partials_used = n
+        return st
+
+    def count_zeros(self):
+        total = 0
+        for p in self.get_parameters():
+            if p.grad is not None and self._norm_owned(p):
+                total += p.grad.numel() - int(torch.count_nonzero(p.grad).item())
+        return float(total)
+
+    # --------------------------------------------------------------- step --
+    def _copy_model_grads_to_main_grads(self):
+        raise NotImplementedError
+
+    @torch.no_grad()
+    def step(self):
+        self._copy_model_grads_to_main_grads()
+        scaler = self.grad_scaler
+        need_norm = self.clip_grad > 0.0
+        st = self._statistics
+        fused = st is not None and self._executor is not None and st.fresh
+        if fused and scaler is not None and st.inv_scale_used != self._inv_scale():
+            raise RuntimeError("loss scale changed between gradient sync and optimizer step")
+        if fused:
+            st.n_partials_used = self._executor.n_partials
+        elif scaler is not None or need_norm:
+            st = self._standalone_statistics(unscale=scaler is not None)
+        if st is not None:
+            st.fresh = False
+        if need_norm:
+            nat.call(
+                "eth_grad_norm_finalize",
+                nat.ptr(st.partials),
+                st.n_partials_used,
+                self.clip_grad,
+                nat.ptr(st.stats),
+                nat.stream_ptr(self._device()),
+            )
+        self.optimizer.step(
+            stats=st.stats if need_norm else None,
+            found_inf=st.found_inf if scaler is not None else None,
+        )
+        if scaler is not None:
+            found = bool(st.found_inf.item() > 0)
+            scaler.update(found)
+            self.optimizer.commit_step(not found)
+            if self._executor is not None:
+                self._executor.set_inv_loss_scale(self._inv_scale())
+            if found:
+                return False, None, None
+        grad_norm = float(st.stats[1].item()) if need_norm else None
+        num_zeros = self.count_zeros() if self.log_num_zeros_in_grad else None
+        return True, grad_norm, num_zeros
+
+    def zero_grad(self, set_to_none=True):
+        for p in self.get_parameters():
+            p.grad = None
+
+    def state_dict(self):
+        out = {"optimizer": self.optimizer.state_dict()}
+        if self.grad_scaler is not None:
+            out["grad_scaler"] = self.grad_scaler.state_dict()
+        return out
+
+
+class Float16OptimizerWithFloat16Params(MegatronOptimizer):
+    """bf16/fp16 model parameters with fp32 masters
+    (eth/runtime/megatron/optimizer/optimizer.py:228-572)."""
+
+    def __init__(
+        self,
+        param_groups,
+        lr,
+        betas,
+        eps,
+        weight_decay,
+        clip_grad,
+        log_num_zeros_in_grad=False,
+        params_have_main_grad=True,
+        use_contiguous_buffers_in_ddp=True,
+        bf16=True,
+        grad_scaler=None,
+    ):
+        self.float16_groups = []
+        self.fp32_from_float16_groups = []
+        self.fp32_from_fp32_groups = []
+        model_params = [p for g in param_groups for p in g["params"]]
+        half = [p for p in model_params if p.dtype in (torch.float16, torch.bfloat16)]
+        self._master_flat, masters = _flat_master_copies(half) if half else (None, [])
+        master_of = {id(p): m for p, m in zip(half, masters)}
+        groups = []
+        for g in param_groups:
+            f16, f32m, f32 = [], [], []
+            for p in g["params"]:
+                if id(p) in master_of:
+                    f16.append(p)
+                    f32m.append(master_of[id(p)])
+                elif p.dtype == torch.float32:
+                    f32.append(p)
+                else:
+                    raise TypeError(f"unsupported parameter dtype {p.dtype}")
+            self.float16_groups.append(f16)
+            self.fp32_from_float16_groups.append(f32m)
+            self.fp32_from_fp32_groups.append(f32)
+            ng = {k: v for k, v in g.items() if k != "params"}
+            ng["params"] = f32m + f32
+            groups.append(ng)
+        optimizer = FusedAdamW(groups, lr=lr, betas=betas, eps=eps, weight_decay=weight_decay)
+        super().__init__(optimizer, clip_grad, log_num_zeros_in_grad, params_have_main_grad)
+        self.bf16 = bf16
+        self.grad_scaler = grad_scaler
+        self.use_contiguous_buffers_in_ddp = use_contiguous_buffers_in_ddp
+        model_dtypes = {p.dtype for p in half}
+        if len(model_dtypes) > 1:
+            raise TypeError("mixed bf16/fp16 model parameters")
+        if half:
+            optimizer.set_model_copies({master_of[id(p)]: p for p in half}, half[0].dtype)
+        for p in model_params:
+            self._model_to_optimizer_param[id(p)] = master_of.get(id(p), p)
+
+    def _bound_main_grads(self):
+        out = []
+        for mg, fg in zip(self.float16_groups, self.fp32_from_float16_groups):
+            out.extend(getattr(p, "main_grad", None) for p in mg)
+        for group in self.fp32_from_fp32_groups:
+            out.extend(getattr(p, "main_grad", None) for p in group)
+        return out
+
+    def _copy_model_grads_to_main_grads(self):
+        for mg, fg in zip(self.float16_groups, self.fp32_from_float16_groups):
+            for model_param, main_param in zip(mg, fg):
+                if self.params_have_main_grad:
+                    main_param.grad = model_param.main_grad.float()
+                elif model_param.grad is not None:
+                    main_param.grad = model_param.grad.float()
+                model_param.grad = None
+        if self.params_have_main_grad:
+            for group in self.fp32_from_fp32_groups:
+                for p in group:
+                    p.grad = p.main_grad
+
+    def _norm_owned(self, param):
+        return super()._norm_owned(param)
+
+    def reload_model_params(self):
+        for mg, fg in zip(self.float16_groups, self.fp32_from_float16_groups):
+            for p, m in zip(mg, fg):
+                m.data.copy_(p.data)
+
+
+class FP32Optimizer(MegatronOptimizer):
+    """fp32 model parameters (eth/runtime/megatron/optimizer/optimizer.py:576-659)."""
+
+    def __init__(self, param_groups, lr, betas, eps, weight_decay, clip_grad, log_num_zeros_in_grad=False, params_have_main_grad=True):
+        optimizer = FusedAdamW(param_groups, lr=lr, betas=betas, eps=eps, weight_decay=weight_decay)
+        super().__init__(optimizer, clip_grad, log_num_zeros_in_grad, params_have_main_grad)
+        for p in self.get_parameters():
+            self._model_to_optimizer_param[id(p)] = p
+
+    def _bound_main_grads(self):
+        return [getattr(p, "main_grad", None) for p in self.get_parameters()]
+
+    def _copy_model_grads_to_main_grads(self):
+        if self.params_have_main_grad:
+            for p in self.get_parameters():
+                p.grad = p.main_grad
+
+
+def get_params_for_weight_decay_optimization(modules, layernorm_types=()):
+    """LayerNorm parameters and every `bias` get weight decay 0
+    (eth/runtime/megatron/optimizer/__init__.py:37-58)."""
+    from ..model.layers import LayerNorm
+
+    ln_types = (LayerNorm, torch.nn.LayerNorm, *layernorm_types)
+    decay = {"params": []}
+    no_decay = {"params": [], "weight_decay": 0.0}
+    for module in modules:
+        for sub in module.modules():
+            items = [(n, p) for n, p in sub._parameters.items() if p is not None]
+            if isinstance(sub, ln_types):
+                no_decay["params"].extend(p for _, p in items)
+            else:
+                decay["params"].extend(p for n, p in items if n != "bias")
+                no_decay["params"].extend(p for n, p in items if n == "bias")
+    return decay, no_decay
+
+
+def get_megatron_optimizer(
+    modules,
+    lr,
+    weight_decay,
+    betas=(0.9, 0.999),
+    eps=1e-8,
+    clip_grad=1.0,
+    fp16=False,
+    bf16=False,
+    loss_scale=None,
+    initial_loss_scale=2.0**32,
+    min_loss_scale=1.0,
+    loss_scale_window=1000,
+    hysteresis=2,
+    log_num_zeros_in_grad=False,
+    params_have_main_grad=True,
+):
+    """Factory with the decisions of eth/runtime/megatron/optimizer/__init__.py:61-126."""
+    from .grad_scaler import ConstantGradScaler, DynamicGradScaler
+
+    groups = [g for g in get_params_for_weight_decay_optimization(modules) if g["params"]]
+    if fp16 or bf16:
+        scaler = None
+        device = groups[0]["params"][0].device
+        if loss_scale:
+            scaler = ConstantGradScaler(loss_scale, device=device)
+        elif fp16:
+            scaler = DynamicGradScaler(
+                initial_scale=initial_loss_scale,
+                min_scale=min_loss_scale,
+                growth_factor=2.0,
+                backoff_factor=0.5,
+                growth_interval=loss_scale_window,
+                hysteresis=hysteresis,
+                device=device,
+            )
+        return Float16OptimizerWithFloat16Params(
+            groups, lr, betas, eps, weight_decay, clip_grad, log_num_zeros_in_grad, params_have_main_grad, True, bf16, scaler
+        )
+    return FP32Optimizer(groups, lr, betas, eps, weight_decay, clip_grad, log_num_zeros_in_grad, params_have_main_grad)

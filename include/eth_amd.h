@@ -1,0 +1,166 @@
+/*
+ * eth_amd.h -- C-ABI of the MI355X (gfx950) implementation of one ETH
+ * pipeline stage's training step.
+ *
+ * Plain pointers, sizes and a hipStream_t (passed as void*); no framework
+ * types.  Every function returns ETH_OK (0) or an error code and, on error,
+ * leaves a message in eth_last_error() (thread-local).  All device pointers
+ * must point to memory of the current HIP device; all work is enqueued on
+ * `stream` and nothing here synchronizes the host or allocates device memory.
+ *
+ * Each declaration names the reference interface it replaces
+ * (paths relative to the YuMJie/ETH tree).
+ */
+#ifndef ETH_AMD_H
+#define ETH_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { ETH_OK = 0, ETH_ERR_INVALID = 1, ETH_ERR_HIP = 2 };
+enum { ETH_F32 = 0, ETH_F16 = 1, ETH_BF16 = 2 };
+
+/* Library identity and error reporting. */
+int eth_abi_version(void);
+const char* eth_last_error(void);
+
+/* Fill n floats with `value` (graph-safe replacement for hipMemsetAsync). */
+int eth_fill_f32(float* dst, int64_t n, float value, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Block-wise gradient synchronization, local half.
+ *
+ * A bucket payload is described by a device table of chunks.  Each chunk is a
+ * 2-D strided block of one main_grad tensor (rows x row_len elements, rows
+ * `src_stride` elements apart) that occupies payload[dst, dst+rows*row_len).
+ * The host splits every TensorSegmentSpec of a LocalFragmentBindingSpec into
+ * chunks of at most ETH_CHUNK_ELEMS elements, once, when the plan is bound.
+ * ---------------------------------------------------------------------- */
+#define ETH_CHUNK_ELEMS 16384
+
+typedef struct eth_chunk {
+  uint64_t src;        /* device address of the chunk's first source element */
+  int64_t dst;         /* element offset of the chunk inside the payload */
+  int64_t src_stride;  /* elements between successive rows of the source */
+  int32_t rows;        /* rows in the chunk (1 for a contiguous run) */
+  int32_t row_len;     /* contiguous elements per row */
+  float scale;         /* LocalFragmentBindingSpec.contribution_scale */
+  int32_t flags;       /* ETH_CHUNK_NORM: counts toward the optimizer L2 norm */
+} eth_chunk_t;
+
+#define ETH_CHUNK_NORM 1
+
+/* Pack: payload[dst + i] = src[i] * scale (the multiply is skipped when
+ * scale == 1, so the copy is bit-exact).
+ * Replaces GradientBucketExecutor._pack / _segment_view
+ * (eth/runtime/megatron/grad_sync/executor.py:173-226). */
+int eth_bucket_pack(const eth_chunk_t* chunks, int64_t n_chunks, void* payload,
+                    int dtype, void* stream);
+
+/* Unpack after the bucket's all-reduce:
+ *   v = payload[i] * normalization_scale       (skipped when == 1)
+ *   if (flags & ETH_UNPACK_WRITEBACK) payload[i] = v
+ *   g = v * inv_loss_scale                      (only with ETH_UNPACK_UNSCALE)
+ *   src[i] = g;  found_inf |= !isfinite(v);  partials[chunk] = sum g^2 over
+ *   ETH_CHUNK_NORM chunks (only with ETH_UNPACK_STATS).
+ * `partials` (one double per chunk, indexed from partial_base) and
+ * `found_inf` (one float, set to 1.0 on a non-finite value, never cleared
+ * here) are only touched with ETH_UNPACK_STATS.
+ * Replaces payload.mul_ + GradientBucketExecutor._unpack
+ * (executor.py:228-261) fused with
+ * torch._amp_foreach_non_finite_check_and_unscale_
+ * (optimizer/optimizer.py:436-461) and the per-tensor pow(2).sum() of
+ * CanonicalOptimizerSemantics.clip_grad_norm
+ * (grad_sync/optimizer_semantics.py:563-595). */
+#define ETH_UNPACK_WRITEBACK 1
+#define ETH_UNPACK_UNSCALE 2
+#define ETH_UNPACK_STATS 4
+int eth_bucket_unpack(const eth_chunk_t* chunks, int64_t n_chunks, void* payload,
+                      int dtype, float normalization_scale, float inv_loss_scale,
+                      int flags, float* found_inf, double* partials,
+                      int64_t partial_base, void* stream);
+
+/* Standalone unscale + inf/nan check + sum of squares over chunk-described
+ * fp32 gradients, in place (g *= inv_scale when ETH_UNPACK_UNSCALE).  Used
+ * when gradients did not pass through eth_bucket_unpack this step.
+ * Replaces torch._amp_foreach_non_finite_check_and_unscale_
+ * (optimizer/optimizer.py:452-453) + the canonical L2 statistic
+ * (grad_sync/optimizer_semantics.py:584-587). */
+int eth_grad_stats(const eth_chunk_t* chunks, int64_t n_chunks, float inv_loss_scale,
+                   int flags, float* found_inf, double* partials, int64_t partial_base,
+                   void* stream);
+
+/* Reduce `n` per-chunk partials into stats[0] = sum of squares (double) and
+ * stats[1] = L2 norm; stats[2] = clip coefficient max_norm/(norm+1e-6)
+ * (1.0 when max_norm <= 0).  Deterministic order.
+ * Replaces the all_reduce + sqrt + coefficient of
+ * grad_sync/optimizer_semantics.py:584-592. */
+int eth_grad_norm_finalize(const double* partials, int64_t n, double max_norm,
+                           double* stats, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Fused AdamW with fp32 master weights (decoupled weight decay), one launch
+ * over a tensor table.  Per element, in fp32, following torch.optim.AdamW
+ * (the reference's fallback for apex FusedAdam,
+ * eth/runtime/megatron/optimizer/__init__.py:28-34,66-72):
+ *   g  = grad * clip          (clip = stats[2] when stats != NULL and < 1)
+ *   p  = p * (1 - lr*wd)
+ *   m  = lerp(m, g, 1-beta1)
+ *   v  = v*beta2 + (1-beta2)*g*g
+ *   p += -(lr/bc1) * m / (sqrt(v)/sqrt(bc2) + eps)
+ *   model = cast(p)           (bf16/fp16 model copy when `model` != 0;
+ *                              Float16Optimizer._copy_main_params_to_model_params,
+ *                              optimizer/optimizer.py:475-479)
+ * The whole launch is a no-op when found_inf != NULL and *found_inf != 0
+ * (the skipped step of optimizer/optimizer.py:501-512).
+ * ---------------------------------------------------------------------- */
+typedef struct eth_adam_tensor {
+  uint64_t param;       /* fp32 master weights */
+  uint64_t grad;        /* fp32 gradient */
+  uint64_t exp_avg;     /* fp32 */
+  uint64_t exp_avg_sq;  /* fp32 */
+  uint64_t model;       /* bf16/fp16 model copy, or 0 */
+  int64_t numel;
+  double lr;
+  double weight_decay;
+} eth_adam_tensor_t;
+
+typedef struct eth_adam_chunk {
+  int32_t tensor;  /* index into the tensor table */
+  int32_t n;       /* elements in this chunk (<= ETH_CHUNK_ELEMS) */
+  int64_t start;   /* first element of the chunk inside the tensor */
+} eth_adam_chunk_t;
+
+int eth_adam_step(const eth_adam_tensor_t* tensors, const eth_adam_chunk_t* chunks,
+                  int64_t n_chunks, double beta1, double beta2, double eps,
+                  int64_t step, int model_dtype, const double* stats,
+                  const float* found_inf, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Dense GEMM on the matrix cores (bf16/fp16 in, fp32 accumulate):
+ *   C[m*ldc + n] (+)= alpha * sum_k A(m,k) * B(k,n)  (+ bias[n])
+ * A(m,k) = a_kcontig ? A[m*lda + k] : A[k*lda + m]
+ * B(k,n) = b_kcontig ? B[n*ldb + k] : B[k*ldb + n]
+ * c_dtype: ETH_BF16 / ETH_F16 (rounded store) or ETH_F32 (store, or add into
+ * C with ETH_GEMM_ACCUMULATE).  bias (in_dtype, length N) with ETH_GEMM_BIAS.
+ * Requires K % 8 == 0, lda/ldb % 8 == 0, 16-byte aligned A/B, and M % 8 == 0
+ * (N % 8 == 0) when A (B) is not K-contiguous.
+ * Replaces F.linear in ColumnParallelLinear/RowParallelLinear forward
+ * (eth/runtime/megatron/mpu/layers.py:357-370,452-470), their autograd
+ * backward products, and the main_grad.add_(grad) hook of
+ * model/distributed.py:116-123 (wgrad with ETH_GEMM_ACCUMULATE).
+ * ---------------------------------------------------------------------- */
+#define ETH_GEMM_ACCUMULATE 1
+#define ETH_GEMM_BIAS 2
+int eth_gemm(const void* A, int64_t lda, int a_kcontig, const void* B, int64_t ldb,
+             int b_kcontig, void* C, int64_t ldc, int c_dtype, const void* bias,
+             int64_t M, int64_t N, int64_t K, int in_dtype, int flags, float alpha,
+             void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* ETH_AMD_H */
