@@ -58,6 +58,18 @@ SIGNATURES = {
     "eth_grad_norm_finalize": [_P, _I64, _F64, _P, _P],
     "eth_adam_step": [_P, _P, _I64, _F64, _F64, _F64, _I64, _I32, _P, _P, _P],
     "eth_gemm": [_P, _I64, _I32, _P, _I64, _I32, _P, _I64, _I32, _P, _I64, _I64, _I64, _I32, _I32, _F32, _P],
+    "eth_ln_fwd": [_P, _P, _P, _P, _P, _P, _I64, _I64, _F32, _I32, _P],
+    "eth_ln_bwd": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I32, _I32, _P],
+    "eth_bias_gelu_fwd": [_P, _P, _P, _I64, _I64, _I32, _P],
+    "eth_bias_gelu_bwd": [_P, _P, _P, _P, _I64, _I64, _I32, _P],
+    "eth_bias_dropout_add_fwd": [_P, _P, _P, _P, _I64, _I64, _F32, ctypes.c_uint64, _I32, _P],
+    "eth_dropout_bwd": [_P, _P, _I64, _I64, _F32, ctypes.c_uint64, _I32, _P],
+    "eth_col_sum": [_P, _I64, _I64, _I64, _P, _P, _I32, _I32, _P],
+}
+# functions returning a value instead of a status
+VALUE_SIGNATURES = {
+    "eth_ln_bwd_workspace": ([_I64, _I64], _I64),
+    "eth_col_sum_workspace": ([_I64, _I64], _I64),
 }
 GEMM_ACCUMULATE, GEMM_BIAS = 1, 2
 
@@ -88,12 +100,20 @@ def load(path=None):
         fn = getattr(lib, name)
         fn.restype = ctypes.c_int
         fn.argtypes = argtypes
+    for name, (argtypes, restype) in VALUE_SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
     _lib = lib
     return lib
 
 
 def exported_symbols():
-    return ["eth_abi_version", "eth_last_error", *SIGNATURES]
+    return ["eth_abi_version", "eth_last_error", *SIGNATURES, *VALUE_SIGNATURES]
+
+
+def value(name, *args):
+    return getattr(load(), name)(*args)
 
 
 def call(name, *args):

@@ -1,0 +1,174 @@
+"""Tensor-level wrappers over the C-ABI (include/eth_amd.h).
+
+Each wrapper checks, on the host, that shapes, strides, dtypes and devices
+match what the kernel and its launch grid assume, then enqueues the kernel on
+the current stream.  There is no CPU fallback: CPU tensors raise.
+"""
+
+import torch
+
+from . import _native as nat
+
+_HALF = (torch.bfloat16, torch.float16)
+
+
+def _check_half(*ts):
+    dt = ts[0].dtype
+    if dt not in _HALF:
+        raise ValueError(f"expected bf16/fp16 tensors, got {dt}")
+    for t in ts:
+        if t.dtype != dt:
+            raise ValueError(f"dtype mismatch {t.dtype} vs {dt}")
+        if not t.is_cuda:
+            raise ValueError("eth_amd kernels run on the GPU only (no CPU fallback)")
+    return nat.dtype_code(dt)
+
+
+def _rows_cols(x):
+    if not x.is_contiguous():
+        raise ValueError("expected a contiguous tensor")
+    cols = x.shape[-1]
+    return x.numel() // cols if cols else 0, cols
+
+
+# --------------------------------------------------------------------- GEMM --
+def _matrix_layout(t):
+    """(ld, kcontig-ready) of a 2-D view: returns (ld, row_major) where
+    row_major means t[i, j] = base[i*ld + j]; column-major views (t.T of a
+    row-major matrix) give row_major False."""
+    if t.dim() != 2:
+        raise ValueError("expected a 2-D operand")
+    s0, s1 = t.stride()
+    if s1 == 1 and s0 >= t.shape[1]:
+        return s0, True
+    if s0 == 1 and s1 >= t.shape[0]:
+        return s1, False
+    raise ValueError(f"operand with strides {t.stride()} is neither row- nor column-major")
+
+
+def gemm(a, b, out=None, bias=None, accumulate=False, out_dtype=None, alpha=1.0):
+    """out (+)= alpha * a @ b (+ bias), a: [M, K], b: [K, N] (any row/column-
+    major 2-D views), out: [M, N] row-major.  fp32 `out` with accumulate=True
+    adds into it."""
+    code = _check_half(a, b)
+    M, K = a.shape
+    K2, N = b.shape
+    if K != K2:
+        raise ValueError(f"inner dimensions differ: {a.shape} @ {b.shape}")
+    lda, a_row = _matrix_layout(a)
+    ldb, b_row = _matrix_layout(b)
+    # A(m,k) K-contiguous <=> a row-major; B(k,n) K-contiguous <=> b column-major
+    a_kcontig = 1 if a_row else 0
+    b_kcontig = 0 if b_row else 1
+    if out is None:
+        out = torch.empty(M, N, dtype=out_dtype or a.dtype, device=a.device)
+    if out.dim() != 2 or out.shape != (M, N) or out.stride(1) != 1:
+        raise ValueError("out must be a row-major [M, N] matrix")
+    if accumulate and out.dtype != torch.float32:
+        raise ValueError("accumulate needs an fp32 output")
+    flags = 0
+    if accumulate:
+        flags |= nat.GEMM_ACCUMULATE
+    if bias is not None:
+        if bias.dtype != a.dtype or bias.numel() != N or not bias.is_contiguous():
+            raise ValueError("bias must be a contiguous [N] tensor of the input dtype")
+        flags |= nat.GEMM_BIAS
+    nat.call(
+        "eth_gemm",
+        nat.ptr(a), lda, a_kcontig,
+        nat.ptr(b), ldb, b_kcontig,
+        nat.ptr(out), out.stride(0), nat.dtype_code(out.dtype),
+        nat.ptr(bias), M, N, K, code, flags, float(alpha),
+        nat.stream_ptr(a.device),
+    )
+    return out
+
+
+def linear(x2d, weight, bias=None):
+    """F.linear: x2d [T, K] @ weight[N, K]^T (+ bias)."""
+    return gemm(x2d, weight.t(), bias=bias)
+
+
+# ---------------------------------------------------------------- LayerNorm --
+def layer_norm_fwd(x, gamma, beta, eps=1e-5):
+    code = _check_half(x, gamma, beta)
+    rows, cols = _rows_cols(x)
+    if gamma.numel() != cols or beta.numel() != cols:
+        raise ValueError("gamma/beta must match the normalized size")
+    y = torch.empty_like(x)
+    mean = torch.empty(rows, dtype=torch.float32, device=x.device)
+    rstd = torch.empty(rows, dtype=torch.float32, device=x.device)
+    nat.call("eth_ln_fwd", nat.ptr(x), nat.ptr(gamma), nat.ptr(beta), nat.ptr(y), nat.ptr(mean), nat.ptr(rstd),
+             rows, cols, float(eps), code, nat.stream_ptr(x.device))
+    return y, mean, rstd
+
+
+def layer_norm_bwd(dy, x, mean, rstd, gamma, dgamma, dbeta, accumulate):
+    """dx (returned); dgamma/dbeta fp32 stored or accumulated in place."""
+    code = _check_half(dy, x, gamma)
+    rows, cols = _rows_cols(x)
+    if dy.shape != x.shape or not dy.is_contiguous():
+        raise ValueError("dy must match x")
+    for t in (dgamma, dbeta):
+        if t.dtype != torch.float32 or t.numel() != cols or not t.is_contiguous():
+            raise ValueError("dgamma/dbeta must be contiguous fp32 [cols]")
+    ws = torch.empty(nat.value("eth_ln_bwd_workspace", rows, cols), dtype=torch.float32, device=x.device)
+    dx = torch.empty_like(x)
+    nat.call("eth_ln_bwd", nat.ptr(dy), nat.ptr(x), nat.ptr(mean), nat.ptr(rstd), nat.ptr(gamma), nat.ptr(dx),
+             nat.ptr(dgamma), nat.ptr(dbeta), nat.ptr(ws), rows, cols, 1 if accumulate else 0, code,
+             nat.stream_ptr(x.device))
+    return dx
+
+
+# -------------------------------------------------------------- elementwise --
+def bias_gelu_fwd(x, bias):
+    code = _check_half(x, bias)
+    rows, cols = _rows_cols(x)
+    if bias.numel() != cols:
+        raise ValueError("bias size mismatch")
+    y = torch.empty_like(x)
+    nat.call("eth_bias_gelu_fwd", nat.ptr(x), nat.ptr(bias), nat.ptr(y), rows, cols, code, nat.stream_ptr(x.device))
+    return y
+
+
+def bias_gelu_bwd(dy, x, bias):
+    code = _check_half(dy, x, bias)
+    rows, cols = _rows_cols(x)
+    if dy.shape != x.shape or not dy.is_contiguous() or bias.numel() != cols:
+        raise ValueError("shape mismatch")
+    dx = torch.empty_like(x)
+    nat.call("eth_bias_gelu_bwd", nat.ptr(dy), nat.ptr(x), nat.ptr(bias), nat.ptr(dx), rows, cols, code,
+             nat.stream_ptr(x.device))
+    return dx
+
+
+def bias_dropout_add_fwd(x, bias, residual, p=0.0, seed=0):
+    code = _check_half(x, bias, residual)
+    rows, cols = _rows_cols(x)
+    if residual.shape != x.shape or not residual.is_contiguous() or bias.numel() != cols:
+        raise ValueError("shape mismatch")
+    out = torch.empty_like(x)
+    nat.call("eth_bias_dropout_add_fwd", nat.ptr(x), nat.ptr(bias), nat.ptr(residual), nat.ptr(out), rows, cols,
+             float(p), int(seed) & (2**64 - 1), code, nat.stream_ptr(x.device))
+    return out
+
+
+def dropout_bwd(dy, p, seed):
+    code = _check_half(dy)
+    rows, cols = _rows_cols(dy)
+    dx = torch.empty_like(dy)
+    nat.call("eth_dropout_bwd", nat.ptr(dy), nat.ptr(dx), rows, cols, float(p), int(seed) & (2**64 - 1), code,
+             nat.stream_ptr(dy.device))
+    return dx
+
+
+def col_sum(x, out, accumulate):
+    """out[c] (+)= sum over rows of x[..., c] (fp32 out)."""
+    code = _check_half(x)
+    rows, cols = _rows_cols(x)
+    if out.dtype != torch.float32 or out.numel() != cols or not out.is_contiguous():
+        raise ValueError("out must be contiguous fp32 [cols]")
+    ws = torch.empty(nat.value("eth_col_sum_workspace", rows, cols), dtype=torch.float32, device=x.device)
+    nat.call("eth_col_sum", nat.ptr(x), cols, rows, cols, nat.ptr(out), nat.ptr(ws), 1 if accumulate else 0, code,
+             nat.stream_ptr(x.device))
+    return out

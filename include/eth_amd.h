@@ -160,6 +160,46 @@ int eth_gemm(const void* A, int64_t lda, int a_kcontig, const void* B, int64_t l
              int64_t M, int64_t N, int64_t K, int in_dtype, int flags, float alpha,
              void* stream);
 
+/* ------------------------------------------------------------------------
+ * LayerNorm (bf16/fp16 rows of `cols` elements, cols % 8 == 0, <= 8192).
+ * Forward writes y and fp32 mean / rstd per row; backward writes dx and
+ * stores (accumulate == 0) or adds (accumulate != 0) fp32 dgamma / dbeta,
+ * using `workspace` of eth_ln_bwd_workspace(rows, cols) floats.
+ * Replaces fused_mix_prec_layer_norm_cuda.forward_affine / backward_affine
+ * (eth/runtime/megatron/fused_kernels/layer_norm_cuda.cpp:121-201) as used
+ * by MixedFusedLayerNorm (model/fused_layer_norm.py:30-89).
+ * ---------------------------------------------------------------------- */
+int eth_ln_fwd(const void* x, const void* gamma, const void* beta, void* y, float* mean,
+               float* rstd, int64_t rows, int64_t cols, float eps, int dtype, void* stream);
+int64_t eth_ln_bwd_workspace(int64_t rows, int64_t cols);
+int eth_ln_bwd(const void* dy, const void* x, const float* mean, const float* rstd,
+               const void* gamma, void* dx, float* dgamma, float* dbeta, float* workspace,
+               int64_t rows, int64_t cols, int accumulate, int dtype, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Elementwise ops of the GPT block ([rows, cols] row-major, cols % 8 == 0).
+ * eth_bias_gelu_fwd/bwd: y = gelu_tanh(x + b), dx = dy * gelu_tanh'(x + b)
+ *   (ParallelMlpGeLUOp, eth/runtime/megatron/model/flex_ops.py:1882-1906,60-63).
+ * eth_bias_dropout_add_fwd: out = residual + dropout(x + b, p, seed); p == 0
+ *   is the identity (bias_dropout_add_fused_train, flex_ops.py:104-134).
+ * eth_dropout_bwd: dx = dy * keep / (1 - p) with the same (seed, index) mask.
+ * eth_col_sum: out[c] (+)= sum_r x[r*ld + c] in fp32 -- the bias gradients
+ *   of the linear / bias-dropout-add / bias-GELU ops; `workspace` holds
+ *   eth_col_sum_workspace(rows, cols) floats.
+ * ---------------------------------------------------------------------- */
+int eth_bias_gelu_fwd(const void* x, const void* bias, void* y, int64_t rows, int64_t cols,
+                      int dtype, void* stream);
+int eth_bias_gelu_bwd(const void* dy, const void* x, const void* bias, void* dx, int64_t rows,
+                      int64_t cols, int dtype, void* stream);
+int eth_bias_dropout_add_fwd(const void* x, const void* bias, const void* residual, void* out,
+                             int64_t rows, int64_t cols, float p, uint64_t seed, int dtype,
+                             void* stream);
+int eth_dropout_bwd(const void* dy, void* dx, int64_t rows, int64_t cols, float p,
+                    uint64_t seed, int dtype, void* stream);
+int64_t eth_col_sum_workspace(int64_t rows, int64_t cols);
+int eth_col_sum(const void* x, int64_t ld, int64_t rows, int64_t cols, float* out,
+                float* workspace, int accumulate, int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

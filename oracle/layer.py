@@ -1,0 +1,94 @@
+"""torch-CPU restatement of the GPT layer ops and one pipeline stage (test
+oracle).  Computes in fp32 (or fp64) from the same 16-bit inputs the GPU
+path sees.
+
+Follows eth/runtime/megatron/model/flex_ops.py:
+  * LayerNorm: MixedFusedLayerNorm, eps 1e-5 (model/fused_layer_norm.py:62-89)
+  * QKV: F.linear + bias, view [s, b, np, 3*hn], split q | k | v per head
+    (flex_ops.py:1069-1103, mpu/utils.py:33-52)
+  * attention: F.scaled_dot_product_attention(is_causal=True) on
+    [b, np, s, hn], output [s, b, np*hn] (flex_ops.py:66-96)
+  * proj / fc2: F.linear without bias (skip_bias_add), bias added in
+    bias-dropout-add: residual + dropout(x + b) (flex_ops.py:104-134)
+  * fc1 + GELU: F.gelu(x + b, approximate="tanh") (flex_ops.py:60-63,1897)
+  * LM head + cross entropy: logits = h @ E^T, loss = logsumexp - z[label]
+    (model/language_model.py:126-141, mpu/cross_entropy.py:36-92)
+"""
+
+import math
+
+import torch
+import torch.nn.functional as F
+
+
+def layer_norm(x, gamma, beta, eps=1e-5):
+    return F.layer_norm(x, (x.shape[-1],), gamma, beta, eps)
+
+
+def bias_gelu(x, bias):
+    return F.gelu(x + bias, approximate="tanh")
+
+
+def bias_dropout_add(x, bias, residual):
+    """p = 0 (the parity setting): residual + (x + bias)."""
+    return residual + (x + bias)
+
+
+def causal_attention(q, k, v):
+    """q, k, v: [s, b, np, hn] -> [s, b, np*hn] (SDPA semantics)."""
+    s, b, n, d = q.shape
+    out = F.scaled_dot_product_attention(
+        q.permute(1, 2, 0, 3), k.permute(1, 2, 0, 3), v.permute(1, 2, 0, 3), is_causal=True
+    )
+    return out.permute(2, 0, 1, 3).reshape(s, b, n * d)
+
+
+def causal_attention_explicit(q, k, v):
+    """Brute-force softmax(QK^T/sqrt(d) + causal -inf) V for tiny shapes."""
+    s, b, n, d = q.shape
+    qh, kh, vh = (t.permute(1, 2, 0, 3) for t in (q, k, v))
+    scores = qh @ kh.transpose(-1, -2) / math.sqrt(d)
+    mask = torch.triu(torch.ones(s, s, dtype=torch.bool), diagonal=1)
+    scores = scores.masked_fill(mask, float("-inf"))
+    out = torch.softmax(scores, dim=-1) @ vh
+    return out.permute(2, 0, 1, 3).reshape(s, b, n * d)
+
+
+def transformer_layer(x, p, heads):
+    """One ParallelTransformerLayer (10 ops) on x [s, b, h]; p holds the
+    layer's parameters (fp32 or fp64 CPU tensors)."""
+    s, b, h = x.shape
+    hn = h // heads
+    ln1 = layer_norm(x, p["ln1_w"], p["ln1_b"])
+    qkv = F.linear(ln1, p["qkv_w"], p["qkv_b"]).view(s, b, heads, 3 * hn)
+    q, k, v = torch.split(qkv, hn, dim=-1)
+    ctx = causal_attention(q, k, v)
+    proj = F.linear(ctx, p["proj_w"])
+    h1 = bias_dropout_add(proj, p["proj_b"], x)
+    ln2 = layer_norm(h1, p["ln2_w"], p["ln2_b"])
+    fc1 = F.linear(ln2, p["fc1_w"])
+    act = bias_gelu(fc1, p["fc1_b"])
+    fc2 = F.linear(act, p["fc2_w"])
+    return bias_dropout_add(fc2, p["fc2_b"], h1)
+
+
+LAYER_PARAM_NAMES = ("ln1_w", "ln1_b", "qkv_w", "qkv_b", "proj_w", "proj_b", "ln2_w", "ln2_b", "fc1_w", "fc1_b", "fc2_w", "fc2_b")
+
+
+def middle_stage_fwd_bwd(x, layers, heads, dy, dtype=torch.float32):
+    """Forward + backward of a middle pipeline stage: returns the output,
+    the input gradient and per-parameter gradients (lists of dicts)."""
+    x = x.to(dtype).detach().requires_grad_(True)
+    params = [{k: v.to(dtype).detach().requires_grad_(True) for k, v in p.items()} for p in layers]
+    h = x
+    for p in params:
+        h = transformer_layer(h, p, heads)
+    h.backward(dy.to(dtype))
+    return h.detach(), x.grad.detach(), [{k: v.grad.detach() for k, v in p.items()} for p in params]
+
+
+def vocab_cross_entropy(logits, labels):
+    """Per-token loss = logsumexp(z) - z[label] in fp32 (the fp32 cast of
+    flex_ops.py:1976-1981)."""
+    z = logits.float()
+    return torch.logsumexp(z, dim=-1) - z.gather(-1, labels.unsqueeze(-1)).squeeze(-1)

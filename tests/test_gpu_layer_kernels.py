@@ -1,0 +1,138 @@
+"""GPU parity of the layer kernels against the torch-CPU fp32 oracle on the
+same 16-bit inputs.  Tolerances: outputs are rounded to bf16/fp16, so the
+bar is a few units of the output dtype's rounding (2^-8 relative for bf16,
+2^-11 for fp16) on top of fp32 accumulation-order noise."""
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from eth_amd import kernels as K
+from oracle import layer as ol
+from tests.conftest import announce
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = [torch.bfloat16, torch.float16]
+
+
+def _tol(dtype):
+    return 2.0**-7 if dtype == torch.bfloat16 else 2.0**-10
+
+
+def _close(out, ref, dtype, what, scale=None):
+    out = out.float().cpu()
+    ref = ref.float().cpu()
+    scale = scale if scale is not None else ref.abs().max().item() + 1e-12
+    err = (out - ref).abs().max().item()
+    assert err <= _tol(dtype) * scale, f"{what}: max err {err:.3e} vs scale {scale:.3e}"
+
+
+def _rand(shape, dtype, gen, std=1.0):
+    return (torch.randn(shape, generator=gen) * std).to(dtype)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("M,N,Kd", [(256, 384, 128), (8, 16, 8), (200, 136, 72), (512, 512, 1024)])
+def test_gemm_three_layouts(cuda, dtype, M, N, Kd):
+    announce(f"gemm {dtype} {M}x{N}x{Kd}")
+    gen = torch.Generator().manual_seed(M * 7 + N)
+    x = _rand((M, Kd), dtype, gen)
+    w = _rand((N, Kd), dtype, gen, 0.05)
+    bias = _rand((N,), dtype, gen)
+    dy = _rand((M, N), dtype, gen)
+    xd, wd, bd, dyd = (t.to(cuda) for t in (x, w, bias, dy))
+    # forward (A K-contiguous, B K-contiguous) with bias
+    y = K.linear(xd, wd, bias=bd)
+    ref = x.float() @ w.float().t() + bias.float()
+    _close(y, ref, dtype, "fwd")
+    # dgrad (B N-contiguous)
+    dx = K.gemm(dyd, wd)
+    _close(dx, dy.float() @ w.float(), dtype, "dgrad")
+    # wgrad accumulate into fp32 (A M-contiguous, B N-contiguous)
+    acc = torch.full((N, Kd), 0.5, dtype=torch.float32, device=cuda)
+    K.gemm(dyd.t(), xd, out=acc, accumulate=True)
+    ref = 0.5 + dy.float().t() @ x.float()
+    err = (acc.cpu() - ref).abs().max().item()
+    assert err <= 1e-4 * ref.abs().max().item() + 1e-5, f"wgrad fp32 err {err}"
+    # M-contiguous A with K-contiguous B
+    z = K.gemm(xd.t().contiguous().t(), wd.t())
+    _close(z, x.float() @ w.float().t(), dtype, "A col-major")
+
+
+def test_gemm_rejects_bad_shapes(cuda):
+    a = torch.zeros(16, 12, dtype=torch.bfloat16, device=cuda)
+    b = torch.zeros(12, 16, dtype=torch.bfloat16, device=cuda)
+    with pytest.raises(ValueError):
+        K.gemm(a, b)  # K = 12 is not a multiple of 8
+    with pytest.raises(ValueError):
+        K.gemm(a.float(), b.float())
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("rows,cols", [(300, 256), (64, 2048), (33, 4096), (5, 8)])
+def test_layer_norm_fwd_bwd(cuda, dtype, rows, cols):
+    announce(f"layernorm {dtype} {rows}x{cols}")
+    gen = torch.Generator().manual_seed(rows + cols)
+    x = _rand((rows, cols), dtype, gen, 2.0) + 0.5
+    g = (1 + _rand((cols,), torch.float32, gen, 0.1)).to(dtype)
+    b = _rand((cols,), dtype, gen, 0.1)
+    dy = _rand((rows, cols), dtype, gen)
+    y, mean, rstd = K.layer_norm_fwd(x.to(cuda), g.to(cuda), b.to(cuda))
+    xr = x.float().requires_grad_(True)
+    gr = g.float().requires_grad_(True)
+    br = b.float().requires_grad_(True)
+    ref = ol.layer_norm(xr, gr, br)
+    _close(y, ref, dtype, "ln fwd")
+    assert torch.allclose(mean.cpu(), x.float().mean(-1), atol=1e-4, rtol=1e-4)
+    ref.backward(dy.float())
+    dg = torch.full((cols,), 1.0, device=cuda)
+    db = torch.zeros(cols, device=cuda)
+    dx = K.layer_norm_bwd(dy.to(cuda), x.to(cuda), mean, rstd, g.to(cuda), dg, db, accumulate=True)
+    _close(dx, xr.grad, dtype, "ln dx")
+    assert torch.allclose(dg.cpu() - 1.0, gr.grad, rtol=1e-3, atol=1e-3 * gr.grad.abs().max().item())
+    assert torch.allclose(db.cpu(), br.grad, rtol=1e-3, atol=1e-3 * br.grad.abs().max().item())
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_bias_gelu_fwd_bwd(cuda, dtype):
+    announce(f"bias-gelu {dtype}")
+    gen = torch.Generator().manual_seed(3)
+    x = _rand((96, 1024), dtype, gen, 2.0)
+    b = _rand((1024,), dtype, gen)
+    dy = _rand((96, 1024), dtype, gen)
+    y = K.bias_gelu_fwd(x.to(cuda), b.to(cuda))
+    # reference rounds x + b to the activation dtype first (separate torch add)
+    t = (x + b).float().requires_grad_(True)
+    ref = F.gelu(t, approximate="tanh")
+    _close(y, ref, dtype, "gelu fwd")
+    ref.backward(dy.float())
+    dx = K.bias_gelu_bwd(dy.to(cuda), x.to(cuda), b.to(cuda))
+    _close(dx, t.grad, dtype, "gelu bwd")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_bias_dropout_add_and_col_sum(cuda, dtype):
+    announce(f"bias-dropout-add {dtype}")
+    gen = torch.Generator().manual_seed(4)
+    x = _rand((130, 512), dtype, gen)
+    b = _rand((512,), dtype, gen)
+    r = _rand((130, 512), dtype, gen)
+    out = K.bias_dropout_add_fwd(x.to(cuda), b.to(cuda), r.to(cuda), p=0.0)
+    ref = (r + (x + b)).float()  # torch bf16 semantics: two rounded adds
+    assert torch.equal(out.cpu().float(), ref)
+    acc = torch.ones(512, device=cuda)
+    K.col_sum(x.to(cuda), acc, accumulate=True)
+    ref = 1.0 + x.float().sum(0)
+    assert torch.allclose(acc.cpu(), ref, rtol=1e-5, atol=1e-4)
+    # dropout p=0.25: kept fraction, scaling, and backward uses the same mask
+    outp = K.bias_dropout_add_fwd(x.to(cuda), b.to(cuda), torch.zeros_like(r).to(cuda), p=0.25, seed=123)
+    kept = (outp.cpu().float() != 0)
+    frac = kept.float().mean().item()
+    assert 0.70 < frac < 0.80
+    xb = (x + b).float()
+    assert torch.allclose(outp.cpu().float()[kept], (xb * (1 / 0.75)).to(dtype).float()[kept], rtol=1e-2, atol=1e-2)
+    dxp = K.dropout_bwd(torch.ones_like(x).to(cuda), 0.25, 123)
+    keep_bwd = dxp.cpu().float() != 0
+    assert torch.all(keep_bwd[kept])  # every element kept forward is kept backward
+    assert 0.70 < keep_bwd.float().mean().item() < 0.80
