@@ -66,6 +66,30 @@ SIGNATURES = {
     "eth_dropout_bwd": [_P, _P, _I64, _I64, _F32, ctypes.c_uint64, _I32, _P],
     "eth_col_sum": [_P, _I64, _I64, _I64, _P, _P, _I32, _I32, _P],
 }
+SIGNATURES["eth_attn_fwd"] = [_P, _P, _P, _P, _P, _P, _P]
+SIGNATURES["eth_attn_bwd"] = [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]
+
+
+class AttnDesc(ctypes.Structure):
+    """struct eth_attn_desc (include/eth_amd.h)."""
+
+    _fields_ = [
+        ("batch", ctypes.c_int32),
+        ("heads", ctypes.c_int32),
+        ("seq", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+        ("q_strides", ctypes.c_int64 * 3),
+        ("k_strides", ctypes.c_int64 * 3),
+        ("v_strides", ctypes.c_int64 * 3),
+        ("o_strides", ctypes.c_int64 * 3),
+        ("do_strides", ctypes.c_int64 * 3),
+        ("dq_strides", ctypes.c_int64 * 3),
+        ("dk_strides", ctypes.c_int64 * 3),
+        ("dv_strides", ctypes.c_int64 * 3),
+    ]
+
+
 # functions returning a value instead of a status
 VALUE_SIGNATURES = {
     "eth_ln_bwd_workspace": ([_I64, _I64], _I64),

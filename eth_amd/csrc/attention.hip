@@ -1,0 +1,626 @@
+// Causal flash attention for the GPT block, forward and backward, on CDNA4
+// matrix cores (v_mfma_f32_32x32x16_{bf16,f16}), head_dim 64 or 128.
+//
+// Semantics: O = softmax(Q K^T / sqrt(hn) + causal -inf) V per (batch, head),
+// i.e. F.scaled_dot_product_attention(q, k, v, is_causal=True) as called by
+// eth/runtime/megatron/model/flex_ops.py:66-96 (ParallelFlashAtten,
+// :1401-1426).  Q, K, V, O and their gradients are addressed in place through
+// (row, batch, head) strides, so the [s, b, np, 3*hn] output of the QKV GEMM
+// is read without the split/permute copies and dQ/dK/dV are written straight
+// into the [s, b, np, 3*hn] gradient the QKV backward consumes.
+//
+// Layout trick.  Scores are computed transposed, S^T = K Q^T, so that each
+// lane owns one query (MFMA column) and 32 of the 64 keys of a block sit in
+// its registers: row max / row sum need one cross-lane exchange (lane ^ 32),
+// and the per-query softmax statistics are per-lane scalars.  K rows are
+// stored in LDS with bits 2 and 3 of the row index swapped, which makes the
+// MFMA result layout of S^T equal to the operand layout of P^T in
+// O^T = V^T P^T, so P never leaves registers.  The dK/dV kernel uses the
+// mirror image (S = Q K^T, lane = key, query rows swizzled); dQ has its own
+// kernel (recomputing P), so no atomics are needed and results are
+// deterministic.  Softmax runs in fp32 base-2 (exp2) with the scale folded.
+#include "common.h"
+
+namespace eth {
+
+typedef __bf16 a_bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 a_f16x8 __attribute__((ext_vector_type(8)));
+typedef float a_f32x16 __attribute__((ext_vector_type(16)));
+
+template <bool FP16>
+__device__ __forceinline__ a_f32x16 mma(const uint4& a, const uint4& b, const a_f32x16& c) {
+  if constexpr (FP16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(a_f16x8, a), __builtin_bit_cast(a_f16x8, b),
+                                                  c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(a_bf16x8, a),
+                                                   __builtin_bit_cast(a_bf16x8, b), c, 0, 0, 0);
+}
+
+template <bool FP16>
+__device__ __forceinline__ float to_f(uint16_t v) {
+  return FP16 ? h2f_bits(v) : bf2f(v);
+}
+template <bool FP16>
+__device__ __forceinline__ uint16_t from_f(float v) {
+  return FP16 ? f2h_bits(v) : f2bf(v);
+}
+template <bool FP16>
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  return (uint32_t)from_f<FP16>(a) | ((uint32_t)from_f<FP16>(b) << 16);
+}
+// 8 fp32 -> one 16-byte MFMA operand
+template <bool FP16>
+__device__ __forceinline__ uint4 pack8(const float* v) {
+  return make_uint4(pack2<FP16>(v[0], v[1]), pack2<FP16>(v[2], v[3]), pack2<FP16>(v[4], v[5]),
+                    pack2<FP16>(v[6], v[7]));
+}
+
+__device__ __forceinline__ int swz(int r) {  // swap bits 2 and 3
+  return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1);
+}
+// index (within a 32-row MFMA tile) held by accumulator register r of a lane
+// in half h, when the operand rows were swizzled
+__device__ __forceinline__ int swz_row(int r, int h) { return (r < 8 ? 0 : 16) + h * 8 + (r & 7); }
+// natural accumulator row of register r for half h
+__device__ __forceinline__ int acc_row(int r, int h) { return (r >> 2) * 8 + h * 4 + (r & 3); }
+
+struct AttnTensor {
+  const uint16_t* p;
+  int64_t ss, sb, sh;  // strides of sequence, batch, head (elements); dim contiguous
+};
+struct AttnOut {
+  uint16_t* p;
+  int64_t ss, sb, sh;
+};
+
+struct AttnArgs {
+  AttnTensor q, k, v, o, dout;
+  AttnOut out, dq, dk, dv;
+  float* lse;    // [B*H, S] log2-domain: m2 + log2(l)
+  float* delta;  // [B*H, S] rowsum(dO * O)
+  int B, H, S;
+  float scale_log2;  // log2(e) / sqrt(hn)
+  float scale;       // 1 / sqrt(hn)
+};
+
+constexpr int kAttnThreads = 256;
+constexpr int kBQ = 128;   // forward / dQ: queries per workgroup (4 waves x 32)
+constexpr int kBKV = 64;   // forward / dQ: keys per step
+constexpr int kBKV2 = 128; // dK/dV: keys per workgroup (4 waves x 32)
+constexpr int kBQ2 = 64;   // dK/dV: queries per step
+
+__device__ __forceinline__ const uint16_t* row_ptr(const AttnTensor& t, int s, int b, int h) {
+  return t.p + (int64_t)s * t.ss + (int64_t)b * t.sb + (int64_t)h * t.sh;
+}
+__device__ __forceinline__ uint16_t* row_ptr(const AttnOut& t, int s, int b, int h) {
+  return t.p + (int64_t)s * t.ss + (int64_t)b * t.sb + (int64_t)h * t.sh;
+}
+
+// ROWS x D tile, rows r0.., into LDS [ROWS][D+8], row index optionally swizzled.
+template <int ROWS, int D>
+struct RowTile {
+  static constexpr int CPR = D / 8;
+  static constexpr int CPT = ROWS * CPR / kAttnThreads;
+  static_assert(ROWS * CPR % kAttnThreads == 0 && CPT >= 1, "tile split");
+  uint4 v[CPT];
+  __device__ __forceinline__ void load(const AttnTensor& t, int r0, int b, int h) {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int c = threadIdx.x + i * kAttnThreads;
+      v[i] = *reinterpret_cast<const uint4*>(row_ptr(t, r0 + c / CPR, b, h) + (c % CPR) * 8);
+    }
+  }
+  template <bool SWZ>
+  __device__ __forceinline__ void store(uint16_t* lds) const {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int c = threadIdx.x + i * kAttnThreads;
+      const int r = SWZ ? swz(c / CPR) : c / CPR;
+      *reinterpret_cast<uint4*>(lds + r * (D + 8) + (c % CPR) * 8) = v[i];
+    }
+  }
+};
+
+// ROWS x D tile stored transposed into LDS [D][ROWS+8] (natural row order).
+template <int ROWS, int D>
+struct ColTile {
+  static constexpr int DG = D / 8, RG = ROWS / 4;
+  static constexpr int NB = DG * RG;
+  static constexpr int BPT = (NB + kAttnThreads - 1) / kAttnThreads;
+  static_assert(NB % kAttnThreads == 0 || NB < kAttnThreads, "tile split");
+  uint4 v[BPT][4];
+  __device__ __forceinline__ void load(const AttnTensor& t, int r0, int b, int h) {
+#pragma unroll
+    for (int i = 0; i < BPT; ++i) {
+      const int blk = threadIdx.x + i * kAttnThreads;
+      if (blk >= NB) break;
+      const int dg = blk % DG, rg = blk / DG;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        v[i][j] = *reinterpret_cast<const uint4*>(row_ptr(t, r0 + rg * 4 + j, b, h) + dg * 8);
+    }
+  }
+  __device__ __forceinline__ void store(uint16_t* lds) const {
+#pragma unroll
+    for (int i = 0; i < BPT; ++i) {
+      const int blk = threadIdx.x + i * kAttnThreads;
+      if (blk >= NB) break;
+      const int dg = blk % DG, rg = blk / DG;
+      const uint32_t* w0 = reinterpret_cast<const uint32_t*>(&v[i][0]);
+      const uint32_t* w1 = reinterpret_cast<const uint32_t*>(&v[i][1]);
+      const uint32_t* w2 = reinterpret_cast<const uint32_t*>(&v[i][2]);
+      const uint32_t* w3 = reinterpret_cast<const uint32_t*>(&v[i][3]);
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        uint2 lo, hi;
+        lo.x = (w0[p] & 0xffffu) | (w1[p] << 16);
+        lo.y = (w2[p] & 0xffffu) | (w3[p] << 16);
+        hi.x = (w0[p] >> 16) | (w1[p] & 0xffff0000u);
+        hi.y = (w2[p] >> 16) | (w3[p] & 0xffff0000u);
+        uint16_t* row = lds + (dg * 8 + 2 * p) * (ROWS + 8) + rg * 4;
+        *reinterpret_cast<uint2*>(row) = lo;
+        *reinterpret_cast<uint2*>(row + (ROWS + 8)) = hi;
+      }
+    }
+  }
+};
+
+// ------------------------------------------------------------------ forward --
+template <int D, bool FP16>
+__global__ void __launch_bounds__(kAttnThreads) attn_fwd_kernel(AttnArgs a) {
+  constexpr int KS = D / 16;  // k-steps over the head dim
+  constexpr int DT = D / 32;  // 32-row tiles over the head dim
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][kBKV * (D + 8)];
+  __shared__ __attribute__((aligned(16))) uint16_t Vt[2][D * (kBKV + 8)];
+
+  const int BH = a.B * a.H, nqb = a.S / kBQ;
+  const int bh = blockIdx.x % BH, qb = nqb - 1 - blockIdx.x / BH;
+  const int b = bh / a.H, h = bh % a.H;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, hl = lane >> 5;
+  const int q0 = qb * kBQ + w * 32;
+  const int q = q0 + (lane & 31);
+
+  uint4 qf[KS];
+  {
+    const uint16_t* qp = row_ptr(a.q, q, b, h) + hl * 8;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) qf[ks] = *reinterpret_cast<const uint4*>(qp + ks * 16);
+  }
+  a_f32x16 o[DT];
+#pragma unroll
+  for (int t = 0; t < DT; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[t][r] = 0.f;
+  float m = -1e30f, l = 0.f;
+
+  const int nkv = (qb * kBQ + kBQ) / kBKV;  // blocks up to the diagonal
+  RowTile<kBKV, D> kt;
+  ColTile<kBKV, D> vt;
+  kt.load(a.k, 0, b, h);
+  vt.load(a.v, 0, b, h);
+  kt.template store<true>(Ks[0]);
+  vt.store(Vt[0]);
+  __syncthreads();
+
+  for (int j = 0; j < nkv; ++j) {
+    const int st = j & 1;
+    const bool more = j + 1 < nkv;
+    if (more) {
+      kt.load(a.k, (j + 1) * kBKV, b, h);
+      vt.load(a.v, (j + 1) * kBKV, b, h);
+    }
+    const int kv0 = j * kBKV;
+    if (kv0 <= q0 + 31) {  // wave has at least one unmasked key in the block
+      a_f32x16 s[2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[t][r] = 0.f;
+        const uint16_t* kp = Ks[st] + (t * 32 + (lane & 31)) * (D + 8) + hl * 8;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+          s[t] = mma<FP16>(*reinterpret_cast<const uint4*>(kp + ks * 16), qf[ks], s[t]);
+      }
+      const bool diag = kv0 + kBKV - 1 > q0;
+      float mx = -1e30f;
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          float v = s[t][r] * a.scale_log2;
+          if (diag && kv0 + t * 32 + swz_row(r, hl) > q) v = -1e30f;
+          s[t][r] = v;
+          mx = fmaxf(mx, v);
+        }
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float mnew = fmaxf(m, mx);
+      const float alpha = exp2f(m - mnew);
+      m = mnew;
+      float rs = 0.f;
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float p = exp2f(s[t][r] - m);
+          s[t][r] = p;
+          rs += p;
+        }
+      l = l * alpha + rs;
+#pragma unroll
+      for (int t = 0; t < DT; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[t][r] *= alpha;
+      // O^T += V^T P^T over the 64 keys (4 k-steps of 16)
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        float pv[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) pv[e] = s[kk >> 1][(kk & 1) * 8 + e];
+        const uint4 pb = pack8<FP16>(pv);
+        const uint16_t* vp = Vt[st] + (lane & 31) * (kBKV + 8) + kk * 16 + hl * 8;
+#pragma unroll
+        for (int t = 0; t < DT; ++t)
+          o[t] = mma<FP16>(*reinterpret_cast<const uint4*>(vp + t * 32 * (kBKV + 8)), pb, o[t]);
+      }
+    }
+    if (more) {
+      kt.template store<true>(Ks[st ^ 1]);
+      vt.store(Vt[st ^ 1]);
+    }
+    __syncthreads();
+  }
+  l += __shfl_xor(l, 32, 64);
+  const float inv = 1.0f / l;
+  uint16_t* op = row_ptr(a.out, q, b, h);
+#pragma unroll
+  for (int t = 0; t < DT; ++t)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      uint2 v;
+      v.x = pack2<FP16>(o[t][g * 4 + 0] * inv, o[t][g * 4 + 1] * inv);
+      v.y = pack2<FP16>(o[t][g * 4 + 2] * inv, o[t][g * 4 + 3] * inv);
+      *reinterpret_cast<uint2*>(op + t * 32 + g * 8 + hl * 4) = v;
+    }
+  if (hl == 0) a.lse[(int64_t)bh * a.S + q] = m + log2f(l);
+}
+
+// --------------------------------------------------------- backward: delta --
+template <int D, bool FP16>
+__global__ void __launch_bounds__(kAttnThreads) attn_bwd_delta_kernel(AttnArgs a) {
+  // one wavefront per (bh, query) row; lanes split the head dim
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= (int64_t)a.B * a.H * a.S) return;
+  const int bh = (int)(row / a.S), qi = (int)(row % a.S);
+  const int b = bh / a.H, h = bh % a.H;
+  float acc = 0.f;
+  if (lane < D / 8) {
+    uint4 x = *reinterpret_cast<const uint4*>(row_ptr(a.o, qi, b, h) + lane * 8);
+    uint4 y = *reinterpret_cast<const uint4*>(row_ptr(a.dout, qi, b, h) + lane * 8);
+    const uint16_t* xe = reinterpret_cast<const uint16_t*>(&x);
+    const uint16_t* ye = reinterpret_cast<const uint16_t*>(&y);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc += to_f<FP16>(xe[e]) * to_f<FP16>(ye[e]);
+  }
+  acc = wave_sum(acc);
+  if (lane == 0) a.delta[row] = acc;
+}
+
+// ------------------------------------------------------- backward: dK, dV --
+template <int D, bool FP16>
+__global__ void __launch_bounds__(kAttnThreads) attn_bwd_dkdv_kernel(AttnArgs a) {
+  constexpr int KS = D / 16, DT = D / 32;
+  __shared__ __attribute__((aligned(16))) uint16_t Qs[kBQ2 * (D + 8)];
+  __shared__ __attribute__((aligned(16))) uint16_t dOs[kBQ2 * (D + 8)];
+  __shared__ __attribute__((aligned(16))) uint16_t Qt[D * (kBQ2 + 8)];
+  __shared__ __attribute__((aligned(16))) uint16_t dOt[D * (kBQ2 + 8)];
+  __shared__ float lse_s[kBQ2], del_s[kBQ2];
+
+  const int BH = a.B * a.H;
+  const int bh = blockIdx.x % BH, kb = blockIdx.x / BH;
+  const int b = bh / a.H, h = bh % a.H;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, hl = lane >> 5;
+  const int k0 = kb * kBKV2 + w * 32;
+  const int key = k0 + (lane & 31);
+
+  uint4 kf[KS], vf[KS];
+  {
+    const uint16_t* kp = row_ptr(a.k, key, b, h) + hl * 8;
+    const uint16_t* vp = row_ptr(a.v, key, b, h) + hl * 8;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      kf[ks] = *reinterpret_cast<const uint4*>(kp + ks * 16);
+      vf[ks] = *reinterpret_cast<const uint4*>(vp + ks * 16);
+    }
+  }
+  a_f32x16 dk[DT], dv[DT];
+#pragma unroll
+  for (int t = 0; t < DT; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dk[t][r] = dv[t][r] = 0.f;
+
+  RowTile<kBQ2, D> qrow, drow;
+  ColTile<kBQ2, D> qcol, dcol;
+  const int first = (kb * kBKV2) / kBQ2, nq = a.S / kBQ2;
+  for (int qb = first; qb < nq; ++qb) {
+    const int qs0 = qb * kBQ2;
+    qrow.load(a.q, qs0, b, h);
+    drow.load(a.dout, qs0, b, h);
+    qcol.load(a.q, qs0, b, h);
+    dcol.load(a.dout, qs0, b, h);
+    __syncthreads();  // previous step's LDS readers are done
+    qrow.template store<true>(Qs);
+    drow.template store<true>(dOs);
+    qcol.store(Qt);
+    dcol.store(dOt);
+    if (threadIdx.x < kBQ2) {
+      lse_s[threadIdx.x] = a.lse[(int64_t)bh * a.S + qs0 + threadIdx.x];
+      del_s[threadIdx.x] = a.delta[(int64_t)bh * a.S + qs0 + threadIdx.x];
+    }
+    __syncthreads();
+    if (qs0 + kBQ2 - 1 < k0) continue;  // every query of the step precedes this wave's keys
+    const bool diag = qs0 < k0 + 31;
+    // S = Q K^T and dP = dO V^T: 2 query tiles of 32, lane = key
+    a_f32x16 s[2], dp[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[t][r] = dp[t][r] = 0.f;
+      const uint16_t* qp = Qs + (t * 32 + (lane & 31)) * (D + 8) + hl * 8;
+      const uint16_t* op = dOs + (t * 32 + (lane & 31)) * (D + 8) + hl * 8;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        s[t] = mma<FP16>(*reinterpret_cast<const uint4*>(qp + ks * 16), kf[ks], s[t]);
+        dp[t] = mma<FP16>(*reinterpret_cast<const uint4*>(op + ks * 16), vf[ks], dp[t]);
+      }
+    }
+    // P and dS (fp32), query index of register r = t*32 + swz_row(r, hl)
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int qi = t * 32 + swz_row(r, hl);
+        float p = exp2f(s[t][r] * a.scale_log2 - lse_s[qi]);
+        if (diag && key > qs0 + qi) p = 0.f;
+        s[t][r] = p;
+        dp[t][r] = p * (dp[t][r] - del_s[qi]);
+      }
+    // dV += P^T dO, dK += dS^T Q: k-steps over 16 queries
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      float pv[8], sv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        pv[e] = s[kk >> 1][(kk & 1) * 8 + e];
+        sv[e] = dp[kk >> 1][(kk & 1) * 8 + e];
+      }
+      const uint4 pa = pack8<FP16>(pv), sa = pack8<FP16>(sv);
+      const uint16_t* dop = dOt + (lane & 31) * (kBQ2 + 8) + kk * 16 + hl * 8;
+      const uint16_t* qtp = Qt + (lane & 31) * (kBQ2 + 8) + kk * 16 + hl * 8;
+#pragma unroll
+      for (int t = 0; t < DT; ++t) {
+        dv[t] = mma<FP16>(pa, *reinterpret_cast<const uint4*>(dop + t * 32 * (kBQ2 + 8)), dv[t]);
+        dk[t] = mma<FP16>(sa, *reinterpret_cast<const uint4*>(qtp + t * 32 * (kBQ2 + 8)), dk[t]);
+      }
+    }
+  }
+  // lane holds d = t*32 + lane%32 for keys k0 + acc_row(r, hl)
+#pragma unroll
+  for (int t = 0; t < DT; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int kr = k0 + acc_row(r, hl);
+      const int d = t * 32 + (lane & 31);
+      row_ptr(a.dk, kr, b, h)[d] = from_f<FP16>(dk[t][r] * a.scale);
+      row_ptr(a.dv, kr, b, h)[d] = from_f<FP16>(dv[t][r]);
+    }
+}
+
+// ------------------------------------------------------------ backward: dQ --
+template <int D, bool FP16>
+__global__ void __launch_bounds__(kAttnThreads) attn_bwd_dq_kernel(AttnArgs a) {
+  constexpr int KS = D / 16, DT = D / 32;
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[kBKV * (D + 8)];
+  __shared__ __attribute__((aligned(16))) uint16_t Vs[kBKV * (D + 8)];
+  __shared__ __attribute__((aligned(16))) uint16_t Kt[D * (kBKV + 8)];
+
+  const int BH = a.B * a.H, nqb = a.S / kBQ;
+  const int bh = blockIdx.x % BH, qb = nqb - 1 - blockIdx.x / BH;
+  const int b = bh / a.H, h = bh % a.H;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, hl = lane >> 5;
+  const int q0 = qb * kBQ + w * 32;
+  const int q = q0 + (lane & 31);
+
+  uint4 qf[KS], of[KS];
+  {
+    const uint16_t* qp = row_ptr(a.q, q, b, h) + hl * 8;
+    const uint16_t* op = row_ptr(a.dout, q, b, h) + hl * 8;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      qf[ks] = *reinterpret_cast<const uint4*>(qp + ks * 16);
+      of[ks] = *reinterpret_cast<const uint4*>(op + ks * 16);
+    }
+  }
+  const float lse = a.lse[(int64_t)bh * a.S + q];
+  const float del = a.delta[(int64_t)bh * a.S + q];
+  a_f32x16 dq[DT];
+#pragma unroll
+  for (int t = 0; t < DT; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dq[t][r] = 0.f;
+
+  RowTile<kBKV, D> krow, vrow;
+  ColTile<kBKV, D> kcol;
+  const int nkv = (qb * kBQ + kBQ) / kBKV;
+  for (int j = 0; j < nkv; ++j) {
+    const int kv0 = j * kBKV;
+    krow.load(a.k, kv0, b, h);
+    vrow.load(a.v, kv0, b, h);
+    kcol.load(a.k, kv0, b, h);
+    __syncthreads();
+    krow.template store<true>(Ks);
+    vrow.template store<true>(Vs);
+    kcol.store(Kt);
+    __syncthreads();
+    if (kv0 > q0 + 31) continue;
+    const bool diag = kv0 + kBKV - 1 > q0;
+    a_f32x16 s[2], dp[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[t][r] = dp[t][r] = 0.f;
+      const uint16_t* kp = Ks + (t * 32 + (lane & 31)) * (D + 8) + hl * 8;
+      const uint16_t* vp = Vs + (t * 32 + (lane & 31)) * (D + 8) + hl * 8;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        s[t] = mma<FP16>(*reinterpret_cast<const uint4*>(kp + ks * 16), qf[ks], s[t]);
+        dp[t] = mma<FP16>(*reinterpret_cast<const uint4*>(vp + ks * 16), of[ks], dp[t]);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float p = exp2f(s[t][r] * a.scale_log2 - lse);
+        if (diag && kv0 + t * 32 + swz_row(r, hl) > q) p = 0.f;
+        dp[t][r] = p * (dp[t][r] - del);
+      }
+    // dQ^T += K^T dS^T
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      float sv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sv[e] = dp[kk >> 1][(kk & 1) * 8 + e];
+      const uint4 sb = pack8<FP16>(sv);
+      const uint16_t* kp = Kt + (lane & 31) * (kBKV + 8) + kk * 16 + hl * 8;
+#pragma unroll
+      for (int t = 0; t < DT; ++t)
+        dq[t] = mma<FP16>(*reinterpret_cast<const uint4*>(kp + t * 32 * (kBKV + 8)), sb, dq[t]);
+    }
+  }
+  uint16_t* dqp = row_ptr(a.dq, q, b, h);
+#pragma unroll
+  for (int t = 0; t < DT; ++t)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      uint2 v;
+      v.x = pack2<FP16>(dq[t][g * 4 + 0] * a.scale, dq[t][g * 4 + 1] * a.scale);
+      v.y = pack2<FP16>(dq[t][g * 4 + 2] * a.scale, dq[t][g * 4 + 3] * a.scale);
+      *reinterpret_cast<uint2*>(dqp + t * 32 + g * 8 + hl * 4) = v;
+    }
+}
+
+}  // namespace eth
+
+using namespace eth;
+
+static int attn_check(const eth_attn_desc_t* d) {
+  ETH_CHECK_ARG(d, "attention: null descriptor");
+  ETH_CHECK_ARG(d->dtype == ETH_BF16 || d->dtype == ETH_F16, "attention: dtype must be bf16/fp16");
+  ETH_CHECK_ARG(d->head_dim == 64 || d->head_dim == 128, "attention: head_dim must be 64 or 128 (got %d)",
+                d->head_dim);
+  ETH_CHECK_ARG(d->seq > 0 && d->seq % 128 == 0, "attention: seq must be a positive multiple of 128 (got %d)",
+                d->seq);
+  ETH_CHECK_ARG(d->batch > 0 && d->heads > 0, "attention: bad batch/heads");
+  return ETH_OK;
+}
+
+static AttnTensor tin(const void* p, const int64_t* st) {
+  AttnTensor t;
+  t.p = (const uint16_t*)p;
+  t.ss = st[0];
+  t.sb = st[1];
+  t.sh = st[2];
+  return t;
+}
+static AttnOut tout(void* p, const int64_t* st) {
+  AttnOut t;
+  t.p = (uint16_t*)p;
+  t.ss = st[0];
+  t.sb = st[1];
+  t.sh = st[2];
+  return t;
+}
+
+static bool aligned_rows(const void* p, const int64_t* st) {
+  return ((uintptr_t)p & 15) == 0 && st[0] % 8 == 0 && st[1] % 8 == 0 && st[2] % 8 == 0;
+}
+
+extern "C" int eth_attn_fwd(const eth_attn_desc_t* d, const void* q, const void* k, const void* v,
+                            void* out, float* lse, void* stream) {
+  if (int rc = attn_check(d)) return rc;
+  ETH_CHECK_ARG(q && k && v && out && lse, "eth_attn_fwd: null pointer");
+  ETH_CHECK_ARG(aligned_rows(q, d->q_strides) && aligned_rows(k, d->k_strides) && aligned_rows(v, d->v_strides) &&
+                    aligned_rows(out, d->o_strides),
+                "eth_attn_fwd: rows must be 16-byte aligned");
+  AttnArgs a{};
+  a.q = tin(q, d->q_strides);
+  a.k = tin(k, d->k_strides);
+  a.v = tin(v, d->v_strides);
+  a.out = tout(out, d->o_strides);
+  a.lse = lse;
+  a.B = d->batch;
+  a.H = d->heads;
+  a.S = d->seq;
+  a.scale = 1.0f / sqrtf((float)d->head_dim);
+  a.scale_log2 = a.scale * 1.4426950408889634f;
+  const int grid = a.B * a.H * (a.S / kBQ);
+  hipStream_t s = (hipStream_t)stream;
+  const bool fp16 = d->dtype == ETH_F16;
+  if (d->head_dim == 128) {
+    if (fp16) attn_fwd_kernel<128, true><<<grid, kAttnThreads, 0, s>>>(a);
+    else attn_fwd_kernel<128, false><<<grid, kAttnThreads, 0, s>>>(a);
+  } else {
+    if (fp16) attn_fwd_kernel<64, true><<<grid, kAttnThreads, 0, s>>>(a);
+    else attn_fwd_kernel<64, false><<<grid, kAttnThreads, 0, s>>>(a);
+  }
+  ETH_CHECK_LAUNCH("eth_attn_fwd");
+  return ETH_OK;
+}
+
+extern "C" int eth_attn_bwd(const eth_attn_desc_t* d, const void* q, const void* k, const void* v,
+                            const void* out, const void* dout, const float* lse, float* delta, void* dq,
+                            void* dk, void* dv, void* stream) {
+  if (int rc = attn_check(d)) return rc;
+  ETH_CHECK_ARG(q && k && v && out && dout && lse && delta && dq && dk && dv, "eth_attn_bwd: null pointer");
+  ETH_CHECK_ARG(aligned_rows(q, d->q_strides) && aligned_rows(k, d->k_strides) && aligned_rows(v, d->v_strides) &&
+                    aligned_rows(out, d->o_strides) && aligned_rows(dout, d->do_strides) &&
+                    aligned_rows(dq, d->dq_strides) && aligned_rows(dk, d->dk_strides) &&
+                    aligned_rows(dv, d->dv_strides),
+                "eth_attn_bwd: rows must be 16-byte aligned");
+  AttnArgs a{};
+  a.q = tin(q, d->q_strides);
+  a.k = tin(k, d->k_strides);
+  a.v = tin(v, d->v_strides);
+  a.o = tin(out, d->o_strides);
+  a.dout = tin(dout, d->do_strides);
+  a.dq = tout(dq, d->dq_strides);
+  a.dk = tout(dk, d->dk_strides);
+  a.dv = tout(dv, d->dv_strides);
+  a.lse = (float*)lse;
+  a.delta = delta;
+  a.B = d->batch;
+  a.H = d->heads;
+  a.S = d->seq;
+  a.scale = 1.0f / sqrtf((float)d->head_dim);
+  a.scale_log2 = a.scale * 1.4426950408889634f;
+  hipStream_t s = (hipStream_t)stream;
+  const bool fp16 = d->dtype == ETH_F16;
+  const int rows = a.B * a.H * a.S;
+  const int g_delta = (rows + 3) / 4;
+  const int g_kv = a.B * a.H * (a.S / kBKV2);
+  const int g_q = a.B * a.H * (a.S / kBQ);
+#define ETH_ATTN_BWD(D, F)                                                       \
+  attn_bwd_delta_kernel<D, F><<<g_delta, kAttnThreads, 0, s>>>(a);              \
+  attn_bwd_dkdv_kernel<D, F><<<g_kv, kAttnThreads, 0, s>>>(a);                  \
+  attn_bwd_dq_kernel<D, F><<<g_q, kAttnThreads, 0, s>>>(a);
+  if (d->head_dim == 128) {
+    if (fp16) { ETH_ATTN_BWD(128, true) } else { ETH_ATTN_BWD(128, false) }
+  } else {
+    if (fp16) { ETH_ATTN_BWD(64, true) } else { ETH_ATTN_BWD(64, false) }
+  }
+#undef ETH_ATTN_BWD
+  ETH_CHECK_LAUNCH("eth_attn_bwd");
+  return ETH_OK;
+}

@@ -5,6 +5,8 @@ match what the kernel and its launch grid assume, then enqueues the kernel on
 the current stream.  There is no CPU fallback: CPU tensors raise.
 """
 
+import ctypes
+
 import torch
 
 from . import _native as nat
@@ -172,3 +174,62 @@ def col_sum(x, out, accumulate):
     nat.call("eth_col_sum", nat.ptr(x), cols, rows, cols, nat.ptr(out), nat.ptr(ws), 1 if accumulate else 0, code,
              nat.stream_ptr(x.device))
     return out
+
+
+# ---------------------------------------------------------------- attention --
+def _sbhd_strides(t):
+    """(seq, batch, head) strides of a [s, b, np, hn] view with hn contiguous."""
+    if t.dim() != 4 or t.stride(3) != 1:
+        raise ValueError("attention operands must be [s, b, np, hn] views with hn contiguous")
+    return (t.stride(0), t.stride(1), t.stride(2))
+
+
+def _attn_desc(q, dtype_code):
+    s, b, n, d = q.shape
+    desc = nat.AttnDesc()
+    desc.batch, desc.heads, desc.seq, desc.head_dim, desc.dtype = b, n, s, d, dtype_code
+    return desc
+
+
+def attention_fwd(q, k, v, out=None):
+    """Causal attention on [s, b, np, hn] views (any seq/batch/head strides).
+    Returns (out [s, b, np, hn] view of a contiguous [s, b, np*hn], lse)."""
+    code = _check_half(q, k, v)
+    if not (q.shape == k.shape == v.shape):
+        raise ValueError("q, k, v shapes differ")
+    s, b, n, d = q.shape
+    if d not in (64, 128) or s % 128:
+        raise ValueError("attention needs head_dim 64/128 and seq % 128 == 0")
+    if out is None:
+        out = torch.empty(s, b, n * d, dtype=q.dtype, device=q.device)
+    o4 = out.view(s, b, n, d)
+    lse = torch.empty(b * n, s, dtype=torch.float32, device=q.device)
+    desc = _attn_desc(q, code)
+    desc.q_strides[:] = _sbhd_strides(q)
+    desc.k_strides[:] = _sbhd_strides(k)
+    desc.v_strides[:] = _sbhd_strides(v)
+    desc.o_strides[:] = _sbhd_strides(o4)
+    nat.call("eth_attn_fwd", ctypes.byref(desc), nat.ptr(q), nat.ptr(k), nat.ptr(v), nat.ptr(o4), nat.ptr(lse),
+             nat.stream_ptr(q.device))
+    return out, lse
+
+
+def attention_bwd(q, k, v, out, dout, lse, dq, dk, dv):
+    """Gradients of causal attention into dq/dk/dv ([s, b, np, hn] views, e.g.
+    of one [s, b, np, 3*hn] buffer).  out/dout are [s, b, np*hn]."""
+    code = _check_half(q, k, v, out, dout, dq, dk, dv)
+    s, b, n, d = q.shape
+    o4 = out.view(s, b, n, d)
+    do4 = dout.reshape(s, b, n, d) if dout.is_contiguous() else None
+    if do4 is None:
+        raise ValueError("dout must be contiguous [s, b, np*hn]")
+    if lse.shape != (b * n, s):
+        raise ValueError("lse shape mismatch")
+    delta = torch.empty(b * n, s, dtype=torch.float32, device=q.device)
+    desc = _attn_desc(q, code)
+    for name, t in (("q", q), ("k", k), ("v", v), ("o", o4), ("do", do4), ("dq", dq), ("dk", dk), ("dv", dv)):
+        if t.shape != q.shape:
+            raise ValueError(f"{name} shape mismatch")
+        getattr(desc, f"{name}_strides")[:] = _sbhd_strides(t)
+    nat.call("eth_attn_bwd", ctypes.byref(desc), nat.ptr(q), nat.ptr(k), nat.ptr(v), nat.ptr(o4), nat.ptr(do4),
+             nat.ptr(lse), nat.ptr(delta), nat.ptr(dq), nat.ptr(dk), nat.ptr(dv), nat.stream_ptr(q.device))

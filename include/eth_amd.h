@@ -200,6 +200,30 @@ int64_t eth_col_sum_workspace(int64_t rows, int64_t cols);
 int eth_col_sum(const void* x, int64_t ld, int64_t rows, int64_t cols, float* out,
                 float* workspace, int accumulate, int dtype, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Causal attention (softmax(Q K^T / sqrt(hn) + causal -inf) V per batch and
+ * head), flash-style, head_dim 64 or 128, seq % 128 == 0.  Every tensor is
+ * addressed as base + s*stride[0] + b*stride[1] + h*stride[2] + d with d
+ * contiguous and rows 16-byte aligned, so q/k/v may be views into the
+ * [s, b, np, 3*hn] QKV output and dq/dk/dv into its gradient.
+ * lse ([batch*heads, seq] fp32) is written by the forward and read by the
+ * backward; delta ([batch*heads, seq] fp32) is backward scratch.
+ * Replaces ParallelFlashAtten / F.scaled_dot_product_attention(is_causal=True)
+ * (eth/runtime/megatron/model/flex_ops.py:66-96,1401-1426) and its autograd
+ * backward.
+ * ---------------------------------------------------------------------- */
+typedef struct eth_attn_desc {
+  int32_t batch, heads, seq, head_dim, dtype;
+  int64_t q_strides[3], k_strides[3], v_strides[3], o_strides[3];
+  int64_t do_strides[3], dq_strides[3], dk_strides[3], dv_strides[3];
+} eth_attn_desc_t;
+
+int eth_attn_fwd(const eth_attn_desc_t* desc, const void* q, const void* k, const void* v,
+                 void* out, float* lse, void* stream);
+int eth_attn_bwd(const eth_attn_desc_t* desc, const void* q, const void* k, const void* v,
+                 const void* out, const void* dout, const float* lse, float* delta, void* dq,
+                 void* dk, void* dv, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
