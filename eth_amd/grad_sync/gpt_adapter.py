@@ -1,0 +1,161 @@
+"""GPT runtime ops -> canonical gradient descriptors (host, init time).
+
+The parameter schema is the one of
+eth/runtime/megatron/grad_sync/gpt_adapter.py:31-91 (op name -> parameter
+path, logical id, shared-weight id, root flag, required, TP semantics), and
+`semantic_order_key = (op_index, parameter_order, logical_id)` as at
+:168-300.  This build runs one rank (TP = DP = CP = 1, stage ranks (0,)),
+which fixes every topology field of the descriptor.
+"""
+
+from .metadata import LocalGradientBinding, SerializableGradientDescriptor
+
+PARAMETERLESS_OPS = {
+    "enc-attention-score",
+    "enc-attention-softmax",
+    "enc-attention-dropout",
+    "enc-attention-context",
+    "enc-flash-attention",
+    "enc-post-attention-dropout",
+    "enc-MLP-gelu",
+    "enc-post-MLP-dropout",
+}
+
+
+def _linear_semantics(op):
+    algo = getattr(op, "algo", None)
+    if algo == "column":
+        return "sharded_dim0", "sharded_dim0"
+    if algo == "row":
+        return "sharded_dim1", "replicated"
+    raise ValueError(f"runtime op {getattr(op, 'op_index', None)} has unsupported linear algo {algo!r}")
+
+
+def parameter_schema(op, layer_index):
+    name = op.name
+    pre = f"gpt.layers.{layer_index}"
+    if name == "encoder-embedding":
+        return (
+            ("word_embeddings.weight", "gpt.word_embeddings.weight", "gpt.word_embeddings", True, True, "sharded_dim0"),
+            ("position_embeddings.weight", "gpt.position_embeddings.weight", None, False, True, "replicated"),
+            ("tokentype_embeddings.weight", "gpt.tokentype_embeddings.weight", None, False, False, "replicated"),
+        )
+    if name in ("enc-1st-layernorm", "enc-2nd-layernorm", "final-layernorm"):
+        comp = {
+            "enc-1st-layernorm": f"{pre}.attention.input_layernorm",
+            "enc-2nd-layernorm": f"{pre}.mlp.input_layernorm",
+            "final-layernorm": "gpt.final_layernorm",
+        }[name]
+        return (
+            ("input_layernorm.weight", f"{comp}.weight", None, False, True, "replicated"),
+            ("input_layernorm.bias", f"{comp}.bias", None, False, True, "replicated"),
+        )
+    if name == "enc-attention-qkv":
+        w, b = "sharded_dim0", "sharded_dim0"
+        comp = f"{pre}.attention.query_key_value"
+        return (
+            ("query_key_value.weight", f"{comp}.weight", None, False, True, w),
+            ("query_key_value.bias", f"{comp}.bias", None, False, True, b),
+        )
+    if name in ("enc-attention-dense", "enc-MLP-GEMM-1", "enc-MLP-GEMM-2"):
+        w, b = _linear_semantics(op)
+        comp = {
+            "enc-attention-dense": f"{pre}.attention.dense",
+            "enc-MLP-GEMM-1": f"{pre}.mlp.dense_h_to_4h",
+            "enc-MLP-GEMM-2": f"{pre}.mlp.dense_4h_to_h",
+        }[name]
+        return (
+            ("dense.weight", f"{comp}.weight", None, False, True, w),
+            ("dense.bias", f"{comp}.bias", None, False, True, b),
+        )
+    if name == "gpt-post-process":
+        return (
+            ("word_embeddings.weight", "gpt.output_head.word_embeddings.weight", "gpt.word_embeddings", False, True, "sharded_dim0"),
+        )
+    if name in PARAMETERLESS_OPS:
+        return ()
+    raise ValueError(f"unsupported GPT manifest op {name!r}")
+
+
+def _resolve(root, path):
+    value = root
+    for part in path.split("."):
+        if value is None or not hasattr(value, part):
+            return None
+        value = getattr(value, part)
+    return value
+
+
+def collect_stage_metadata(ops, stage_op_begin, stage_op_end, model_impl="gpt", manifest_hash="manifest"):
+    """Descriptors and main_grad bindings of every trainable parameter of the
+    stage's ops (single rank)."""
+    descriptors, bindings = [], []
+    for op in ops:
+        layer = (op.op_index - 1) // 10 if op.name.startswith("enc-") else None
+        seen = set()
+        for order, (path, lid, shared_id, shared_root, required, semantics) in enumerate(parameter_schema(op, layer)):
+            p = _resolve(op, path)
+            if p is None:
+                if required:
+                    raise ValueError(f"logical_param_id {lid} rank 0 is missing {path}")
+                continue
+            if id(p) in seen:
+                raise ValueError(f"duplicate parameter for logical_param_id {lid} rank 0")
+            seen.add(id(p))
+            if not p.requires_grad:
+                continue
+            mg = getattr(p, "main_grad", None)
+            if mg is None:
+                raise ValueError(f"logical_param_id {lid} rank 0 is missing main_grad")
+            tp = bool(p.tensor_model_parallel)
+            pdim = int(p.partition_dim)
+            if tp and pdim < 0:
+                pdim += p.dim()
+            actual = f"sharded_dim{pdim}" if tp else "replicated"
+            if actual != semantics:
+                raise ValueError(f"logical_param_id {lid} rank 0 expected {semantics}, got {actual}")
+            shape = tuple(int(s) for s in p.shape)
+            descriptors.append(
+                SerializableGradientDescriptor(
+                    logical_param_id=lid,
+                    shared_weight_id=shared_id,
+                    shared_weight_root=shared_root,
+                    logical_region_key=lid,
+                    semantic_order_key=(op.op_index, order, lid),
+                    global_rank=0,
+                    model_impl=model_impl,
+                    op_manifest_hash=manifest_hash,
+                    pipeline_id=0,
+                    stage_id=0,
+                    model_chunk_id=0,
+                    global_op_index=op.op_index,
+                    manifest_op_name=op.name,
+                    runtime_op_name=op.name,
+                    relative_parameter_name=path,
+                    stage_global_op_begin=stage_op_begin,
+                    stage_global_op_end=stage_op_end,
+                    local_tp_degree=1,
+                    local_tp_rank=0,
+                    local_dp_degree=1,
+                    local_dp_rank=0,
+                    local_cp_degree=1,
+                    local_cp_rank=0,
+                    stage_ranks=(0,),
+                    local_tp_group_ranks=(0,),
+                    local_dp_group_ranks=(0,),
+                    full_shape=shape,
+                    local_shape=shape,
+                    tensor_parallel=tp,
+                    tp_replica_semantics=None if tp else "identical_duplicate",
+                    partition_dim=pdim if tp else -1,
+                    partition_stride=int(p.partition_stride),
+                    parameter_dtype=str(p.dtype),
+                    gradient_dtype=str(mg.dtype),
+                    requires_grad=True,
+                )
+            )
+            bindings.append(LocalGradientBinding(logical_param_id=lid, parameter=p, main_grad=mg, device=p.device))
+        unlisted = {id(p) for p in op.parameters() if p.requires_grad} - seen
+        if unlisted:
+            raise ValueError(f"unlisted trainable parameter on rank 0 op {op.op_index} ({op.name})")
+    return tuple(descriptors), tuple(bindings)

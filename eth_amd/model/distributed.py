@@ -1,0 +1,94 @@
+"""Local DDP wrapper: contiguous main-grad buffers.
+
+Restates eth/runtime/megatron/model/distributed.py:18-127: one buffer per
+gradient dtype (fp32 when accumulate_allreduce_grads_in_fp32, which bf16
+forces), parameters carved from the END of the buffer in
+module.parameters() order, `param.main_grad` views, a hook that folds any
+`param.grad` into main_grad and clears it, and zero_grad_buffer().  The HIP
+autograd Functions accumulate straight into main_grad, so the hook only
+fires for gradients produced outside them.  Zeroing uses a fill kernel (no
+hipMemsetAsync).
+"""
+
+import torch
+from torch import nn
+
+from .. import _native as nat
+
+
+class MemoryBuffer:
+    def __init__(self, numel, dtype, device):
+        self.numel = numel
+        self.dtype = dtype
+        self.data = torch.zeros(numel, dtype=dtype, device=device)
+
+    def zero(self):
+        if self.dtype == torch.float32 and self.data.is_cuda:
+            nat.call("eth_fill_f32", nat.ptr(self.data), self.numel, 0.0, nat.stream_ptr(self.data.device))
+        else:
+            self.data.zero_()
+
+    def get(self, shape, start_index):
+        end = start_index + torch.Size(shape).numel()
+        if end > self.numel:
+            raise ValueError("requested tensor is out of the buffer range")
+        return self.data[start_index:end].view(shape)
+
+
+class DistributedDataParallel(nn.Module):
+    def __init__(self, module, accumulate_allreduce_grads_in_fp32=True, use_contiguous_buffers=True):
+        super().__init__()
+        self.module = module
+        self.accumulate_allreduce_grads_in_fp32 = accumulate_allreduce_grads_in_fp32
+        self.use_contiguous_buffers = use_contiguous_buffers
+        self._grad_buffers = {}
+        self._initialize_main_grad_buffers()
+
+    def _grad_dtype(self, p):
+        return torch.float32 if self.accumulate_allreduce_grads_in_fp32 else p.dtype
+
+    def _initialize_main_grad_buffers(self):
+        numel, device = {}, {}
+        for p in self.module.parameters():
+            if not p.requires_grad:
+                continue
+            dt = self._grad_dtype(p)
+            dev = torch.device(p.device)
+            if device.setdefault(dt, dev) != dev:
+                raise ValueError(f"parameters with gradient dtype {dt} span devices")
+            numel[dt] = numel.get(dt, 0) + p.numel()
+        self._grad_buffers = {dt: MemoryBuffer(n, dt, device[dt]) for dt, n in numel.items()}
+        remaining = dict(numel)
+        for p in self.module.parameters():
+            if not p.requires_grad:
+                continue
+            dt = self._grad_dtype(p)
+            remaining[dt] -= p.numel()
+            p.main_grad = self._grad_buffers[dt].get(p.shape, remaining[dt])
+        self.grad_accs = []
+        for p in self.module.parameters():
+            if not p.requires_grad:
+                continue
+            acc = p.expand_as(p).grad_fn.next_functions[0][0]
+            acc.register_hook(self._make_param_hook(p))
+            self.grad_accs.append(acc)
+
+    @staticmethod
+    def _make_param_hook(param):
+        def hook(*unused):
+            if param.grad is not None:
+                param.main_grad.add_(param.grad.data)
+                param.grad = None
+
+        return hook
+
+    def zero_grad_buffer(self):
+        for buf in self._grad_buffers.values():
+            buf.zero()
+
+    @property
+    def grad_buffers(self):
+        return self._grad_buffers
+
+    def forward(self, *args, **kwargs):
+        return self.module(*args, **kwargs)

@@ -1,0 +1,186 @@
+"""autograd Functions over the HIP kernels.
+
+Weight and bias gradients follow the Megatron local-DDP contract
+(eth/runtime/megatron/model/distributed.py:116-123): when a parameter has a
+`main_grad` (fp32) buffer, its gradient is accumulated straight into it by
+the kernel (the wgrad GEMM adds into main_grad; bias / LayerNorm gradients
+are reduced in fp32 and added), and the autograd gradient returned for the
+parameter is None, so `param.grad` stays None.  Without `main_grad` the
+gradient is returned in the parameter's dtype.
+"""
+
+import torch
+
+from .. import kernels as K
+
+
+def _fp32_accum_target(param):
+    mg = getattr(param, "main_grad", None)
+    if mg is not None and mg.dtype != torch.float32:
+        raise ValueError("main_grad must be fp32 for the fused accumulation")
+    return mg
+
+
+def _flat(x):
+    return x.reshape(-1, x.shape[-1])
+
+
+class LinearFn(torch.autograd.Function):
+    """y = x @ W^T (+ b): ColumnParallelLinear / RowParallelLinear at TP=1."""
+
+    @staticmethod
+    def forward(ctx, x, weight, bias):
+        x2 = _flat(x.contiguous())
+        y = K.gemm(x2, weight.t(), bias=bias)
+        ctx.save_for_backward(x2, weight, bias)
+        ctx.in_shape = x.shape
+        return y.view(*x.shape[:-1], weight.shape[0])
+
+    @staticmethod
+    def backward(ctx, dy):
+        x2, weight, bias = ctx.saved_tensors
+        dy2 = _flat(dy.contiguous())
+        dx = K.gemm(dy2, weight).view(ctx.in_shape) if ctx.needs_input_grad[0] else None
+        dw = db = None
+        if ctx.needs_input_grad[1]:
+            mg = _fp32_accum_target(weight)
+            if mg is not None:
+                K.gemm(dy2.t(), x2, out=mg, accumulate=True)
+            else:
+                acc = torch.zeros(weight.shape, dtype=torch.float32, device=weight.device)
+                K.gemm(dy2.t(), x2, out=acc, accumulate=True)
+                dw = acc.to(weight.dtype)
+        if bias is not None and ctx.needs_input_grad[2]:
+            mg = _fp32_accum_target(bias)
+            if mg is not None:
+                K.col_sum(dy2, mg, accumulate=True)
+            else:
+                acc = torch.zeros(bias.shape, dtype=torch.float32, device=bias.device)
+                K.col_sum(dy2, acc, accumulate=False)
+                db = acc.to(bias.dtype)
+        return dx, dw, db
+
+
+class LayerNormFn(torch.autograd.Function):
+    """MixedFusedLayerNorm (model/fused_layer_norm.py:30-89)."""
+
+    @staticmethod
+    def forward(ctx, x, gamma, beta, eps):
+        xc = x.contiguous()
+        y, mean, rstd = K.layer_norm_fwd(_flat(xc), gamma, beta, eps)
+        ctx.save_for_backward(xc, gamma, beta, mean, rstd)
+        return y.view(x.shape)
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, gamma, beta, mean, rstd = ctx.saved_tensors
+        mg_g, mg_b = _fp32_accum_target(gamma), _fp32_accum_target(beta)
+        if mg_g is not None and mg_b is not None:
+            dg, db, acc = mg_g, mg_b, True
+        else:
+            dg = torch.zeros(gamma.shape, dtype=torch.float32, device=x.device)
+            db = torch.zeros(beta.shape, dtype=torch.float32, device=x.device)
+            acc = False
+        dx = K.layer_norm_bwd(_flat(dy.contiguous()), _flat(x), mean, rstd, gamma, dg, db, accumulate=acc)
+        if acc:
+            return dx.view(x.shape), None, None, None
+        return dx.view(x.shape), dg.to(gamma.dtype), db.to(beta.dtype), None
+
+
+class BiasGeluFn(torch.autograd.Function):
+    """gelu_tanh(x + b) (flex_ops.py:1882-1906)."""
+
+    @staticmethod
+    def forward(ctx, x, bias):
+        xc = x.contiguous()
+        y = K.bias_gelu_fwd(_flat(xc), bias)
+        ctx.save_for_backward(xc, bias)
+        return y.view(x.shape)
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, bias = ctx.saved_tensors
+        dx = K.bias_gelu_bwd(_flat(dy.contiguous()), _flat(x), bias)
+        db = None
+        if ctx.needs_input_grad[1]:
+            mg = _fp32_accum_target(bias)
+            if mg is not None:
+                K.col_sum(dx, mg, accumulate=True)
+            else:
+                acc = torch.zeros(bias.shape, dtype=torch.float32, device=bias.device)
+                K.col_sum(dx, acc, accumulate=False)
+                db = acc.to(bias.dtype)
+        return dx.view(x.shape), db
+
+
+class BiasDropoutAddFn(torch.autograd.Function):
+    """residual + dropout(x + b, p) (flex_ops.py:104-134)."""
+
+    @staticmethod
+    def forward(ctx, x, bias, residual, p, seed):
+        out = K.bias_dropout_add_fwd(_flat(x.contiguous()), bias, _flat(residual.contiguous()), p=p, seed=seed)
+        ctx.p, ctx.seed = p, seed
+        ctx.save_for_backward(bias)
+        return out.view(x.shape)
+
+    @staticmethod
+    def backward(ctx, dout):
+        (bias,) = ctx.saved_tensors
+        dout = dout.contiguous()
+        dx = K.dropout_bwd(_flat(dout), ctx.p, ctx.seed).view(dout.shape) if ctx.p > 0 else dout
+        db = None
+        if ctx.needs_input_grad[1]:
+            mg = _fp32_accum_target(bias)
+            if mg is not None:
+                K.col_sum(_flat(dx), mg, accumulate=True)
+            else:
+                acc = torch.zeros(bias.shape, dtype=torch.float32, device=bias.device)
+                K.col_sum(_flat(dx), acc, accumulate=False)
+                db = acc.to(bias.dtype)
+        return dx, db, dout, None, None
+
+
+class SplitQKVFn(torch.autograd.Function):
+    """[s, b, np, 3*hn] -> q, k, v views (split_tensor_along_last_dim,
+    mpu/utils.py:33-52) without copies.  When the incoming gradients are the
+    three views of one [s, b, np, 3*hn] buffer (what attention's backward
+    writes), that buffer is passed back as is."""
+
+    @staticmethod
+    def forward(ctx, mixed, hn):
+        ctx.hn = hn
+        ctx.shape = mixed.shape
+        q, k, v = torch.split(mixed, hn, dim=-1)
+        return q, k, v
+
+    @staticmethod
+    def backward(ctx, dq, dk, dv):
+        hn = ctx.hn
+        base = getattr(dq, "_eth_qkv_base", None)
+        if base is not None and dk is not None and dv is not None:
+            return base, None
+        out = torch.zeros(ctx.shape, dtype=(dq if dq is not None else dk).dtype, device=(dq if dq is not None else dk).device)
+        for i, g in enumerate((dq, dk, dv)):
+            if g is not None:
+                out[..., i * hn : (i + 1) * hn].copy_(g)
+        return out, None
+
+
+class CausalAttentionFn(torch.autograd.Function):
+    """softmax(QK^T/sqrt(hn) + causal) V on [s, b, np, hn] views -> [s, b, np*hn]."""
+
+    @staticmethod
+    def forward(ctx, q, k, v):
+        out, lse = K.attention_fwd(q, k, v)
+        ctx.save_for_backward(q, k, v, out, lse)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        q, k, v, out, lse = ctx.saved_tensors
+        s, b, n, hn = q.shape
+        dqkv = torch.empty(s, b, n, 3 * hn, dtype=q.dtype, device=q.device)
+        dq, dk, dv = torch.split(dqkv, hn, dim=-1)
+        K.attention_bwd(q, k, v, out, dout.contiguous(), lse, dq, dk, dv)
+        dq._eth_qkv_base = dqkv
+        return dq, dk, dv
