@@ -176,15 +176,6 @@ __global__ void __launch_bounds__(kEwThreads) col_sum_part_kernel(const uint16_t
   for (int j = 0; j < 8; ++j) p[j] = acc[j];
 }
 
-__global__ void col_sum_reduce_kernel(const float* __restrict__ part, int groups, int cols,
-                                      float* __restrict__ out, int accumulate) {
-  const int c = blockIdx.x * blockDim.x + threadIdx.x;
-  if (c >= cols) return;
-  float a = 0.f;
-  for (int g = 0; g < groups; ++g) a += part[(int64_t)g * cols + c];
-  out[c] = accumulate ? out[c] + a : a;
-}
-
 inline int ew_grid(int64_t nvec) {
   int64_t g = (nvec + kEwThreads - 1) / kEwThreads;
   return (int)(g > 8192 ? 8192 : (g < 1 ? 1 : g));
@@ -299,7 +290,8 @@ extern "C" int eth_col_sum(const void* x, int64_t ld, int64_t rows, int64_t cols
     col_sum_part_kernel<true><<<grid, kEwThreads, 0, s>>>((const uint16_t*)x, ld, (int)rows, (int)cols, rpg,
                                                           workspace);
   ETH_CHECK_LAUNCH("eth_col_sum");
-  col_sum_reduce_kernel<<<(int)((cols + 255) / 256), 256, 0, s>>>(workspace, groups, (int)cols, out, accumulate);
+  reduce_partials_kernel<<<reduce_partials_grid((int)cols), kReducePartialsThreads, 0, s>>>(
+      workspace, groups, (int)cols, cols, out, accumulate);
   ETH_CHECK_LAUNCH("eth_col_sum reduce");
   return ETH_OK;
 }

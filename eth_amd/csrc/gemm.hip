@@ -41,7 +41,6 @@ __device__ __forceinline__ f32x16_t mfma32(const uint4& a, const uint4& b, const
   }
 }
 
-constexpr int kGemmThreads = 256;
 constexpr int kPad = 8;  // LDS row padding (elements): 16 B breaks bank aliasing
 
 // Map a linear workgroup id to (tile_m, tile_n): XCD-contiguous, then
@@ -60,71 +59,105 @@ __device__ __forceinline__ void tile_coords(int pid, int tiles_m, int tiles_n, i
   tn = (pid % in_group) / gm;
 }
 
-// Load a ROWS x BK tile of a K-contiguous operand (row r at P[(r0+r)*ld + k])
-// into registers: CPT 16-byte chunks per thread.
-template <int ROWS, int BK>
+// Buffer-resource loads: 32-bit byte offsets (one VGPR per chunk, fixed for
+// the whole K loop; the k advance goes in the scalar offset) and hardware
+// bounds checking -- an offset of kOob reads zeros, which masks rows past
+// the matrix and k past K without branches.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr int32_t kOob = (int32_t)0x80000000u;
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 buf_load16(rsrc_t r, int32_t voff, int32_t soff) {
+  auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+  return __builtin_bit_cast(uint4, v);
+}
+
+// ROWS x BK tile of a K-contiguous operand (row r at P[(r0+r)*ld + k]):
+// CPT 16-byte chunks per thread.
+template <int ROWS, int BK, int NT>
 struct KTile {
   static constexpr int CPR = BK / 8;
-  static constexpr int CPT = ROWS * CPR / kGemmThreads;
+  static constexpr int CPT = ROWS * CPR / NT;
+  static_assert(CPT >= 1 && ROWS * CPR % NT == 0, "tile split");
   uint4 v[CPT];
-  __device__ __forceinline__ void load(const uint16_t* __restrict__ P, int64_t ld, int r0, int rows,
-                                       int k0, int K) {
+  int32_t off[CPT];
+  __device__ __forceinline__ void init(int64_t ld, int r0, int rows) {
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
-      const int c = threadIdx.x + i * kGemmThreads;
+      const int c = threadIdx.x + i * NT;
       const int r = c / CPR, kc = (c % CPR) * 8;
-      if (r0 + r < rows && k0 + kc < K)
-        v[i] = *reinterpret_cast<const uint4*>(P + (int64_t)(r0 + r) * ld + k0 + kc);
-      else
-        v[i] = make_uint4(0, 0, 0, 0);
+      off[i] = r0 + r < rows ? (int32_t)((((int64_t)(r0 + r)) * ld + kc) * 2) : kOob;
+    }
+  }
+  __device__ __forceinline__ void load(rsrc_t rs, int64_t ld, int k0, int K, bool kfull) {
+    const int32_t soff = k0 * 2;
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      int32_t o = off[i];
+      if (!kfull && k0 + ((threadIdx.x + i * NT) % CPR) * 8 >= K) o = kOob;
+      v[i] = buf_load16(rs, o, soff);
     }
   }
   __device__ __forceinline__ void store(uint16_t* S) const {
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
-      const int c = threadIdx.x + i * kGemmThreads;
+      const int c = threadIdx.x + i * NT;
       const int r = c / CPR, kc = (c % CPR) * 8;
       *reinterpret_cast<uint4*>(S + r * (BK + kPad) + kc) = v[i];
     }
   }
 };
 
-// Load a BK x ROWS tile of an operand contiguous along the row index
-// (element (r, k) at P[k*ld + r0 + r]): each thread reads 4 k-rows of 8
-// consecutive r and writes them transposed (8 rows of 4 k) into LDS.
-template <int ROWS, int BK>
+// BK x ROWS tile of an operand contiguous along the row index (element
+// (r, k) at P[k*ld + r0 + r]): each thread reads 4 k-rows of 8 consecutive
+// r and writes them transposed (8 rows of 4 k) into LDS.  The k-group index
+// varies fastest across lanes, so the 8-byte LDS writes of a wavefront
+// spread over all banks (rows 8 apart would alias otherwise).
+template <int ROWS, int BK, int NT>
 struct RTile {
   static constexpr int RG = ROWS / 8, KG = BK / 4;
-  static constexpr int BPT = RG * KG / kGemmThreads;
+  static constexpr int BPT = RG * KG / NT;
+  static_assert(BPT >= 1 && RG * KG % NT == 0, "tile split");
   uint4 v[BPT][4];
-  __device__ __forceinline__ void load(const uint16_t* __restrict__ P, int64_t ld, int r0, int rows,
-                                       int k0, int K) {
+  int32_t off[BPT];
+  __device__ __forceinline__ void init(int64_t ld, int r0, int rows) {
 #pragma unroll
     for (int b = 0; b < BPT; ++b) {
-      const int blk = threadIdx.x + b * kGemmThreads;
-      const int rg = blk % RG, kg = blk / RG;
+      const int blk = threadIdx.x + b * NT;
+      const int kg = blk % KG, rg = blk / KG;
       const int r = r0 + rg * 8;
+      off[b] = r < rows ? (int32_t)((((int64_t)kg * 4) * ld + r) * 2) : kOob;
+    }
+  }
+  __device__ __forceinline__ void load(rsrc_t rs, int64_t ld, int k0, int K, bool kfull) {
+    const int32_t soff = (int32_t)((int64_t)k0 * ld * 2);
+    const int32_t row_bytes = (int32_t)(ld * 2);
+#pragma unroll
+    for (int b = 0; b < BPT; ++b) {
+      const int kg = (threadIdx.x + b * NT) % KG;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int k = k0 + kg * 4 + j;
-        if (r < rows && k < K)
-          v[b][j] = *reinterpret_cast<const uint4*>(P + (int64_t)k * ld + r);
-        else
-          v[b][j] = make_uint4(0, 0, 0, 0);
+        int32_t o = off[b] == kOob ? kOob : off[b] + j * row_bytes;
+        if (!kfull && k0 + kg * 4 + j >= K) o = kOob;
+        v[b][j] = buf_load16(rs, o, soff);
       }
     }
   }
-  __device__ __forceinline__ void store(uint16_t* S) const {
+  __device__ __forceinline__ void store(uint16_t* S) const { store_part(S, 0, 1); }
+  __device__ __forceinline__ void store_part(uint16_t* S, int part, int parts) const {
 #pragma unroll
     for (int b = 0; b < BPT; ++b) {
-      const int blk = threadIdx.x + b * kGemmThreads;
-      const int rg = blk % RG, kg = blk / RG;
+      const int blk = threadIdx.x + b * NT;
+      const int kg = blk % KG, rg = blk / KG;
       const uint32_t* w0 = reinterpret_cast<const uint32_t*>(&v[b][0]);
       const uint32_t* w1 = reinterpret_cast<const uint32_t*>(&v[b][1]);
       const uint32_t* w2 = reinterpret_cast<const uint32_t*>(&v[b][2]);
       const uint32_t* w3 = reinterpret_cast<const uint32_t*>(&v[b][3]);
 #pragma unroll
       for (int p = 0; p < 4; ++p) {
+        if ((b * 4 + p) * parts / (BPT * 4) != part) continue;
         // rows 2p and 2p+1 of the 8-row group
         const uint32_t a0 = w0[p], a1 = w1[p], a2 = w2[p], a3 = w3[p];
         uint2 lo, hi;
@@ -140,16 +173,17 @@ struct RTile {
   }
 };
 
-template <int ROWS, int BK, bool KCONTIG>
+template <int ROWS, int BK, int NT, bool KCONTIG>
 struct TileLoader;
-template <int ROWS, int BK>
-struct TileLoader<ROWS, BK, true> : KTile<ROWS, BK> {};
-template <int ROWS, int BK>
-struct TileLoader<ROWS, BK, false> : RTile<ROWS, BK> {};
+template <int ROWS, int BK, int NT>
+struct TileLoader<ROWS, BK, NT, true> : KTile<ROWS, BK, NT> {};
+template <int ROWS, int BK, int NT>
+struct TileLoader<ROWS, BK, NT, false> : RTile<ROWS, BK, NT> {};
 
 struct GemmArgs {
   const uint16_t* A;
   const uint16_t* B;
+  uint32_t a_bytes, b_bytes;  // extent of A / B for the buffer range checks
   void* C;
   const uint16_t* bias;
   int M, N, K;
@@ -159,9 +193,10 @@ struct GemmArgs {
   float alpha;
 };
 
-template <int BM, int BN, int BK, bool A_K, bool B_K, bool FP16>
-__global__ void __launch_bounds__(kGemmThreads) gemm_kernel(GemmArgs g) {
-  constexpr int WM = BM / 2, WN = BN / 2;
+template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, bool A_K, bool B_K, bool FP16>
+__global__ void __launch_bounds__(64 * WAVES_M * WAVES_N) gemm_kernel(GemmArgs g) {
+  constexpr int NT = 64 * WAVES_M * WAVES_N;
+  constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
   constexpr int TM = WM / 32, TN = WN / 32;
   constexpr int LDS_ROW = BK + kPad;
   __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * LDS_ROW];
@@ -172,7 +207,7 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_kernel(GemmArgs g) {
   tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  const int wm = wid >> 1, wn = wid & 1;
+  const int wm = wid / WAVES_N, wn = wid % WAVES_N;
   const int lr = lane & 31, lk = (lane >> 5) * 8;
 
   f32x16_t acc[TM][TN];
@@ -183,38 +218,54 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_kernel(GemmArgs g) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  TileLoader<BM, BK, A_K> la;
-  TileLoader<BN, BK, B_K> lb;
   const int nk = (g.K + BK - 1) / BK;
-  la.load(g.A, g.lda, m0, g.M, 0, g.K);
-  lb.load(g.B, g.ldb, n0, g.N, 0, g.K);
+  // MFMA over one LDS stage; operand fragments of k-step ks+1 are read from
+  // LDS while the MFMAs of k-step ks run
+  auto compute = [&](int st) {
+    const uint16_t* as = As[st] + (wm * WM + lr) * LDS_ROW + lk;
+    const uint16_t* bs = Bs[st] + (wn * WN + lr) * LDS_ROW + lk;
+    uint4 af[2][TM], bfr[2][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) af[0][i] = *reinterpret_cast<const uint4*>(as + i * 32 * LDS_ROW);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) bfr[0][j] = *reinterpret_cast<const uint4*>(bs + j * 32 * LDS_ROW);
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ++ks) {
+      const int cur = ks & 1, nxt = cur ^ 1;
+      if (ks + 1 < BK / 16) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+          af[nxt][i] = *reinterpret_cast<const uint4*>(as + i * 32 * LDS_ROW + (ks + 1) * 16);
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          bfr[nxt][j] = *reinterpret_cast<const uint4*>(bs + j * 32 * LDS_ROW + (ks + 1) * 16);
+      }
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = mfma32<FP16>(af[cur][i], bfr[cur][j], acc[i][j]);
+    }
+  };
+
+  const rsrc_t ra = make_rsrc(g.A, g.a_bytes), rb = make_rsrc(g.B, g.b_bytes);
+  const bool kfull = g.K % BK == 0;
+  TileLoader<BM, BK, NT, A_K> la;
+  TileLoader<BN, BK, NT, B_K> lb;
+  la.init(g.lda, m0, g.M);
+  lb.init(g.ldb, n0, g.N);
+  la.load(ra, g.lda, 0, g.K, kfull);
+  lb.load(rb, g.ldb, 0, g.K, kfull);
   la.store(As[0]);
   lb.store(Bs[0]);
   __syncthreads();
-
   for (int kt = 0; kt < nk; ++kt) {
     const int st = kt & 1;
     const bool more = kt + 1 < nk;
     if (more) {
-      la.load(g.A, g.lda, m0, g.M, (kt + 1) * BK, g.K);
-      lb.load(g.B, g.ldb, n0, g.N, (kt + 1) * BK, g.K);
+      la.load(ra, g.lda, (kt + 1) * BK, g.K, kfull);
+      lb.load(rb, g.ldb, (kt + 1) * BK, g.K, kfull);
     }
-    const uint16_t* as = As[st] + (wm * WM + lr) * LDS_ROW + lk;
-    const uint16_t* bs = Bs[st] + (wn * WN + lr) * LDS_ROW + lk;
-#pragma unroll
-    for (int ks = 0; ks < BK / 16; ++ks) {
-      uint4 af[TM], bfr[TN];
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-        af[i] = *reinterpret_cast<const uint4*>(as + i * 32 * LDS_ROW + ks * 16);
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-        bfr[j] = *reinterpret_cast<const uint4*>(bs + j * 32 * LDS_ROW + ks * 16);
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = mfma32<FP16>(af[i], bfr[j], acc[i][j]);
-    }
+    compute(st);
     if (more) {
       la.store(As[st ^ 1]);
       lb.store(Bs[st ^ 1]);
@@ -252,17 +303,18 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_kernel(GemmArgs g) {
   }
 }
 
-template <int BM, int BN, int BK, bool FP16>
+template <int BM, int BN, int BK, int WMW, int WNW, bool FP16>
 static int launch_layout(const GemmArgs& a, int a_k, int b_k, hipStream_t s) {
   const int tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
+  constexpr int NT = 64 * WMW * WNW;
   if (a_k && b_k)
-    gemm_kernel<BM, BN, BK, true, true, FP16><<<tiles, kGemmThreads, 0, s>>>(a);
+    gemm_kernel<BM, BN, BK, WMW, WNW, true, true, FP16><<<tiles, NT, 0, s>>>(a);
   else if (a_k && !b_k)
-    gemm_kernel<BM, BN, BK, true, false, FP16><<<tiles, kGemmThreads, 0, s>>>(a);
+    gemm_kernel<BM, BN, BK, WMW, WNW, true, false, FP16><<<tiles, NT, 0, s>>>(a);
   else if (!a_k && !b_k)
-    gemm_kernel<BM, BN, BK, false, false, FP16><<<tiles, kGemmThreads, 0, s>>>(a);
+    gemm_kernel<BM, BN, BK, WMW, WNW, false, false, FP16><<<tiles, NT, 0, s>>>(a);
   else
-    gemm_kernel<BM, BN, BK, false, true, FP16><<<tiles, kGemmThreads, 0, s>>>(a);
+    gemm_kernel<BM, BN, BK, WMW, WNW, false, true, FP16><<<tiles, NT, 0, s>>>(a);
   ETH_CHECK_LAUNCH("eth_gemm");
   return ETH_OK;
 }
@@ -288,9 +340,16 @@ extern "C" int eth_gemm(const void* A, int64_t lda, int a_kcontig, const void* B
   ETH_CHECK_ARG(ldc >= N, "eth_gemm: ldc < N");
   ETH_CHECK_ARG(!(flags & ETH_GEMM_ACCUMULATE) || c_dtype == ETH_F32, "eth_gemm: accumulate needs fp32 C");
   ETH_CHECK_ARG(!(flags & ETH_GEMM_BIAS) || bias, "eth_gemm: bias flag without bias");
+  // extents: A spans M rows of lda (K-contiguous) or K rows of lda; same for B
+  const int64_t a_elems = a_kcontig ? (M - 1) * lda + K : (K - 1) * lda + M;
+  const int64_t b_elems = b_kcontig ? (N - 1) * ldb + K : (K - 1) * ldb + N;
+  ETH_CHECK_ARG(a_elems * 2 < (1LL << 31) && b_elems * 2 < (1LL << 31),
+                "eth_gemm: operands above 2 GiB are not supported");
   GemmArgs a;
   a.A = (const uint16_t*)A;
   a.B = (const uint16_t*)B;
+  a.a_bytes = (uint32_t)(a_elems * 2);
+  a.b_bytes = (uint32_t)(b_elems * 2);
   a.C = C;
   a.bias = (const uint16_t*)bias;
   a.M = (int)M;
@@ -303,6 +362,13 @@ extern "C" int eth_gemm(const void* A, int64_t lda, int a_kcontig, const void* B
   a.flags = flags;
   a.alpha = alpha;
   hipStream_t s = (hipStream_t)stream;
-  if (in_dtype == ETH_BF16) return launch_layout<128, 128, 64, false>(a, a_kcontig, b_kcontig, s);
-  return launch_layout<128, 128, 64, true>(a, a_kcontig, b_kcontig, s);
+  // 256x256 tiles (8 waves of 128x64) when the grid still fills the chip,
+  // 128x128 (4 waves of 64x64) otherwise
+  const int64_t big_tiles = ((M + 255) / 256) * ((N + 255) / 256);
+  const bool big = big_tiles >= 192;
+  if (in_dtype == ETH_BF16)
+    return big ? launch_layout<256, 256, 64, 2, 4, false>(a, a_kcontig, b_kcontig, s)
+               : launch_layout<128, 128, 64, 2, 2, false>(a, a_kcontig, b_kcontig, s);
+  return big ? launch_layout<256, 256, 64, 2, 4, true>(a, a_kcontig, b_kcontig, s)
+             : launch_layout<128, 128, 64, 2, 2, true>(a, a_kcontig, b_kcontig, s);
 }

@@ -218,6 +218,23 @@ __global__ void __launch_bounds__(1024) finalize_kernel(const double* __restrict
   }
 }
 
+__global__ void __launch_bounds__(kReducePartialsThreads)
+    reduce_partials_kernel(const float* __restrict__ part, int groups, int cols, int64_t ld,
+                           float* __restrict__ out, int accumulate) {
+  __shared__ float red[4][64];
+  const int c = blockIdx.x * 64 + (threadIdx.x & 63);
+  const int lane_g = threadIdx.x >> 6;
+  float a = 0.f;
+  if (c < cols)
+    for (int g = lane_g; g < groups; g += 4) a += part[(int64_t)g * ld + c];
+  red[lane_g][threadIdx.x & 63] = a;
+  __syncthreads();
+  if (lane_g == 0 && c < cols) {
+    const float t = (red[0][threadIdx.x] + red[1][threadIdx.x]) + (red[2][threadIdx.x] + red[3][threadIdx.x]);
+    out[c] = accumulate ? out[c] + t : t;
+  }
+}
+
 __global__ void fill_kernel(float* dst, int64_t n, float v) {
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * blockDim.x)

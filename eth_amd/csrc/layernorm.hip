@@ -198,26 +198,6 @@ __global__ void __launch_bounds__(64 * kLnWaves) ln_bwd_kernel(
   }
 }
 
-// Column reduction of the partials: one thread per column, fixed order.
-__global__ void ln_bwd_reduce_kernel(const float* __restrict__ part, int groups, int cols,
-                                     float* __restrict__ dgamma, float* __restrict__ dbeta,
-                                     int accumulate) {
-  const int col = blockIdx.x * blockDim.x + threadIdx.x;
-  if (col >= cols) return;
-  float a = 0.f, b = 0.f;
-  for (int gi = 0; gi < groups; ++gi) {
-    a += part[(int64_t)gi * 2 * cols + col];
-    b += part[(int64_t)gi * 2 * cols + cols + col];
-  }
-  if (accumulate) {
-    dgamma[col] += a;
-    dbeta[col] += b;
-  } else {
-    dgamma[col] = a;
-    dbeta[col] = b;
-  }
-}
-
 template <bool FP16>
 static void launch_fwd(const uint16_t* x, const uint16_t* g, const uint16_t* b, uint16_t* y, float* mean,
                        float* rstd, int rows, int cols, float eps, hipStream_t s) {
@@ -300,8 +280,11 @@ extern "C" int eth_ln_bwd(const void* dy, const void* x, const float* mean, cons
     launch_bwd<true>((const uint16_t*)dy, (const uint16_t*)x, mean, rstd, (const uint16_t*)gamma,
                      (uint16_t*)dx, workspace, groups, rpg, (int)rows, (int)cols, s);
   ETH_CHECK_LAUNCH("eth_ln_bwd");
-  ln_bwd_reduce_kernel<<<(int)((cols + 255) / 256), 256, 0, s>>>(workspace, groups, (int)cols, dgamma,
-                                                                   dbeta, accumulate);
+  // partials are [groups][2][cols]: dgamma rows at offset 0, dbeta at +cols
+  reduce_partials_kernel<<<reduce_partials_grid((int)cols), kReducePartialsThreads, 0, s>>>(
+      workspace, groups, (int)cols, 2 * cols, dgamma, accumulate);
+  reduce_partials_kernel<<<reduce_partials_grid((int)cols), kReducePartialsThreads, 0, s>>>(
+      workspace + cols, groups, (int)cols, 2 * cols, dbeta, accumulate);
   ETH_CHECK_LAUNCH("eth_ln_bwd reduce");
   return ETH_OK;
 }

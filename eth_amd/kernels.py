@@ -48,6 +48,17 @@ def _matrix_layout(t):
     raise ValueError(f"operand with strides {t.stride()} is neither row- nor column-major")
 
 
+_gemm_observer = None
+
+
+def set_gemm_observer(fn):
+    """fn(phase, M, N, K) is called right before ("begin") and after ("end")
+    every GEMM launch (used by the benchmark to time the GEMMs with events on
+    the launch stream); None disables it."""
+    global _gemm_observer
+    _gemm_observer = fn
+
+
 def gemm(a, b, out=None, bias=None, accumulate=False, out_dtype=None, alpha=1.0):
     """out (+)= alpha * a @ b (+ bias), a: [M, K], b: [K, N] (any row/column-
     major 2-D views), out: [M, N] row-major.  fp32 `out` with accumulate=True
@@ -75,6 +86,9 @@ def gemm(a, b, out=None, bias=None, accumulate=False, out_dtype=None, alpha=1.0)
         if bias.dtype != a.dtype or bias.numel() != N or not bias.is_contiguous():
             raise ValueError("bias must be a contiguous [N] tensor of the input dtype")
         flags |= nat.GEMM_BIAS
+    obs = _gemm_observer
+    if obs is not None:
+        obs("begin", M, N, K)
     nat.call(
         "eth_gemm",
         nat.ptr(a), lda, a_kcontig,
@@ -83,6 +97,8 @@ def gemm(a, b, out=None, bias=None, accumulate=False, out_dtype=None, alpha=1.0)
         nat.ptr(bias), M, N, K, code, flags, float(alpha),
         nat.stream_ptr(a.device),
     )
+    if obs is not None:
+        obs("end", M, N, K)
     return out
 
 
