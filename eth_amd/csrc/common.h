@@ -96,11 +96,11 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
   return t;
 }
 
-// out[c] (+)= sum_g part[g*ld + c] for c < cols: 64 columns per workgroup,
-// 4 lanes of groups per column, fixed summation order (deterministic).
+// out[c] (+)= sum_g part[g*ld + c] for c < cols: 32 columns per workgroup,
+// 8 lanes of groups per column, fixed summation order (deterministic).
 __global__ void reduce_partials_kernel(const float* __restrict__ part, int groups, int cols, int64_t ld,
                                        float* __restrict__ out, int accumulate);
-inline dim3 reduce_partials_grid(int cols) { return dim3((cols + 63) / 64); }
+inline dim3 reduce_partials_grid(int cols) { return dim3((cols + 31) / 32); }
 constexpr int kReducePartialsThreads = 256;
 
 inline int dtype_size(int dtype) { return dtype == ETH_F32 ? 4 : 2; }

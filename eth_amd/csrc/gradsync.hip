@@ -221,16 +221,21 @@ __global__ void __launch_bounds__(1024) finalize_kernel(const double* __restrict
 __global__ void __launch_bounds__(kReducePartialsThreads)
     reduce_partials_kernel(const float* __restrict__ part, int groups, int cols, int64_t ld,
                            float* __restrict__ out, int accumulate) {
-  __shared__ float red[4][64];
-  const int c = blockIdx.x * 64 + (threadIdx.x & 63);
-  const int lane_g = threadIdx.x >> 6;
+  // 32 columns x 8 group-lanes per workgroup; each lane sums every 8th group
+  __shared__ float red[8][33];
+  const int c = blockIdx.x * 32 + (threadIdx.x & 31);
+  const int lane_g = threadIdx.x >> 5;
   float a = 0.f;
-  if (c < cols)
-    for (int g = lane_g; g < groups; g += 4) a += part[(int64_t)g * ld + c];
-  red[lane_g][threadIdx.x & 63] = a;
+  if (c < cols) {
+#pragma unroll 8
+    for (int g = lane_g; g < groups; g += 8) a += part[(int64_t)g * ld + c];
+  }
+  red[lane_g][threadIdx.x & 31] = a;
   __syncthreads();
   if (lane_g == 0 && c < cols) {
-    const float t = (red[0][threadIdx.x] + red[1][threadIdx.x]) + (red[2][threadIdx.x] + red[3][threadIdx.x]);
+    float t = 0.f;
+#pragma unroll
+    for (int w = 0; w < 8; ++w) t += red[w][threadIdx.x];
     out[c] = accumulate ? out[c] + t : t;
   }
 }
