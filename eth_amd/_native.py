@@ -66,6 +66,11 @@ SIGNATURES = {
     "eth_dropout_bwd": [_P, _P, _I64, _I64, _F32, ctypes.c_uint64, _I32, _P],
     "eth_col_sum": [_P, _I64, _I64, _I64, _P, _P, _I32, _I32, _P],
 }
+SIGNATURES["eth_embedding_fwd"] = [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _I32, _P]
+SIGNATURES["eth_embedding_bwd"] = [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I32, _P]
+SIGNATURES["eth_xent_fwd"] = [_P, _I64, _P, _P, _P, _I64, _I64, _P, _I32, _P]
+SIGNATURES["eth_xent_bwd"] = [_P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _I32, _P]
+SIGNATURES["eth_tied_grad_sum"] = [_P, _P, _I64, _P]
 SIGNATURES["eth_attn_fwd"] = [_P, _P, _P, _P, _P, _P, _P]
 SIGNATURES["eth_attn_bwd"] = [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]
 

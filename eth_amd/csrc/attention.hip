@@ -123,6 +123,8 @@ struct RowTile {
 };
 
 // ROWS x D tile stored transposed into LDS [D][ROWS+8] (natural row order).
+// The 4-row group index varies fastest across lanes, so a wavefront's 8-byte
+// LDS writes land in distinct banks (LDS rows 8 apart alias).
 template <int ROWS, int D>
 struct ColTile {
   static constexpr int DG = D / 8, RG = ROWS / 4;
@@ -135,7 +137,7 @@ struct ColTile {
     for (int i = 0; i < BPT; ++i) {
       const int blk = threadIdx.x + i * kAttnThreads;
       if (blk >= NB) break;
-      const int dg = blk % DG, rg = blk / DG;
+      const int rg = blk % RG, dg = blk / RG;
 #pragma unroll
       for (int j = 0; j < 4; ++j)
         v[i][j] = *reinterpret_cast<const uint4*>(row_ptr(t, r0 + rg * 4 + j, b, h) + dg * 8);
@@ -146,7 +148,7 @@ struct ColTile {
     for (int i = 0; i < BPT; ++i) {
       const int blk = threadIdx.x + i * kAttnThreads;
       if (blk >= NB) break;
-      const int dg = blk % DG, rg = blk / DG;
+      const int rg = blk % RG, dg = blk / RG;
       const uint32_t* w0 = reinterpret_cast<const uint32_t*>(&v[i][0]);
       const uint32_t* w1 = reinterpret_cast<const uint32_t*>(&v[i][1]);
       const uint32_t* w2 = reinterpret_cast<const uint32_t*>(&v[i][2]);

@@ -249,3 +249,79 @@ def attention_bwd(q, k, v, out, dout, lse, dq, dk, dv):
         getattr(desc, f"{name}_strides")[:] = _sbhd_strides(t)
     nat.call("eth_attn_bwd", ctypes.byref(desc), nat.ptr(q), nat.ptr(k), nat.ptr(v), nat.ptr(o4), nat.ptr(do4),
              nat.ptr(lse), nat.ptr(delta), nat.ptr(dq), nat.ptr(dk), nat.ptr(dv), nat.stream_ptr(q.device))
+
+
+# --------------------------------------------------------------- vocabulary --
+def _check_ids(t, shape=None):
+    if t.dtype != torch.int64 or not t.is_contiguous() or not t.is_cuda:
+        raise ValueError("token / position ids must be contiguous int64 GPU tensors")
+    if shape is not None and tuple(t.shape) != tuple(shape):
+        raise ValueError(f"ids shape {tuple(t.shape)} != {tuple(shape)}")
+
+
+def embedding_fwd(tokens, positions, word, pos, bad_flag):
+    """[b, s] ids -> [s, b, h] = word[tokens] + pos[positions] (16-bit)."""
+    code = _check_half(word, pos)
+    b, s = tokens.shape
+    _check_ids(tokens)
+    _check_ids(positions, (b, s))
+    V, h = word.shape
+    P, h2 = pos.shape
+    if h != h2 or not word.is_contiguous() or not pos.is_contiguous():
+        raise ValueError("embedding tables must be contiguous [rows, hidden] with equal hidden")
+    out = torch.empty(s, b, h, dtype=word.dtype, device=word.device)
+    nat.call("eth_embedding_fwd", nat.ptr(tokens), nat.ptr(positions), nat.ptr(word), nat.ptr(pos), nat.ptr(out),
+             b, s, h, V, P, nat.ptr(bad_flag), code, nat.stream_ptr(word.device))
+    return out
+
+
+def embedding_bwd(tokens, positions, dout, dword, dpos):
+    """fp32 dword[tokens] += dout and dpos[positions] += dout (dout [s, b, h])."""
+    code = _check_half(dout)
+    b, s = tokens.shape
+    _check_ids(tokens)
+    _check_ids(positions, (b, s))
+    if dout.shape[:2] != (s, b) or not dout.is_contiguous():
+        raise ValueError("dout must be contiguous [s, b, h]")
+    h = dout.shape[2]
+    for t in (dword, dpos):
+        if t is not None and (t.dtype != torch.float32 or t.shape[1] != h or not t.is_contiguous()):
+            raise ValueError("embedding gradients must be contiguous fp32 [rows, hidden]")
+    V = dword.shape[0] if dword is not None else 1
+    P = dpos.shape[0] if dpos is not None else 1
+    nat.call("eth_embedding_bwd", nat.ptr(tokens), nat.ptr(positions), nat.ptr(dout), nat.ptr(dword), nat.ptr(dpos),
+             b, s, h, V, P, code, nat.stream_ptr(dout.device))
+
+
+def xent_fwd(logits2d, labels, bad_flag):
+    """Per-row loss and lse (fp32) of 16-bit logits [rows, V]."""
+    code = _check_half(logits2d)
+    rows, V = logits2d.shape
+    if logits2d.stride(1) != 1:
+        raise ValueError("logits rows must be contiguous")
+    _check_ids(labels, (rows,))
+    loss = torch.empty(rows, dtype=torch.float32, device=logits2d.device)
+    lse = torch.empty(rows, dtype=torch.float32, device=logits2d.device)
+    nat.call("eth_xent_fwd", nat.ptr(logits2d), logits2d.stride(0), nat.ptr(labels), nat.ptr(loss), nat.ptr(lse),
+             rows, V, nat.ptr(bad_flag), code, nat.stream_ptr(logits2d.device))
+    return loss, lse
+
+
+def xent_bwd(logits2d, labels, lse, dloss):
+    code = _check_half(logits2d)
+    rows, V = logits2d.shape
+    if dloss.dtype != torch.float32 or dloss.numel() != rows or not dloss.is_contiguous():
+        raise ValueError("dloss must be contiguous fp32 [rows]")
+    dz = torch.empty(rows, V, dtype=logits2d.dtype, device=logits2d.device)
+    nat.call("eth_xent_bwd", nat.ptr(logits2d), logits2d.stride(0), nat.ptr(labels), nat.ptr(lse), nat.ptr(dloss),
+             nat.ptr(dz), V, rows, V, code, nat.stream_ptr(logits2d.device))
+    return dz
+
+
+def tied_grad_sum(root, copy):
+    """root = copy = root + copy (fp32 main grads of a tied weight)."""
+    if root.dtype != torch.float32 or copy.dtype != torch.float32 or root.shape != copy.shape:
+        raise ValueError("tied gradients must be fp32 tensors of one shape")
+    if not (root.is_contiguous() and copy.is_contiguous()):
+        raise ValueError("tied gradients must be contiguous")
+    nat.call("eth_tied_grad_sum", nat.ptr(root), nat.ptr(copy), root.numel(), nat.stream_ptr(root.device))

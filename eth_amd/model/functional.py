@@ -184,3 +184,45 @@ class CausalAttentionFn(torch.autograd.Function):
         K.attention_bwd(q, k, v, out, dout.contiguous(), lse, dq, dk, dv)
         dq._eth_qkv_base = dqkv
         return dq, dk, dv
+
+
+class EmbeddingFn(torch.autograd.Function):
+    """word[tokens] + pos[positions] -> [s, b, h] (Embedding_v1, dropout p = 0
+    handled by the caller)."""
+
+    @staticmethod
+    def forward(ctx, word, pos, tokens, positions, bad_flag):
+        out = K.embedding_fwd(tokens, positions, word, pos, bad_flag)
+        ctx.save_for_backward(tokens, positions, word, pos)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        tokens, positions, word, pos = ctx.saved_tensors
+        mw, mp = _fp32_accum_target(word), _fp32_accum_target(pos)
+        gw = mw if mw is not None else torch.zeros(word.shape, dtype=torch.float32, device=word.device)
+        gp = mp if mp is not None else torch.zeros(pos.shape, dtype=torch.float32, device=pos.device)
+        K.embedding_bwd(tokens, positions, dout.contiguous(), gw, gp)
+        return (None if mw is not None else gw.to(word.dtype), None if mp is not None else gp.to(pos.dtype), None,
+                None, None)
+
+
+class CrossEntropyFn(torch.autograd.Function):
+    """Per-token loss of 16-bit logits [..., V] against int64 labels [...]
+    (vocab_parallel_cross_entropy at TP = 1, computed in fp32)."""
+
+    @staticmethod
+    def forward(ctx, logits, labels, bad_flag):
+        shape = logits.shape[:-1]
+        z = logits.reshape(-1, logits.shape[-1])
+        lab = labels.reshape(-1).contiguous()
+        loss, lse = K.xent_fwd(z, lab, bad_flag)
+        ctx.save_for_backward(z, lab, lse)
+        ctx.shape = logits.shape
+        return loss.view(shape)
+
+    @staticmethod
+    def backward(ctx, dloss):
+        z, lab, lse = ctx.saved_tensors
+        dz = K.xent_bwd(z, lab, lse, dloss.reshape(-1).float().contiguous())
+        return dz.view(ctx.shape), None, None

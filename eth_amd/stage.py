@@ -16,10 +16,12 @@ unpack bound to the optimizer.
 
 import torch
 
+from . import kernels as K
 from .grad_sync.gpt_adapter import collect_stage_metadata
+from .loss import global_normalization_scale, gpt_loss_output, synthetic_gpt_batch
 from .grad_sync.manager import initialize_gradient_sync
 from .model.distributed import DistributedDataParallel
-from .model.flex_model import middle_stage
+from .model.flex_model import FlexGPTModel, middle_stage
 from .model.flex_ops import GPTConfig
 from .optimizer.optimizer import get_megatron_optimizer
 
@@ -108,3 +110,55 @@ class MiddleStageTrainer:
                     obj = getattr(obj, part)
                 layer[key] = obj
         return [layers[k] for k in sorted(layers)]
+
+
+class FirstLastStageTrainer:
+    """A stage holding the whole GPT model (embedding, layers, final LN, LM
+    head + cross entropy) on one rank: BASELINE configs[0] (fp32 plumbing
+    shape) and configs[4] (GPT-6.7B first+last, fp16)."""
+
+    def __init__(self, cfg: GPTConfig, lr=1e-4, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01, clip_grad=1.0,
+                 sync_mode="block", bucket_cap_bytes=1024 * 1024, initial_loss_scale=2.0**16, unpadded_vocab=50257):
+        self.cfg = cfg
+        self.unpadded_vocab = unpadded_vocab
+        n_ops = 10 * cfg.num_layers + 3
+        self.model = FlexGPTModel(cfg, 0, n_ops)
+        ops = self.model.language_model.ops
+        self.embedding, self.post = ops[0], ops[-1]
+        with torch.no_grad():  # the head copy starts from the root (training.py:349-470)
+            self.post.word_embeddings.weight.copy_(self.embedding.word_embeddings.weight)
+        self.ddp = DistributedDataParallel(self.model, accumulate_allreduce_grads_in_fp32=True)
+        descriptors, bindings = collect_stage_metadata(ops, 0, n_ops)
+        self.grad_sync = initialize_gradient_sync(descriptors, bindings, global_rank=0, expected_pipeline_ids=(0,),
+                                                  sync_mode=sync_mode, bucket_cap_bytes=bucket_cap_bytes)
+        self.optimizer = get_megatron_optimizer(
+            [self.model], lr=lr, weight_decay=weight_decay, betas=betas, eps=eps, clip_grad=clip_grad,
+            bf16=cfg.params_dtype == torch.bfloat16, fp16=cfg.params_dtype == torch.float16,
+            initial_loss_scale=initial_loss_scale,
+        )
+        # tied weights: the norm / unscale run after the tied-gradient sum,
+        # so the optimizer computes its statistics itself (no fused binding)
+        self.nominal = float(cfg.micro_batch_size * cfg.seq_length)
+
+    def forward_backward(self, sample_ids, labels=None):
+        """Returns (per-token loss [b, s], LossOutput)."""
+        tokens, mask, positions, _ = synthetic_gpt_batch(sample_ids, self.cfg.seq_length, self.unpadded_vocab,
+                                                         self.embedding.word_embeddings.weight.device)
+        extra = {} if labels is None else {"labels": labels}
+        out = self.model({"enc_input_ids": tokens, "enc_position_ids": positions}, extra)
+        losses = out["output"]
+        lo = gpt_loss_output(losses, mask, self.nominal)
+        output_tensor = lo.local_loss_sum / lo.nominal_global_loss_scale
+        torch.autograd.backward(self.optimizer.scale_loss(output_tensor))
+        return losses.detach(), lo
+
+    def tie_gradients(self):
+        K.tied_grad_sum(self.embedding.word_embeddings.weight.main_grad, self.post.word_embeddings.weight.main_grad)
+
+    def train_step(self, sample_ids, labels=None):
+        self.ddp.zero_grad_buffer()
+        losses, lo = self.forward_backward(sample_ids, labels)
+        self.grad_sync.execute(global_normalization_scale(self.nominal, lo.local_loss_weight))
+        self.tie_gradients()
+        ok, norm, zeros = self.optimizer.step()
+        return losses, lo, ok, norm

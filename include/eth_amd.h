@@ -224,6 +224,36 @@ int eth_attn_bwd(const eth_attn_desc_t* desc, const void* q, const void* k, cons
                  const void* out, const void* dout, const float* lse, float* delta, void* dq,
                  void* dk, void* dv, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Vocabulary side of the first / last stage.
+ * eth_embedding_fwd: out[s, b, :] = word[tokens[b, s]] + pos[positions[b, s]]
+ *   (tokens/positions int64 [batch, seq]; out [seq, batch, hidden]); replaces
+ *   Embedding_v1.forward (eth/runtime/megatron/model/flex_ops.py:450-485,
+ *   VocabParallelEmbedding mpu/layers.py:136-205 at TP = 1).
+ * eth_embedding_bwd: fp32 dword[tok] += dout, dpos[pos] += dout (atomic).
+ * eth_xent_fwd / eth_xent_bwd: per-row loss = logsumexp(z) - z[label] from
+ *   16-bit logits [rows, ld], saving lse; dz = (softmax - onehot) * dloss.
+ *   Replace vocab_parallel_cross_entropy(logits.float(), labels)
+ *   (mpu/cross_entropy.py:36-115; flex_ops.py:1976-1981).
+ * Out-of-range ids are clamped and flagged in *bad_index (set to 1).
+ * ---------------------------------------------------------------------- */
+int eth_embedding_fwd(const int64_t* tokens, const int64_t* positions, const void* word,
+                      const void* pos, void* out, int64_t batch, int64_t seq, int64_t hidden,
+                      int64_t vocab, int64_t max_pos, int* bad_index, int dtype, void* stream);
+int eth_embedding_bwd(const int64_t* tokens, const int64_t* positions, const void* dout,
+                      float* dword, float* dpos, int64_t batch, int64_t seq, int64_t hidden,
+                      int64_t vocab, int64_t max_pos, int dtype, void* stream);
+int eth_xent_fwd(const void* logits, int64_t ld, const int64_t* labels, float* loss, float* lse,
+                 int64_t rows, int64_t vocab, int* bad_index, int dtype, void* stream);
+int eth_xent_bwd(const void* logits, int64_t ld, const int64_t* labels, const float* lse,
+                 const float* dloss, void* dlogits, int64_t ldd, int64_t rows, int64_t vocab,
+                 int dtype, void* stream);
+
+/* Tied word-embedding gradients on one rank: root = copy = root + copy (fp32,
+ * 16-byte aligned).  Replaces the same-rank branch of
+ * synchronize_shared_weights_grads (eth/runtime/megatron/training.py:489-531). */
+int eth_tied_grad_sum(float* root, float* copy, int64_t n, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -92,3 +92,30 @@ def vocab_cross_entropy(logits, labels):
     flex_ops.py:1976-1981)."""
     z = logits.float()
     return torch.logsumexp(z, dim=-1) - z.gather(-1, labels.unsqueeze(-1)).squeeze(-1)
+
+
+def full_model_fwd_bwd(tokens, positions, loss_mask, params, heads, labels=None, dtype=torch.float64):
+    """Whole GPT on one stage (embedding -> layers -> final LN -> tied LM
+    head -> cross entropy -> masked mean), the way the first+last stage runs
+    it (flex_ops.py:450-485,547-575,1952-1985; grad_sync/loss.py:16-39).
+
+    Returns (per-token loss [b, s], mean masked loss, gradients of the mean
+    masked loss by parameter name, with the word embedding's gradient being
+    the tied sum of its embedding and LM-head uses)."""
+    p = {k: (v.to(dtype).detach().requires_grad_(True) if torch.is_tensor(v) else v) for k, v in params.items()}
+    layers = [{k: v.to(dtype).detach().requires_grad_(True) for k, v in lp.items()} for lp in params["layers"]]
+    head = p["word"].detach().clone().requires_grad_(True)
+    x = (p["word"][tokens] + p["pos"][positions]).transpose(0, 1)  # [s, b, h]
+    for lp in layers:
+        x = transformer_layer(x, lp, heads)
+    hidden = layer_norm(x.transpose(0, 1), p["lnf_w"], p["lnf_b"])  # [b, s, h]
+    logits = hidden @ head.t()
+    if labels is None:
+        labels = torch.zeros(tokens.shape, dtype=torch.long)
+    losses = vocab_cross_entropy(logits, labels).to(dtype)
+    mask = loss_mask.to(dtype)
+    mean = (losses * mask).sum() / mask.sum()
+    mean.backward()
+    grads = {"word": p["word"].grad + head.grad, "pos": p["pos"].grad, "lnf_w": p["lnf_w"].grad, "lnf_b": p["lnf_b"].grad}
+    grads["layers"] = [{k: v.grad for k, v in lp.items()} for lp in layers]
+    return losses.detach(), mean.detach(), grads
