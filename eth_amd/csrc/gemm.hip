@@ -14,11 +14,22 @@
 // way into LDS (4 k-rows x 8 columns per thread), so every LDS tile is stored
 // K-contiguous and each MFMA operand is one 16-byte LDS read.
 //
-// Workgroup: 256 threads = 4 waves in a 2x2 grid; each wave owns a
-// (BM/2) x (BN/2) sub-tile made of 32x32 MFMA blocks.  Tiles are assigned
-// XCD-aware (consecutive workgroups land on different XCDs, so the tile id
-// is remapped to give each XCD a contiguous range) and in GROUP_M-row
-// groups so neighbouring workgroups share A and B tiles in L2.
+// Two kernels:
+//  * gemm256_kernel, the main one: 256x256x64 tiles, 4 waves (one per SIMD)
+//    of 128x128 each, 256 accumulator registers per lane held in AGPRs.  The
+//    k loop is software-pipelined by hand: while the MFMAs of k-tile t run,
+//    the registers holding k-tile t+1 are written to the other LDS stage and
+//    refilled with k-tile t+2, and the fragments of the next k-step are read
+//    from LDS, each spread between MFMA pairs (sched_barrier fixes the
+//    order).  One LDS-only barrier per k-tile.  The epilogue stages each
+//    32-row slab through LDS and writes whole rows with buffer stores.
+//    Needs K % 128 == 0, 16-byte aligned C rows and enough tiles to fill
+//    the chip.
+//  * gemm_kernel, the general fallback: 256x256 (8 waves) or 128x128 (4
+//    waves) tiles, register-staged double buffering, any K % 8 == 0.
+// Tiles are assigned XCD-aware (consecutive workgroups land on different
+// XCDs, so the tile id is remapped to give each XCD a contiguous range) and
+// in GROUP_M-row groups so neighbouring workgroups share A and B tiles in L2.
 //
 // Replaces the F.linear / cuBLAS calls of mpu/layers.py:357-370,452-470 and
 // the main_grad.add_ hook of model/distributed.py:116-123.
@@ -29,6 +40,8 @@ namespace eth {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 template <bool FP16>
 __device__ __forceinline__ f32x16_t mfma32(const uint4& a, const uint4& b, const f32x16_t& c) {
@@ -42,6 +55,18 @@ __device__ __forceinline__ f32x16_t mfma32(const uint4& a, const uint4& b, const
 }
 
 constexpr int kPad = 8;  // LDS row padding (elements): 16 B breaks bank aliasing
+
+// two floats -> packed bf16 pair, round to nearest even (v_cvt_pk_bf16_f32)
+__device__ __forceinline__ uint32_t bf16_pair(float lo, float hi) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)lo) |
+         ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)hi) << 16);
+}
+
+// Workgroup barrier ordering LDS only.  __syncthreads also fences global
+// memory, which makes every wave wait for its outstanding stores.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
 
 // Map a linear workgroup id to (tile_m, tile_n): XCD-contiguous, then
 // GROUP_M-row grouped.
@@ -108,6 +133,23 @@ struct KTile {
       *reinterpret_cast<uint4*>(S + r * (BK + kPad) + kc) = v[i];
     }
   }
+  // whole-tile load when K % BK == 0 (an empty resource reads zeros)
+  __device__ __forceinline__ void fetch(rsrc_t rs, int64_t, int k0) {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) v[i] = buf_load16(rs, off[i], k0 * 2);
+  }
+  // part P of NP: store the staged chunks to LDS, then refill the same
+  // registers with k-tile k0
+  template <int P, int NP>
+  __device__ __forceinline__ void cycle(uint16_t* S, rsrc_t rs, int64_t, int k0) {
+#pragma unroll
+    for (int i = P * CPT / NP; i < (P + 1) * CPT / NP; ++i) {
+      const int c = threadIdx.x + i * NT;
+      const int r = c / CPR, kc = (c % CPR) * 8;
+      *reinterpret_cast<uint4*>(S + r * (BK + kPad) + kc) = v[i];
+      v[i] = buf_load16(rs, off[i], k0 * 2);
+    }
+  }
 };
 
 // BK x ROWS tile of an operand contiguous along the row index (element
@@ -145,30 +187,48 @@ struct RTile {
       }
     }
   }
-  __device__ __forceinline__ void store(uint16_t* S) const { store_part(S, 0, 1); }
-  __device__ __forceinline__ void store_part(uint16_t* S, int part, int parts) const {
+  __device__ __forceinline__ void store(uint16_t* S) const {
 #pragma unroll
-    for (int b = 0; b < BPT; ++b) {
-      const int blk = threadIdx.x + b * NT;
-      const int kg = blk % KG, rg = blk / KG;
-      const uint32_t* w0 = reinterpret_cast<const uint32_t*>(&v[b][0]);
-      const uint32_t* w1 = reinterpret_cast<const uint32_t*>(&v[b][1]);
-      const uint32_t* w2 = reinterpret_cast<const uint32_t*>(&v[b][2]);
-      const uint32_t* w3 = reinterpret_cast<const uint32_t*>(&v[b][3]);
+    for (int b = 0; b < BPT; ++b) store_block(S, b);
+  }
+  __device__ __forceinline__ void fetch(rsrc_t rs, int64_t ld, int k0) {
+    const int32_t soff = (int32_t)((int64_t)k0 * ld * 2);
+    const int32_t row_bytes = (int32_t)(ld * 2);
 #pragma unroll
-      for (int p = 0; p < 4; ++p) {
-        if ((b * 4 + p) * parts / (BPT * 4) != part) continue;
-        // rows 2p and 2p+1 of the 8-row group
-        const uint32_t a0 = w0[p], a1 = w1[p], a2 = w2[p], a3 = w3[p];
-        uint2 lo, hi;
-        lo.x = (a0 & 0xffffu) | (a1 << 16);
-        lo.y = (a2 & 0xffffu) | (a3 << 16);
-        hi.x = (a0 >> 16) | (a1 & 0xffff0000u);
-        hi.y = (a2 >> 16) | (a3 & 0xffff0000u);
-        uint16_t* row = S + (rg * 8 + 2 * p) * (BK + kPad) + kg * 4;
-        *reinterpret_cast<uint2*>(row) = lo;
-        *reinterpret_cast<uint2*>(row + (BK + kPad)) = hi;
-      }
+    for (int b = 0; b < BPT; ++b)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[b][j] = buf_load16(rs, off[b] == kOob ? kOob : off[b] + j * row_bytes, soff);
+  }
+  template <int P, int NP>
+  __device__ __forceinline__ void cycle(uint16_t* S, rsrc_t rs, int64_t ld, int k0) {
+    const int32_t soff = (int32_t)((int64_t)k0 * ld * 2);
+    const int32_t row_bytes = (int32_t)(ld * 2);
+#pragma unroll
+    for (int b = P * BPT / NP; b < (P + 1) * BPT / NP; ++b) {
+      store_block(S, b);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[b][j] = buf_load16(rs, off[b] == kOob ? kOob : off[b] + j * row_bytes, soff);
+    }
+  }
+  __device__ __forceinline__ void store_block(uint16_t* S, int b) const {
+    const int blk = threadIdx.x + b * NT;
+    const int kg = blk % KG, rg = blk / KG;
+    const uint32_t* w0 = reinterpret_cast<const uint32_t*>(&v[b][0]);
+    const uint32_t* w1 = reinterpret_cast<const uint32_t*>(&v[b][1]);
+    const uint32_t* w2 = reinterpret_cast<const uint32_t*>(&v[b][2]);
+    const uint32_t* w3 = reinterpret_cast<const uint32_t*>(&v[b][3]);
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      // rows 2p and 2p+1 of the 8-row group
+      const uint32_t a0 = w0[p], a1 = w1[p], a2 = w2[p], a3 = w3[p];
+      uint2 lo, hi;
+      lo.x = (a0 & 0xffffu) | (a1 << 16);
+      lo.y = (a2 & 0xffffu) | (a3 << 16);
+      hi.x = (a0 >> 16) | (a1 & 0xffff0000u);
+      hi.y = (a2 >> 16) | (a3 & 0xffff0000u);
+      uint16_t* row = S + (rg * 8 + 2 * p) * (BK + kPad) + kg * 4;
+      *reinterpret_cast<uint2*>(row) = lo;
+      *reinterpret_cast<uint2*>(row + (BK + kPad)) = hi;
     }
   }
 };
@@ -191,6 +251,7 @@ struct GemmArgs {
   int c_dtype;
   int flags;
   float alpha;
+  uint32_t c_bytes;  // extent of C (gemm256_kernel's store range)
 };
 
 template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, bool A_K, bool B_K, bool FP16>
@@ -303,6 +364,228 @@ __global__ void __launch_bounds__(64 * WAVES_M * WAVES_N) gemm_kernel(GemmArgs g
   }
 }
 
+// 256x256x64 tiles, 4 waves of 128x128 (one per SIMD), K % 128 == 0.
+template <bool A_K, bool B_K, bool FP16>
+__global__ void __launch_bounds__(256, 1) gemm256_kernel(GemmArgs g) {
+  constexpr int BM = 256, BN = 256, BK = 64, NT = 256, R = BK + kPad;
+  constexpr int STAGE = (BM + BN) * R;  // one LDS stage: A tile then B tile
+  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * STAGE];
+
+  const int tiles_m = (g.M + BM - 1) / BM, tiles_n = (g.N + BN - 1) / BN;
+  int tm, tn;
+  tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int wm = wid >> 1, wn = wid & 1;
+  const int lr = lane & 31, lk = (lane >> 5) * 8;
+  // the 4 output columns this lane writes in the epilogue, and their bias
+  // (read now so its latency is hidden behind the k loop)
+  const int col = (lane & 31) * 4;
+  const int n = n0 + wn * 128 + col;
+  float bn[4] = {0.f, 0.f, 0.f, 0.f};
+  if ((g.flags & ETH_GEMM_BIAS) && g.bias) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (n + e < g.N) bn[e] = FP16 ? h2f_bits(g.bias[n + e]) : bf2f(g.bias[n + e]);
+  }
+
+  f32x16_t acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  const int nk = g.K / BK;
+  const rsrc_t ra = make_rsrc(g.A, g.a_bytes), rb = make_rsrc(g.B, g.b_bytes);
+  // empty ranges: the loads issued past the last k-tile read zeros
+  const rsrc_t ra0 = make_rsrc(g.A, 0), rb0 = make_rsrc(g.B, 0);
+  TileLoader<BM, BK, NT, A_K> la;
+  TileLoader<BN, BK, NT, B_K> lb;
+  la.init(g.lda, m0, g.M);
+  lb.init(g.ldb, n0, g.N);
+  la.fetch(ra, g.lda, 0);
+  lb.fetch(rb, g.ldb, 0);
+  la.store(smem);
+  lb.store(smem + BM * R);
+  la.fetch(ra, g.lda, BK);
+  lb.fetch(rb, g.ldb, BK);
+  __syncthreads();
+
+  // fragment of (row block I, k-step KS): lanes 0-31 hold rows, lanes 32-63
+  // the second 8 k of the 16
+  const int a_frag = (wm * 128 + lr) * R + lk;
+  const int b_frag = BM * R + (wn * 128 + lr) * R + lk;
+  uint4 fa0[4], fb0[4], fa1[4], fb1[4];
+#define SB __builtin_amdgcn_sched_barrier(0);
+#define RD_A(FA, BASE, KS, I) FA[I] = *reinterpret_cast<const uint4*>((BASE) + a_frag + (I) * 32 * R + (KS) * 16);
+#define RD_B(FB, BASE, KS, J) FB[J] = *reinterpret_cast<const uint4*>((BASE) + b_frag + (J) * 32 * R + (KS) * 16);
+// B fragment as the MFMA's first operand: the lane then holds 4 consecutive
+// output columns (r % 4) of one output row (lane % 32)
+#define MMA2(FA, FB, I, J0)                                         \
+  acc[I][J0] = mfma32<FP16>(FB[J0], FA[I], acc[I][J0]);             \
+  acc[I][J0 + 1] = mfma32<FP16>(FB[J0 + 1], FA[I], acc[I][J0 + 1]);
+// next k-step's fragments in the order its MFMA pairs consume them:
+// B0 B1 A0 B2 B3 A1 A2 A3
+#define RD_SEQ0(GA, GB, RB, RK) RD_B(GB, RB, RK, 0)
+#define RD_SEQ1(GA, GB, RB, RK) RD_B(GB, RB, RK, 1)
+#define RD_SEQ2(GA, GB, RB, RK) RD_A(GA, RB, RK, 0)
+#define RD_SEQ3(GA, GB, RB, RK) RD_B(GB, RB, RK, 2)
+#define RD_SEQ4(GA, GB, RB, RK) RD_B(GB, RB, RK, 3)
+#define RD_SEQ5(GA, GB, RB, RK) RD_A(GA, RB, RK, 1)
+#define RD_SEQ6(GA, GB, RB, RK) RD_A(GA, RB, RK, 2)
+#define RD_SEQ7(GA, GB, RB, RK) RD_A(GA, RB, RK, 3)
+// one row block of a k-step: 4 MFMAs on (FA, FB), two fragment reads of the
+// next k-step into (GA, GB) and part I of a tile cycle between them
+#define KSTEP_ROW(FA, FB, GA, GB, RB, RK, I, S0, S1, CYC) \
+  SB MMA2(FA, FB, I, 0) SB S0(GA, GB, RB, RK) SB MMA2(FA, FB, I, 2) SB S1(GA, GB, RB, RK) SB CYC(I)
+#define NOCYC(P)
+#define CYC_A(P) la.template cycle<P, 4>(nxt, rsa, g.lda, k2);
+#define CYC_B(P) lb.template cycle<P, 4>(nxt + BM * R, rsb, g.ldb, k2);
+#define KSTEP(FA, FB, GA, GB, RB, RK, CYC)                     \
+  KSTEP_ROW(FA, FB, GA, GB, RB, RK, 0, RD_SEQ0, RD_SEQ1, CYC) \
+  KSTEP_ROW(FA, FB, GA, GB, RB, RK, 1, RD_SEQ2, RD_SEQ3, CYC) \
+  KSTEP_ROW(FA, FB, GA, GB, RB, RK, 2, RD_SEQ4, RD_SEQ5, CYC) \
+  KSTEP_ROW(FA, FB, GA, GB, RB, RK, 3, RD_SEQ6, RD_SEQ7, CYC) SB
+// k-tile KT: MFMAs from stage CUR; k-tile KT+1 moves from registers into
+// stage NXT (A during k-step 0, B during k-step 1) while k-tile KT+2 is
+// loaded; after k-step 2 every wave is done with CUR and has written NXT,
+// so k-step 3 reads the first fragments of KT+1 from NXT
+#define ITER(CUR, NXT, KT)                              \
+  {                                                     \
+    uint16_t* const cur = (CUR);                        \
+    uint16_t* const nxt = (NXT);                        \
+    const int k2 = ((KT) + 2) * BK;                     \
+    const rsrc_t rsa = (KT) + 2 < nk ? ra : ra0;        \
+    const rsrc_t rsb = (KT) + 2 < nk ? rb : rb0;        \
+    KSTEP(fa0, fb0, fa1, fb1, cur, 1, CYC_A)            \
+    KSTEP(fa1, fb1, fa0, fb0, cur, 2, CYC_B)            \
+    KSTEP(fa0, fb0, fa1, fb1, cur, 3, NOCYC)            \
+    lds_barrier();                                      \
+    KSTEP(fa1, fb1, fa0, fb0, nxt, 0, NOCYC)            \
+  }
+  SB RD_SEQ0(fa0, fb0, smem, 0) SB RD_SEQ1(fa0, fb0, smem, 0) SB RD_SEQ2(fa0, fb0, smem, 0) SB
+  RD_SEQ3(fa0, fb0, smem, 0) SB RD_SEQ4(fa0, fb0, smem, 0) SB RD_SEQ5(fa0, fb0, smem, 0) SB
+  RD_SEQ6(fa0, fb0, smem, 0) SB RD_SEQ7(fa0, fb0, smem, 0) SB
+  // two k-tiles per trip, so both LDS stages have fixed addresses
+  for (int kt = 0; kt < nk; kt += 2) {
+    ITER(smem, smem + STAGE, kt)
+    ITER(smem + STAGE, smem, kt + 1)
+  }
+#undef ITER
+#undef KSTEP
+#undef CYC_A
+#undef CYC_B
+#undef NOCYC
+#undef KSTEP_ROW
+#undef RD_SEQ0
+#undef RD_SEQ1
+#undef RD_SEQ2
+#undef RD_SEQ3
+#undef RD_SEQ4
+#undef RD_SEQ5
+#undef RD_SEQ6
+#undef RD_SEQ7
+#undef MMA2
+#undef RD_A
+#undef RD_B
+#undef SB
+
+  // Epilogue: each wave stages one 32-row slab of its 128x128 block at a
+  // time in its own LDS region (fp32, padded rows) and writes it back as
+  // whole rows, two rows per store instruction.  C goes through a buffer
+  // resource spanning exactly its extent, so rows past M are dropped by the
+  // hardware; lanes whose columns are past N get an out-of-range offset.
+  constexpr int ER = 128 + 4;
+  float* stage = reinterpret_cast<float*>(smem) + wid * 32 * ER;
+  const int esz = g.c_dtype == ETH_F32 ? 4 : 2;
+  const int mode = g.c_dtype == ETH_BF16 ? 0 : g.c_dtype == ETH_F16 ? 1 : (g.flags & ETH_GEMM_ACCUMULATE) ? 3 : 2;
+  const rsrc_t rc = make_rsrc(g.C, g.c_bytes);
+  const int32_t row2 = (int32_t)(2 * g.ldc * esz);
+  auto write_slab = [&](const int i) __attribute__((always_inline)) {
+    // the slab is private to this wave, whose LDS accesses complete in order
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    float4 v[16];
+#pragma unroll
+    for (int it = 0; it < 16; ++it) {
+      v[it] = *reinterpret_cast<const float4*>(stage + (it * 2 + (lane >> 5)) * ER + col);
+      v[it].x = v[it].x * g.alpha + bn[0];
+      v[it].y = v[it].y * g.alpha + bn[1];
+      v[it].z = v[it].z * g.alpha + bn[2];
+      v[it].w = v[it].w * g.alpha + bn[3];
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    const int mrow = m0 + wm * 128 + i * 32 + (lane >> 5);
+    const int32_t voff = n < g.N ? (int32_t)(((int64_t)mrow * g.ldc + n) * esz) : kOob;
+#define OFF(IT) (voff == kOob ? kOob : voff + (IT) * row2)
+    if (mode == 0) {
+#pragma unroll
+      for (int it = 0; it < 16; ++it) {
+        u32x2_t o;
+        o.x = bf16_pair(v[it].x, v[it].y);
+        o.y = bf16_pair(v[it].z, v[it].w);
+        __builtin_amdgcn_raw_buffer_store_b64(o, rc, OFF(it), 0, 0);
+      }
+    } else if (mode == 1) {
+#pragma unroll
+      for (int it = 0; it < 16; ++it) {
+        u32x2_t o;
+        o.x = f2h_bits(v[it].x) | ((uint32_t)f2h_bits(v[it].y) << 16);
+        o.y = f2h_bits(v[it].z) | ((uint32_t)f2h_bits(v[it].w) << 16);
+        __builtin_amdgcn_raw_buffer_store_b64(o, rc, OFF(it), 0, 0);
+      }
+    } else if (mode == 2) {
+#pragma unroll
+      for (int it = 0; it < 16; ++it)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v[it]), rc, OFF(it), 0, 0);
+    } else {
+      // fp32 C += (the main_grad accumulation): all loads first
+      u32x4_t old[16];
+#pragma unroll
+      for (int it = 0; it < 16; ++it) old[it] = __builtin_amdgcn_raw_buffer_load_b128(rc, OFF(it), 0, 0);
+#pragma unroll
+      for (int it = 0; it < 16; ++it) {
+        float4 o = __builtin_bit_cast(float4, old[it]);
+        o.x += v[it].x;
+        o.y += v[it].y;
+        o.z += v[it].z;
+        o.w += v[it].w;
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, o), rc, OFF(it), 0, 0);
+      }
+    }
+#undef OFF
+  };
+  lds_barrier();  // every wave is done with the k-loop stages
+#define STAGE_SLAB(I)                                                                  \
+  {                                                                                    \
+    _Pragma("unroll") for (int j = 0; j < 4; ++j)                                      \
+      _Pragma("unroll") for (int q = 0; q < 4; ++q) {                                  \
+        const float4 o = make_float4(acc[I][j][q * 4 + 0], acc[I][j][q * 4 + 1],       \
+                                     acc[I][j][q * 4 + 2], acc[I][j][q * 4 + 3]);      \
+        *reinterpret_cast<float4*>(stage + lr * ER + j * 32 + q * 8 + (lane >> 5) * 4) = o; \
+      }                                                                                \
+    write_slab(I);                                                                     \
+  }
+  STAGE_SLAB(0) STAGE_SLAB(1) STAGE_SLAB(2) STAGE_SLAB(3)
+#undef STAGE_SLAB
+}
+
+template <bool FP16>
+static int launch_256(const GemmArgs& a, int a_k, int b_k, hipStream_t s) {
+  const int tiles = ((a.M + 255) / 256) * ((a.N + 255) / 256);
+  if (a_k && b_k)
+    gemm256_kernel<true, true, FP16><<<tiles, 256, 0, s>>>(a);
+  else if (a_k && !b_k)
+    gemm256_kernel<true, false, FP16><<<tiles, 256, 0, s>>>(a);
+  else if (!a_k && !b_k)
+    gemm256_kernel<false, false, FP16><<<tiles, 256, 0, s>>>(a);
+  else
+    gemm256_kernel<false, true, FP16><<<tiles, 256, 0, s>>>(a);
+  ETH_CHECK_LAUNCH("eth_gemm");
+  return ETH_OK;
+}
+
 template <int BM, int BN, int BK, int WMW, int WNW, bool FP16>
 static int launch_layout(const GemmArgs& a, int a_k, int b_k, hipStream_t s) {
   const int tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
@@ -362,9 +645,21 @@ extern "C" int eth_gemm(const void* A, int64_t lda, int a_kcontig, const void* B
   a.flags = flags;
   a.alpha = alpha;
   hipStream_t s = (hipStream_t)stream;
-  // 256x256 tiles (8 waves of 128x64) when the grid still fills the chip,
-  // 128x128 (4 waves of 64x64) otherwise
   const int64_t big_tiles = ((M + 255) / 256) * ((N + 255) / 256);
+  // the pipelined 256x256 kernel: K in whole k-tile pairs, C rows 16-byte
+  // aligned (vector stores), C extent plus one tile of rows below 2 GiB (its
+  // buffer offsets), and at least half a wave of tiles per chip
+  const int esz = c_dtype == ETH_F32 ? 4 : 2;
+  const int64_t c_extent = ((M - 1) * ldc + N) * esz;
+  const bool c_vec = ldc % 4 == 0 && N % 4 == 0 && ((uintptr_t)C % (4 * esz)) == 0;
+  if (K % 128 == 0 && c_vec && big_tiles >= 128 && c_extent + 256 * ldc * esz < (1LL << 31)) {
+    a.c_bytes = (uint32_t)c_extent;
+    return in_dtype == ETH_BF16 ? launch_256<false>(a, a_kcontig, b_kcontig, s)
+                                : launch_256<true>(a, a_kcontig, b_kcontig, s);
+  }
+  a.c_bytes = 0;
+  // otherwise 256x256 tiles (8 waves of 128x64) when the grid still fills
+  // the chip, 128x128 (4 waves of 64x64) below that
   const bool big = big_tiles >= 192;
   if (in_dtype == ETH_BF16)
     return big ? launch_layout<256, 256, 64, 2, 4, false>(a, a_kcontig, b_kcontig, s)

@@ -60,6 +60,33 @@ def test_gemm_three_layouts(cuda, dtype, M, N, Kd):
     _close(z, x.float() @ w.float().t(), dtype, "A col-major")
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("a_k,b_k", [(True, True), (True, False), (False, False), (False, True)])
+def test_gemm_pipelined_kernel_layouts(cuda, dtype, a_k, b_k):
+    """Shapes that take the 256x256 pipelined kernel (>= 128 tiles of 256,
+    K % 128 == 0) with ragged M and N: every operand layout, 16-bit output
+    with bias, fp32 output, and fp32 accumulation with alpha."""
+    M, N, Kd = 4000, 2056, 384  # 16 x 9 tiles, last row and column tiles partial
+    announce(f"gemm256 {dtype} a_k={a_k} b_k={b_k} {M}x{N}x{Kd}")
+    gen = torch.Generator().manual_seed(17 + 2 * a_k + b_k)
+    a = _rand((M, Kd), dtype, gen)
+    b = _rand((Kd, N), dtype, gen, 0.05)
+    bias = _rand((N,), dtype, gen)
+    ad = a.to(cuda) if a_k else a.t().contiguous().to(cuda).t()
+    bd = b.t().contiguous().to(cuda).t() if b_k else b.to(cuda)
+    ref = a.float() @ b.float()
+    y = K.gemm(ad, bd, bias=bias.to(cuda))
+    _close(y, ref + bias.float(), dtype, "16-bit out + bias")
+    y32 = K.gemm(ad, bd, out_dtype=torch.float32)
+    err = (y32.cpu() - ref).abs().max().item()
+    assert err <= 1e-4 * ref.abs().max().item(), f"fp32 out err {err}"
+    acc = torch.full((M, N), 0.25, dtype=torch.float32, device=cuda)
+    K.gemm(ad, bd, out=acc, accumulate=True, alpha=0.5)
+    ref2 = 0.25 + 0.5 * ref
+    err = (acc.cpu() - ref2).abs().max().item()
+    assert err <= 1e-4 * ref2.abs().max().item(), f"accumulate err {err}"
+
+
 def test_gemm_rejects_bad_shapes(cuda):
     a = torch.zeros(16, 12, dtype=torch.bfloat16, device=cuda)
     b = torch.zeros(12, 16, dtype=torch.bfloat16, device=cuda)
