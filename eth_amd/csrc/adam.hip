@@ -86,8 +86,8 @@ __global__ void __launch_bounds__(kAdamThreads) adam_kernel(const eth_adam_tenso
       if (MODEL_DT != ETH_F32 && out) {
         uint2 o;
         if (MODEL_DT == ETH_BF16) {
-          o.x = (uint32_t)f2bf(pp.x) | ((uint32_t)f2bf(pp.y) << 16);
-          o.y = (uint32_t)f2bf(pp.z) | ((uint32_t)f2bf(pp.w) << 16);
+          o.x = f2bf_pair(pp.x, pp.y);
+          o.y = f2bf_pair(pp.z, pp.w);
         } else {
           o.x = (uint32_t)f2h_bits(pp.x) | ((uint32_t)f2h_bits(pp.y) << 16);
           o.y = (uint32_t)f2h_bits(pp.z) | ((uint32_t)f2h_bits(pp.w) << 16);

@@ -26,6 +26,7 @@ namespace eth {
 typedef __bf16 a_bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 a_f16x8 __attribute__((ext_vector_type(8)));
 typedef float a_f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t a_u32x4 __attribute__((ext_vector_type(4)));
 
 template <bool FP16>
 __device__ __forceinline__ a_f32x16 mma(const uint4& a, const uint4& b, const a_f32x16& c) {
@@ -47,8 +48,12 @@ __device__ __forceinline__ uint16_t from_f(float v) {
 }
 template <bool FP16>
 __device__ __forceinline__ uint32_t pack2(float a, float b) {
-  return (uint32_t)from_f<FP16>(a) | ((uint32_t)from_f<FP16>(b) << 16);
+  if constexpr (FP16)
+    return (uint32_t)f2h_bits(a) | ((uint32_t)f2h_bits(b) << 16);
+  else
+    return f2bf_pair(a, b);
 }
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 // 8 fp32 -> one 16-byte MFMA operand
 template <bool FP16>
 __device__ __forceinline__ uint4 pack8(const float* v) {
@@ -103,12 +108,12 @@ struct RowTile {
   static constexpr int CPR = D / 8;
   static constexpr int CPT = ROWS * CPR / kAttnThreads;
   static_assert(ROWS * CPR % kAttnThreads == 0 && CPT >= 1, "tile split");
-  uint4 v[CPT];
+  a_u32x4 v[CPT];  // native vectors: plain loads/stores, no struct copies
   __device__ __forceinline__ void load(const AttnTensor& t, int r0, int b, int h) {
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
       const int c = threadIdx.x + i * kAttnThreads;
-      v[i] = *reinterpret_cast<const uint4*>(row_ptr(t, r0 + c / CPR, b, h) + (c % CPR) * 8);
+      v[i] = *reinterpret_cast<const a_u32x4*>(row_ptr(t, r0 + c / CPR, b, h) + (c % CPR) * 8);
     }
   }
   template <bool SWZ>
@@ -117,10 +122,11 @@ struct RowTile {
     for (int i = 0; i < CPT; ++i) {
       const int c = threadIdx.x + i * kAttnThreads;
       const int r = SWZ ? swz(c / CPR) : c / CPR;
-      *reinterpret_cast<uint4*>(lds + r * (D + 8) + (c % CPR) * 8) = v[i];
+      *reinterpret_cast<a_u32x4*>(lds + r * (D + 8) + (c % CPR) * 8) = v[i];
     }
   }
 };
+
 
 // ROWS x D tile stored transposed into LDS [D][ROWS+8] (natural row order).
 // The 4-row group index varies fastest across lanes, so a wavefront's 8-byte
@@ -131,35 +137,32 @@ struct ColTile {
   static constexpr int NB = DG * RG;
   static constexpr int BPT = (NB + kAttnThreads - 1) / kAttnThreads;
   static_assert(NB % kAttnThreads == 0 || NB < kAttnThreads, "tile split");
-  uint4 v[BPT][4];
+  a_u32x4 v[BPT][4];  // element vectors: word p of row j is v[i][j][p]
   __device__ __forceinline__ void load(const AttnTensor& t, int r0, int b, int h) {
 #pragma unroll
     for (int i = 0; i < BPT; ++i) {
       const int blk = threadIdx.x + i * kAttnThreads;
-      if (blk >= NB) break;
+      if (NB % kAttnThreads != 0 && blk >= NB) break;
       const int rg = blk % RG, dg = blk / RG;
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        v[i][j] = *reinterpret_cast<const uint4*>(row_ptr(t, r0 + rg * 4 + j, b, h) + dg * 8);
+        v[i][j] = *reinterpret_cast<const a_u32x4*>(row_ptr(t, r0 + rg * 4 + j, b, h) + dg * 8);
     }
   }
   __device__ __forceinline__ void store(uint16_t* lds) const {
 #pragma unroll
     for (int i = 0; i < BPT; ++i) {
       const int blk = threadIdx.x + i * kAttnThreads;
-      if (blk >= NB) break;
+      if (NB % kAttnThreads != 0 && blk >= NB) break;
       const int rg = blk % RG, dg = blk / RG;
-      const uint32_t* w0 = reinterpret_cast<const uint32_t*>(&v[i][0]);
-      const uint32_t* w1 = reinterpret_cast<const uint32_t*>(&v[i][1]);
-      const uint32_t* w2 = reinterpret_cast<const uint32_t*>(&v[i][2]);
-      const uint32_t* w3 = reinterpret_cast<const uint32_t*>(&v[i][3]);
 #pragma unroll
       for (int p = 0; p < 4; ++p) {
+        const uint32_t w0 = v[i][0][p], w1 = v[i][1][p], w2 = v[i][2][p], w3 = v[i][3][p];
         uint2 lo, hi;
-        lo.x = (w0[p] & 0xffffu) | (w1[p] << 16);
-        lo.y = (w2[p] & 0xffffu) | (w3[p] << 16);
-        hi.x = (w0[p] >> 16) | (w1[p] & 0xffff0000u);
-        hi.y = (w2[p] >> 16) | (w3[p] & 0xffff0000u);
+        lo.x = (w0 & 0xffffu) | (w1 << 16);
+        lo.y = (w2 & 0xffffu) | (w3 << 16);
+        hi.x = (w0 >> 16) | (w1 & 0xffff0000u);
+        hi.y = (w2 >> 16) | (w3 & 0xffff0000u);
         uint16_t* row = lds + (dg * 8 + 2 * p) * (ROWS + 8) + rg * 4;
         *reinterpret_cast<uint2*>(row) = lo;
         *reinterpret_cast<uint2*>(row + (ROWS + 8)) = hi;
@@ -169,8 +172,11 @@ struct ColTile {
 };
 
 // ------------------------------------------------------------------ forward --
+// 4 waves x 32 queries; K/V blocks of 64 keys double-buffered in LDS (the
+// next block's global loads are in flight while this one is computed); two
+// workgroups per CU, so one wave's softmax overlaps the other's MFMAs.
 template <int D, bool FP16>
-__global__ void __launch_bounds__(kAttnThreads) attn_fwd_kernel(AttnArgs a) {
+__global__ void __launch_bounds__(kAttnThreads, 2) attn_fwd_kernel(AttnArgs a) {
   constexpr int KS = D / 16;  // k-steps over the head dim
   constexpr int DT = D / 32;  // 32-row tiles over the head dim
   __shared__ __attribute__((aligned(16))) uint16_t Ks[2][kBKV * (D + 8)];
@@ -182,6 +188,7 @@ __global__ void __launch_bounds__(kAttnThreads) attn_fwd_kernel(AttnArgs a) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, hl = lane >> 5;
   const int q0 = qb * kBQ + w * 32;
   const int q = q0 + (lane & 31);
+  const float sl2 = a.scale_log2;
 
   uint4 qf[KS];
   {
@@ -194,7 +201,7 @@ __global__ void __launch_bounds__(kAttnThreads) attn_fwd_kernel(AttnArgs a) {
   for (int t = 0; t < DT; ++t)
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[t][r] = 0.f;
-  float m = -1e30f, l = 0.f;
+  float m = -1e30f, l = 0.f;  // running max (log2 units) and sum for query q
 
   const int nkv = (qb * kBQ + kBQ) / kBKV;  // blocks up to the diagonal
   RowTile<kBKV, D> kt;
@@ -214,6 +221,7 @@ __global__ void __launch_bounds__(kAttnThreads) attn_fwd_kernel(AttnArgs a) {
     }
     const int kv0 = j * kBKV;
     if (kv0 <= q0 + 31) {  // wave has at least one unmasked key in the block
+      // S^T = K Q^T (raw scores; lane = query, registers = 32 of the keys)
       a_f32x16 s[2];
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
@@ -224,46 +232,49 @@ __global__ void __launch_bounds__(kAttnThreads) attn_fwd_kernel(AttnArgs a) {
         for (int ks = 0; ks < KS; ++ks)
           s[t] = mma<FP16>(*reinterpret_cast<const uint4*>(kp + ks * 16), qf[ks], s[t]);
       }
-      const bool diag = kv0 + kBKV - 1 > q0;
-      float mx = -1e30f;
+      if (kv0 + kBKV - 1 > q0) {  // diagonal block: mask keys after the query
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            if (kv0 + t * 32 + swz_row(r, hl) > q) s[t][r] = -1e30f;
+      }
+      float mx = s[0][0];
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          float v = s[t][r] * a.scale_log2;
-          if (diag && kv0 + t * 32 + swz_row(r, hl) > q) v = -1e30f;
-          s[t][r] = v;
-          mx = fmaxf(mx, v);
-        }
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[t][r]);
       mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float mnew = fmaxf(m, mx);
-      const float alpha = exp2f(m - mnew);
-      m = mnew;
+      const float mnew = fmaxf(m, mx * sl2);
+      if (__any(mnew != m)) {  // rescale only when some running max moved
+        const float alpha = fast_exp2(m - mnew);
+        l *= alpha;
+#pragma unroll
+        for (int t = 0; t < DT; ++t)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o[t][r] *= alpha;
+        m = mnew;
+      }
       float rs = 0.f;
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const float p = exp2f(s[t][r] - m);
+          const float p = fast_exp2(__builtin_fmaf(s[t][r], sl2, -m));
           s[t][r] = p;
           rs += p;
         }
-      l = l * alpha + rs;
-#pragma unroll
-      for (int t = 0; t < DT; ++t)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o[t][r] *= alpha;
+      l += rs;
       // O^T += V^T P^T over the 64 keys (4 k-steps of 16)
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
-        float pv[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) pv[e] = s[kk >> 1][(kk & 1) * 8 + e];
-        const uint4 pb = pack8<FP16>(pv);
+        const int t = kk >> 1, e0 = (kk & 1) * 8;
+        const uint4 pb = make_uint4(pack2<FP16>(s[t][e0 + 0], s[t][e0 + 1]), pack2<FP16>(s[t][e0 + 2], s[t][e0 + 3]),
+                                    pack2<FP16>(s[t][e0 + 4], s[t][e0 + 5]), pack2<FP16>(s[t][e0 + 6], s[t][e0 + 7]));
         const uint16_t* vp = Vt[st] + (lane & 31) * (kBKV + 8) + kk * 16 + hl * 8;
 #pragma unroll
-        for (int t = 0; t < DT; ++t)
-          o[t] = mma<FP16>(*reinterpret_cast<const uint4*>(vp + t * 32 * (kBKV + 8)), pb, o[t]);
+        for (int dt = 0; dt < DT; ++dt)
+          o[dt] = mma<FP16>(*reinterpret_cast<const uint4*>(vp + dt * 32 * (kBKV + 8)), pb, o[dt]);
       }
     }
     if (more) {
@@ -311,7 +322,7 @@ __global__ void __launch_bounds__(kAttnThreads) attn_bwd_delta_kernel(AttnArgs a
 
 // ------------------------------------------------------- backward: dK, dV --
 template <int D, bool FP16>
-__global__ void __launch_bounds__(kAttnThreads) attn_bwd_dkdv_kernel(AttnArgs a) {
+__global__ void __launch_bounds__(kAttnThreads, D == 64 ? 2 : 1) attn_bwd_dkdv_kernel(AttnArgs a) {
   constexpr int KS = D / 16, DT = D / 32;
   __shared__ __attribute__((aligned(16))) uint16_t Qs[kBQ2 * (D + 8)];
   __shared__ __attribute__((aligned(16))) uint16_t dOs[kBQ2 * (D + 8)];
@@ -347,14 +358,18 @@ __global__ void __launch_bounds__(kAttnThreads) attn_bwd_dkdv_kernel(AttnArgs a)
   const int first = (kb * kBKV2) / kBQ2, nq = a.S / kBQ2;
   for (int qb = first; qb < nq; ++qb) {
     const int qs0 = qb * kBQ2;
+    // tiles are staged one at a time (few registers live beside dK, dV, K, V)
     qrow.load(a.q, qs0, b, h);
-    drow.load(a.dout, qs0, b, h);
-    qcol.load(a.q, qs0, b, h);
-    dcol.load(a.dout, qs0, b, h);
     __syncthreads();  // previous step's LDS readers are done
     qrow.template store<true>(Qs);
+    __builtin_amdgcn_sched_barrier(0);
+    drow.load(a.dout, qs0, b, h);
     drow.template store<true>(dOs);
+    __builtin_amdgcn_sched_barrier(0);
+    qcol.load(a.q, qs0, b, h);
     qcol.store(Qt);
+    __builtin_amdgcn_sched_barrier(0);
+    dcol.load(a.dout, qs0, b, h);
     dcol.store(dOt);
     if (threadIdx.x < kBQ2) {
       lse_s[threadIdx.x] = a.lse[(int64_t)bh * a.S + qs0 + threadIdx.x];
@@ -363,47 +378,43 @@ __global__ void __launch_bounds__(kAttnThreads) attn_bwd_dkdv_kernel(AttnArgs a)
     __syncthreads();
     if (qs0 + kBQ2 - 1 < k0) continue;  // every query of the step precedes this wave's keys
     const bool diag = qs0 < k0 + 31;
-    // S = Q K^T and dP = dO V^T: 2 query tiles of 32, lane = key
-    a_f32x16 s[2], dp[2];
+    // one 32-query tile at a time: S = Q K^T and dP = dO V^T (lane = key),
+    // then dV += P^T dO and dK += dS^T Q over those 32 queries
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
+      a_f32x16 s, dp;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) s[t][r] = dp[t][r] = 0.f;
+      for (int r = 0; r < 16; ++r) s[r] = dp[r] = 0.f;
       const uint16_t* qp = Qs + (t * 32 + (lane & 31)) * (D + 8) + hl * 8;
       const uint16_t* op = dOs + (t * 32 + (lane & 31)) * (D + 8) + hl * 8;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        s[t] = mma<FP16>(*reinterpret_cast<const uint4*>(qp + ks * 16), kf[ks], s[t]);
-        dp[t] = mma<FP16>(*reinterpret_cast<const uint4*>(op + ks * 16), vf[ks], dp[t]);
+        s = mma<FP16>(*reinterpret_cast<const uint4*>(qp + ks * 16), kf[ks], s);
+        dp = mma<FP16>(*reinterpret_cast<const uint4*>(op + ks * 16), vf[ks], dp);
       }
-    }
-    // P and dS (fp32), query index of register r = t*32 + swz_row(r, hl)
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
+      // P and dS (fp32); query index of register r = t*32 + swz_row(r, hl)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int qi = t * 32 + swz_row(r, hl);
-        float p = exp2f(s[t][r] * a.scale_log2 - lse_s[qi]);
+        float p = fast_exp2(__builtin_fmaf(s[r], a.scale_log2, -lse_s[qi]));
         if (diag && key > qs0 + qi) p = 0.f;
-        s[t][r] = p;
-        dp[t][r] = p * (dp[t][r] - del_s[qi]);
+        s[r] = p;
+        dp[r] = p * (dp[r] - del_s[qi]);
       }
-    // dV += P^T dO, dK += dS^T Q: k-steps over 16 queries
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      float pv[8], sv[8];
+      for (int k2 = 0; k2 < 2; ++k2) {
+        const int kk = t * 2 + k2, e0 = k2 * 8;
+        const uint4 pa = make_uint4(pack2<FP16>(s[e0 + 0], s[e0 + 1]), pack2<FP16>(s[e0 + 2], s[e0 + 3]),
+                                    pack2<FP16>(s[e0 + 4], s[e0 + 5]), pack2<FP16>(s[e0 + 6], s[e0 + 7]));
+        const uint4 sa = make_uint4(pack2<FP16>(dp[e0 + 0], dp[e0 + 1]), pack2<FP16>(dp[e0 + 2], dp[e0 + 3]),
+                                    pack2<FP16>(dp[e0 + 4], dp[e0 + 5]), pack2<FP16>(dp[e0 + 6], dp[e0 + 7]));
+        const uint16_t* dop = dOt + (lane & 31) * (kBQ2 + 8) + kk * 16 + hl * 8;
+        const uint16_t* qtp = Qt + (lane & 31) * (kBQ2 + 8) + kk * 16 + hl * 8;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        pv[e] = s[kk >> 1][(kk & 1) * 8 + e];
-        sv[e] = dp[kk >> 1][(kk & 1) * 8 + e];
-      }
-      const uint4 pa = pack8<FP16>(pv), sa = pack8<FP16>(sv);
-      const uint16_t* dop = dOt + (lane & 31) * (kBQ2 + 8) + kk * 16 + hl * 8;
-      const uint16_t* qtp = Qt + (lane & 31) * (kBQ2 + 8) + kk * 16 + hl * 8;
-#pragma unroll
-      for (int t = 0; t < DT; ++t) {
-        dv[t] = mma<FP16>(pa, *reinterpret_cast<const uint4*>(dop + t * 32 * (kBQ2 + 8)), dv[t]);
-        dk[t] = mma<FP16>(sa, *reinterpret_cast<const uint4*>(qtp + t * 32 * (kBQ2 + 8)), dk[t]);
+        for (int dt = 0; dt < DT; ++dt) {
+          dv[dt] = mma<FP16>(pa, *reinterpret_cast<const uint4*>(dop + dt * 32 * (kBQ2 + 8)), dv[dt]);
+          dk[dt] = mma<FP16>(sa, *reinterpret_cast<const uint4*>(qtp + dt * 32 * (kBQ2 + 8)), dk[dt]);
+        }
       }
     }
   }
@@ -421,7 +432,7 @@ __global__ void __launch_bounds__(kAttnThreads) attn_bwd_dkdv_kernel(AttnArgs a)
 
 // ------------------------------------------------------------ backward: dQ --
 template <int D, bool FP16>
-__global__ void __launch_bounds__(kAttnThreads) attn_bwd_dq_kernel(AttnArgs a) {
+__global__ void __launch_bounds__(kAttnThreads, 2) attn_bwd_dq_kernel(AttnArgs a) {
   constexpr int KS = D / 16, DT = D / 32;
   __shared__ __attribute__((aligned(16))) uint16_t Ks[kBKV * (D + 8)];
   __shared__ __attribute__((aligned(16))) uint16_t Vs[kBKV * (D + 8)];
@@ -467,38 +478,36 @@ __global__ void __launch_bounds__(kAttnThreads) attn_bwd_dq_kernel(AttnArgs a) {
     __syncthreads();
     if (kv0 > q0 + 31) continue;
     const bool diag = kv0 + kBKV - 1 > q0;
-    a_f32x16 s[2], dp[2];
+    // one 32-key tile at a time: S^T = K Q^T, dP^T = V dO^T (lane = query),
+    // dS^T, then dQ^T += K^T dS^T over those 32 keys
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
+      a_f32x16 s, dp;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) s[t][r] = dp[t][r] = 0.f;
+      for (int r = 0; r < 16; ++r) s[r] = dp[r] = 0.f;
       const uint16_t* kp = Ks + (t * 32 + (lane & 31)) * (D + 8) + hl * 8;
       const uint16_t* vp = Vs + (t * 32 + (lane & 31)) * (D + 8) + hl * 8;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        s[t] = mma<FP16>(*reinterpret_cast<const uint4*>(kp + ks * 16), qf[ks], s[t]);
-        dp[t] = mma<FP16>(*reinterpret_cast<const uint4*>(vp + ks * 16), of[ks], dp[t]);
+        s = mma<FP16>(*reinterpret_cast<const uint4*>(kp + ks * 16), qf[ks], s);
+        dp = mma<FP16>(*reinterpret_cast<const uint4*>(vp + ks * 16), of[ks], dp);
       }
-    }
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        float p = exp2f(s[t][r] * a.scale_log2 - lse);
+        float p = fast_exp2(__builtin_fmaf(s[r], a.scale_log2, -lse));
         if (diag && kv0 + t * 32 + swz_row(r, hl) > q) p = 0.f;
-        dp[t][r] = p * (dp[t][r] - del);
+        dp[r] = p * (dp[r] - del);
       }
-    // dQ^T += K^T dS^T
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      float sv[8];
+      for (int k2 = 0; k2 < 2; ++k2) {
+        const int kk = t * 2 + k2, e0 = k2 * 8;
+        const uint4 sb = make_uint4(pack2<FP16>(dp[e0 + 0], dp[e0 + 1]), pack2<FP16>(dp[e0 + 2], dp[e0 + 3]),
+                                    pack2<FP16>(dp[e0 + 4], dp[e0 + 5]), pack2<FP16>(dp[e0 + 6], dp[e0 + 7]));
+        const uint16_t* ktp = Kt + (lane & 31) * (kBKV + 8) + kk * 16 + hl * 8;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) sv[e] = dp[kk >> 1][(kk & 1) * 8 + e];
-      const uint4 sb = pack8<FP16>(sv);
-      const uint16_t* kp = Kt + (lane & 31) * (kBKV + 8) + kk * 16 + hl * 8;
-#pragma unroll
-      for (int t = 0; t < DT; ++t)
-        dq[t] = mma<FP16>(*reinterpret_cast<const uint4*>(kp + t * 32 * (kBKV + 8)), sb, dq[t]);
+        for (int dt = 0; dt < DT; ++dt)
+          dq[dt] = mma<FP16>(*reinterpret_cast<const uint4*>(ktp + dt * 32 * (kBKV + 8)), sb, dq[dt]);
+      }
     }
   }
   uint16_t* dqp = row_ptr(a.dq, q, b, h);

@@ -37,12 +37,17 @@ void set_error(const char* fmt, ...);
 typedef uint16_t bf16_t;
 typedef _Float16 f16_t;
 
-// float -> bfloat16, round to nearest even; NaN stays a quiet NaN.
+// float -> bfloat16, round to nearest even (v_cvt_pk_bf16_f32; denormals are
+// kept, NaN stays NaN).
 __device__ __forceinline__ bf16_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (bf16_t)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (bf16_t)(u >> 16);
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
+}
+// two floats -> packed bf16 pair (lo in bits 0-15), one conversion instruction
+typedef float eth_f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 eth_bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t f2bf_pair(float lo, float hi) {
+  const eth_f32x2_t v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, eth_bf16x2_t));
 }
 __device__ __forceinline__ float bf2f(bf16_t h) {
   return __uint_as_float(((uint32_t)h) << 16);

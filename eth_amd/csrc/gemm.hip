@@ -56,12 +56,6 @@ __device__ __forceinline__ f32x16_t mfma32(const uint4& a, const uint4& b, const
 
 constexpr int kPad = 8;  // LDS row padding (elements): 16 B breaks bank aliasing
 
-// two floats -> packed bf16 pair, round to nearest even (v_cvt_pk_bf16_f32)
-__device__ __forceinline__ uint32_t bf16_pair(float lo, float hi) {
-  return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)lo) |
-         ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)hi) << 16);
-}
-
 // Workgroup barrier ordering LDS only.  __syncthreads also fences global
 // memory, which makes every wave wait for its outstanding stores.
 __device__ __forceinline__ void lds_barrier() {
@@ -523,8 +517,8 @@ __global__ void __launch_bounds__(256, 1) gemm256_kernel(GemmArgs g) {
 #pragma unroll
       for (int it = 0; it < 16; ++it) {
         u32x2_t o;
-        o.x = bf16_pair(v[it].x, v[it].y);
-        o.y = bf16_pair(v[it].z, v[it].w);
+        o.x = f2bf_pair(v[it].x, v[it].y);
+        o.y = f2bf_pair(v[it].z, v[it].w);
         __builtin_amdgcn_raw_buffer_store_b64(o, rc, OFF(it), 0, 0);
       }
     } else if (mode == 1) {
