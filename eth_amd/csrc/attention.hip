@@ -18,7 +18,8 @@
 // O^T = V^T P^T, so P never leaves registers.  The dK/dV kernel uses the
 // mirror image (S = Q K^T, lane = key, query rows swizzled); dQ has its own
 // kernel (recomputing P), so no atomics are needed and results are
-// deterministic.  Softmax runs in fp32 base-2 (exp2) with the scale folded.
+// deterministic.  The dQ kernel runs first and also writes
+// delta = rowsum(dO * O), which the dK/dV kernel reads.  Softmax runs in fp32 base-2 (exp2) with the scale folded.
 #include "common.h"
 
 namespace eth {
@@ -298,28 +299,6 @@ __global__ void __launch_bounds__(kAttnThreads, 2) attn_fwd_kernel(AttnArgs a) {
   if (hl == 0) a.lse[(int64_t)bh * a.S + q] = m + log2f(l);
 }
 
-// --------------------------------------------------------- backward: delta --
-template <int D, bool FP16>
-__global__ void __launch_bounds__(kAttnThreads) attn_bwd_delta_kernel(AttnArgs a) {
-  // one wavefront per (bh, query) row; lanes split the head dim
-  const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= (int64_t)a.B * a.H * a.S) return;
-  const int bh = (int)(row / a.S), qi = (int)(row % a.S);
-  const int b = bh / a.H, h = bh % a.H;
-  float acc = 0.f;
-  if (lane < D / 8) {
-    uint4 x = *reinterpret_cast<const uint4*>(row_ptr(a.o, qi, b, h) + lane * 8);
-    uint4 y = *reinterpret_cast<const uint4*>(row_ptr(a.dout, qi, b, h) + lane * 8);
-    const uint16_t* xe = reinterpret_cast<const uint16_t*>(&x);
-    const uint16_t* ye = reinterpret_cast<const uint16_t*>(&y);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc += to_f<FP16>(xe[e]) * to_f<FP16>(ye[e]);
-  }
-  acc = wave_sum(acc);
-  if (lane == 0) a.delta[row] = acc;
-}
-
 // ------------------------------------------------------- backward: dK, dV --
 template <int D, bool FP16>
 __global__ void __launch_bounds__(kAttnThreads, D == 64 ? 2 : 1) attn_bwd_dkdv_kernel(AttnArgs a) {
@@ -456,7 +435,26 @@ __global__ void __launch_bounds__(kAttnThreads, 2) attn_bwd_dq_kernel(AttnArgs a
     }
   }
   const float lse = a.lse[(int64_t)bh * a.S + q];
-  const float del = a.delta[(int64_t)bh * a.S + q];
+  // delta = rowsum(dO * O) for this query, from the dO fragments already in
+  // registers (the two half-waves hold alternate 8-element chunks of the row);
+  // written out for the dK/dV kernel, which runs next
+  float del = 0.f;
+  {
+    const uint16_t* opp = row_ptr(a.o, q, b, h) + hl * 8;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const uint4 ov = *reinterpret_cast<const uint4*>(opp + ks * 16);
+      const uint32_t ow[4] = {ov.x, ov.y, ov.z, ov.w};
+      const uint32_t dw[4] = {of[ks].x, of[ks].y, of[ks].z, of[ks].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        del += to_f<FP16>((uint16_t)(ow[e] & 0xffffu)) * to_f<FP16>((uint16_t)(dw[e] & 0xffffu));
+        del += to_f<FP16>((uint16_t)(ow[e] >> 16)) * to_f<FP16>((uint16_t)(dw[e] >> 16));
+      }
+    }
+    del += __shfl_xor(del, 32, 64);
+    if (hl == 0) a.delta[(int64_t)bh * a.S + q] = del;
+  }
   a_f32x16 dq[DT];
 #pragma unroll
   for (int t = 0; t < DT; ++t)
@@ -618,14 +616,12 @@ extern "C" int eth_attn_bwd(const eth_attn_desc_t* d, const void* q, const void*
   a.scale_log2 = a.scale * 1.4426950408889634f;
   hipStream_t s = (hipStream_t)stream;
   const bool fp16 = d->dtype == ETH_F16;
-  const int rows = a.B * a.H * a.S;
-  const int g_delta = (rows + 3) / 4;
   const int g_kv = a.B * a.H * (a.S / kBKV2);
   const int g_q = a.B * a.H * (a.S / kBQ);
+  // dQ first: it also writes delta = rowsum(dO * O), which dK/dV reads
 #define ETH_ATTN_BWD(D, F)                                                       \
-  attn_bwd_delta_kernel<D, F><<<g_delta, kAttnThreads, 0, s>>>(a);              \
-  attn_bwd_dkdv_kernel<D, F><<<g_kv, kAttnThreads, 0, s>>>(a);                  \
-  attn_bwd_dq_kernel<D, F><<<g_q, kAttnThreads, 0, s>>>(a);
+  attn_bwd_dq_kernel<D, F><<<g_q, kAttnThreads, 0, s>>>(a);                    \
+  attn_bwd_dkdv_kernel<D, F><<<g_kv, kAttnThreads, 0, s>>>(a);
   if (d->head_dim == 128) {
     if (fp16) { ETH_ATTN_BWD(128, true) } else { ETH_ATTN_BWD(128, false) }
   } else {
