@@ -300,13 +300,17 @@ __global__ void __launch_bounds__(kAttnThreads, 2) attn_fwd_kernel(AttnArgs a) {
 }
 
 // ------------------------------------------------------- backward: dK, dV --
-template <int D, bool FP16>
-__global__ void __launch_bounds__(kAttnThreads, D == 64 ? 2 : 1) attn_bwd_dkdv_kernel(AttnArgs a) {
+// PART 1: dV only, 2: dK only, 3: both.  Split, each part fits two
+// workgroups per CU (the fused kernel needs K, V fragments and both
+// accumulators live and runs one); splitting recomputes S once more.
+template <int D, bool FP16, int PART>
+__global__ void __launch_bounds__(kAttnThreads, PART == 3 ? 1 : 2) attn_bwd_dkdv_kernel(AttnArgs a) {
   constexpr int KS = D / 16, DT = D / 32;
+  constexpr bool DV = PART & 1, DK = PART & 2;
   __shared__ __attribute__((aligned(16))) uint16_t Qs[kBQ2 * (D + 8)];
-  __shared__ __attribute__((aligned(16))) uint16_t dOs[kBQ2 * (D + 8)];
-  __shared__ __attribute__((aligned(16))) uint16_t Qt[D * (kBQ2 + 8)];
-  __shared__ __attribute__((aligned(16))) uint16_t dOt[D * (kBQ2 + 8)];
+  __shared__ __attribute__((aligned(16))) uint16_t dOs[DK ? kBQ2 * (D + 8) : 8];
+  __shared__ __attribute__((aligned(16))) uint16_t Qt[DK ? D * (kBQ2 + 8) : 8];
+  __shared__ __attribute__((aligned(16))) uint16_t dOt[DV ? D * (kBQ2 + 8) : 8];
   __shared__ float lse_s[kBQ2], del_s[kBQ2];
 
   const int BH = a.B * a.H;
@@ -323,7 +327,7 @@ __global__ void __launch_bounds__(kAttnThreads, D == 64 ? 2 : 1) attn_bwd_dkdv_k
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       kf[ks] = *reinterpret_cast<const uint4*>(kp + ks * 16);
-      vf[ks] = *reinterpret_cast<const uint4*>(vp + ks * 16);
+      if constexpr (DK) vf[ks] = *reinterpret_cast<const uint4*>(vp + ks * 16);
     }
   }
   a_f32x16 dk[DT], dv[DT];
@@ -337,22 +341,27 @@ __global__ void __launch_bounds__(kAttnThreads, D == 64 ? 2 : 1) attn_bwd_dkdv_k
   const int first = (kb * kBKV2) / kBQ2, nq = a.S / kBQ2;
   for (int qb = first; qb < nq; ++qb) {
     const int qs0 = qb * kBQ2;
-    // tiles are staged one at a time (few registers live beside dK, dV, K, V)
+    // tiles are staged one at a time (few registers live beside the
+    // accumulators and K, V fragments)
     qrow.load(a.q, qs0, b, h);
     __syncthreads();  // previous step's LDS readers are done
     qrow.template store<true>(Qs);
-    __builtin_amdgcn_sched_barrier(0);
-    drow.load(a.dout, qs0, b, h);
-    drow.template store<true>(dOs);
-    __builtin_amdgcn_sched_barrier(0);
-    qcol.load(a.q, qs0, b, h);
-    qcol.store(Qt);
-    __builtin_amdgcn_sched_barrier(0);
-    dcol.load(a.dout, qs0, b, h);
-    dcol.store(dOt);
+    if constexpr (DK) {
+      __builtin_amdgcn_sched_barrier(0);
+      drow.load(a.dout, qs0, b, h);
+      drow.template store<true>(dOs);
+      __builtin_amdgcn_sched_barrier(0);
+      qcol.load(a.q, qs0, b, h);
+      qcol.store(Qt);
+    }
+    if constexpr (DV) {
+      __builtin_amdgcn_sched_barrier(0);
+      dcol.load(a.dout, qs0, b, h);
+      dcol.store(dOt);
+    }
     if (threadIdx.x < kBQ2) {
       lse_s[threadIdx.x] = a.lse[(int64_t)bh * a.S + qs0 + threadIdx.x];
-      del_s[threadIdx.x] = a.delta[(int64_t)bh * a.S + qs0 + threadIdx.x];
+      if constexpr (DK) del_s[threadIdx.x] = a.delta[(int64_t)bh * a.S + qs0 + threadIdx.x];
     }
     __syncthreads();
     if (qs0 + kBQ2 - 1 < k0) continue;  // every query of the step precedes this wave's keys
@@ -369,7 +378,7 @@ __global__ void __launch_bounds__(kAttnThreads, D == 64 ? 2 : 1) attn_bwd_dkdv_k
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         s = mma<FP16>(*reinterpret_cast<const uint4*>(qp + ks * 16), kf[ks], s);
-        dp = mma<FP16>(*reinterpret_cast<const uint4*>(op + ks * 16), vf[ks], dp);
+        if constexpr (DK) dp = mma<FP16>(*reinterpret_cast<const uint4*>(op + ks * 16), vf[ks], dp);
       }
       // P and dS (fp32); query index of register r = t*32 + swz_row(r, hl)
 #pragma unroll
@@ -378,21 +387,26 @@ __global__ void __launch_bounds__(kAttnThreads, D == 64 ? 2 : 1) attn_bwd_dkdv_k
         float p = fast_exp2(__builtin_fmaf(s[r], a.scale_log2, -lse_s[qi]));
         if (diag && key > qs0 + qi) p = 0.f;
         s[r] = p;
-        dp[r] = p * (dp[r] - del_s[qi]);
+        if constexpr (DK) dp[r] = p * (dp[r] - del_s[qi]);
       }
 #pragma unroll
       for (int k2 = 0; k2 < 2; ++k2) {
         const int kk = t * 2 + k2, e0 = k2 * 8;
-        const uint4 pa = make_uint4(pack2<FP16>(s[e0 + 0], s[e0 + 1]), pack2<FP16>(s[e0 + 2], s[e0 + 3]),
-                                    pack2<FP16>(s[e0 + 4], s[e0 + 5]), pack2<FP16>(s[e0 + 6], s[e0 + 7]));
-        const uint4 sa = make_uint4(pack2<FP16>(dp[e0 + 0], dp[e0 + 1]), pack2<FP16>(dp[e0 + 2], dp[e0 + 3]),
-                                    pack2<FP16>(dp[e0 + 4], dp[e0 + 5]), pack2<FP16>(dp[e0 + 6], dp[e0 + 7]));
-        const uint16_t* dop = dOt + (lane & 31) * (kBQ2 + 8) + kk * 16 + hl * 8;
-        const uint16_t* qtp = Qt + (lane & 31) * (kBQ2 + 8) + kk * 16 + hl * 8;
+        if constexpr (DV) {
+          const uint4 pa = make_uint4(pack2<FP16>(s[e0 + 0], s[e0 + 1]), pack2<FP16>(s[e0 + 2], s[e0 + 3]),
+                                      pack2<FP16>(s[e0 + 4], s[e0 + 5]), pack2<FP16>(s[e0 + 6], s[e0 + 7]));
+          const uint16_t* dop = dOt + (lane & 31) * (kBQ2 + 8) + kk * 16 + hl * 8;
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-          dv[dt] = mma<FP16>(pa, *reinterpret_cast<const uint4*>(dop + dt * 32 * (kBQ2 + 8)), dv[dt]);
-          dk[dt] = mma<FP16>(sa, *reinterpret_cast<const uint4*>(qtp + dt * 32 * (kBQ2 + 8)), dk[dt]);
+          for (int dt = 0; dt < DT; ++dt)
+            dv[dt] = mma<FP16>(pa, *reinterpret_cast<const uint4*>(dop + dt * 32 * (kBQ2 + 8)), dv[dt]);
+        }
+        if constexpr (DK) {
+          const uint4 sa = make_uint4(pack2<FP16>(dp[e0 + 0], dp[e0 + 1]), pack2<FP16>(dp[e0 + 2], dp[e0 + 3]),
+                                      pack2<FP16>(dp[e0 + 4], dp[e0 + 5]), pack2<FP16>(dp[e0 + 6], dp[e0 + 7]));
+          const uint16_t* qtp = Qt + (lane & 31) * (kBQ2 + 8) + kk * 16 + hl * 8;
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt)
+            dk[dt] = mma<FP16>(sa, *reinterpret_cast<const uint4*>(qtp + dt * 32 * (kBQ2 + 8)), dk[dt]);
         }
       }
     }
@@ -404,8 +418,8 @@ __global__ void __launch_bounds__(kAttnThreads, D == 64 ? 2 : 1) attn_bwd_dkdv_k
     for (int r = 0; r < 16; ++r) {
       const int kr = k0 + acc_row(r, hl);
       const int d = t * 32 + (lane & 31);
-      row_ptr(a.dk, kr, b, h)[d] = from_f<FP16>(dk[t][r] * a.scale);
-      row_ptr(a.dv, kr, b, h)[d] = from_f<FP16>(dv[t][r]);
+      if constexpr (DK) row_ptr(a.dk, kr, b, h)[d] = from_f<FP16>(dk[t][r] * a.scale);
+      if constexpr (DV) row_ptr(a.dv, kr, b, h)[d] = from_f<FP16>(dv[t][r]);
     }
 }
 
@@ -621,7 +635,8 @@ extern "C" int eth_attn_bwd(const eth_attn_desc_t* d, const void* q, const void*
   // dQ first: it also writes delta = rowsum(dO * O), which dK/dV reads
 #define ETH_ATTN_BWD(D, F)                                                       \
   attn_bwd_dq_kernel<D, F><<<g_q, kAttnThreads, 0, s>>>(a);                    \
-  attn_bwd_dkdv_kernel<D, F><<<g_kv, kAttnThreads, 0, s>>>(a);
+  attn_bwd_dkdv_kernel<D, F, 1><<<g_kv, kAttnThreads, 0, s>>>(a);              \
+  attn_bwd_dkdv_kernel<D, F, 2><<<g_kv, kAttnThreads, 0, s>>>(a);
   if (d->head_dim == 128) {
     if (fp16) { ETH_ATTN_BWD(128, true) } else { ETH_ATTN_BWD(128, false) }
   } else {
