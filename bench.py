@@ -14,7 +14,8 @@ covers the dominant kernel (the MFMA GEMM): algorithmic FLOPs of its
 launches / their summed duration, from HIP events recorded on the launch
 stream around every GEMM of the timed steps.  `hbm_path` reports the
 grad-pack+unscale+L2 pass and AdamW at BASELINE configs[2]/[3] scale
-(1,208,598,528 fp32 elements).  `cpu_baseline` times the oracle's torch-CPU
+(1,208,598,528 fp32 elements).  `first_last_stage` times the GPT-6.7B
+first+last stage in fp16.  `cpu_baseline` times the oracle's torch-CPU
 fp32 restatement of one layer (forward + backward + grad sync + AdamW) on
 the host cores, on a bounded sample, scaled to the 6-layer stage.
 """
@@ -180,6 +181,49 @@ def hbm_path(torch, iters=5):
     return out
 
 
+def first_last_stage(torch, steps=5, warmup=2):
+    """the GPT-6.7B first+last stage in fp16 -- token +
+    position embedding, 2 layers (hidden 4096, 32 heads, FFN 16384), final
+    LN, tied LM head over the padded vocabulary (50304) and vocab cross
+    entropy on the reference's synthetic batch (labels 0), seq 2048,
+    micro-batch 2; dynamic loss scale (2^16), grad sync, tied-gradient sum,
+    unscale + clip 1.0, AdamW with the fp16 model copy."""
+    from eth_amd.model.flex_ops import GPTConfig
+    from eth_amd.stage import FirstLastStageTrainer
+
+    h, heads, f, layers, s, b, V = 4096, 32, 16384, 2, 2048, 2, 50304
+    cfg = GPTConfig(hidden_size=h, num_attention_heads=heads, ffn_hidden_size=f, num_layers=layers, seq_length=s,
+                    micro_batch_size=b, padded_vocab_size=V, params_dtype=torch.float16, device="cuda", seed=1234)
+    tr = FirstLastStageTrainer(cfg, lr=1e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, clip_grad=1.0,
+                               bucket_cap_bytes=32 << 20, initial_loss_scale=2.0**16)
+    for i in range(warmup):
+        tr.train_step([2 * i, 2 * i + 1])
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    oks = 0
+    for i in range(steps):
+        _, _, ok, _ = tr.train_step([2 * (warmup + i), 2 * (warmup + i) + 1])
+        oks += bool(ok)
+    torch.cuda.synchronize()
+    ms = 1e3 * (time.perf_counter() - t0) / steps
+    T = s * b
+    flops = step_flops(layers, s, b, h, f) + 3 * 2.0 * T * h * V  # + LM head fwd, dgrad, wgrad
+    tflops = flops / (ms * 1e-3) / 1e12
+    del tr
+    torch.cuda.empty_cache()
+    return {
+        "workload": "GPT-6.7B first+last stage: embedding + 2 layers (h 4096, 32 heads, FFN 16384) + final LN + "
+                    "tied LM head (V 50304) + vocab CE, seq 2048, micro-batch 2, fp16, dynamic loss scale 2^16",
+        "tokens_per_s": T / (ms * 1e-3),
+        "ms_per_step": ms,
+        "steps": steps,
+        "steps_applied": oks,
+        "step_tflops": tflops,
+        "step_mfma_frac": tflops / PEAK_BF16_TFLOPS,
+        "dtype": "f16",
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -187,6 +231,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-hbm-path", action="store_true")
+    ap.add_argument("--no-first-last", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: every GPU box of this build has a single MI355X and no "
@@ -263,6 +308,8 @@ def main():
     torch.cuda.empty_cache()
     if not args.no_hbm_path:
         result["hbm_path"] = hbm_path(torch)
+    if not args.no_first_last:
+        result["first_last_stage"] = first_last_stage(torch)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline()
     print(json.dumps(result), flush=True)
