@@ -234,6 +234,71 @@ struct TileLoader<ROWS, BK, NT, true> : KTile<ROWS, BK, NT> {};
 template <int ROWS, int BK, int NT>
 struct TileLoader<ROWS, BK, NT, false> : RTile<ROWS, BK, NT> {};
 
+// BK x ROWS tile of an operand contiguous along the row index (element
+// (r, k) at P[k*ld + r0 + r]), copied as it is into LDS [BK][ROWS + 32]:
+// whole 512-byte k-rows per 32 lanes from global memory, 16-byte LDS
+// writes, and ds_read_b64_tr_b16 transposes on the way out (tr_frag).  The
+// 32-element pad puts the four k-rows one transposing read touches in
+// disjoint bank ranges.
+template <int ROWS, int BK, int NT>
+struct MTile {
+  static constexpr int CPR = ROWS / 8;  // 16-byte chunks per k-row
+  static constexpr int CPT = BK * CPR / NT;
+  static constexpr int LROW = ROWS + 32;
+  static_assert(CPT >= 1 && BK * CPR % NT == 0, "tile split");
+  u32x4_t v[CPT];
+  int32_t off[CPT];
+  __device__ __forceinline__ void init(int64_t ld, int r0, int rows) {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int c = threadIdx.x + i * NT;
+      const int k = c / CPR, r = (c % CPR) * 8;
+      off[i] = r0 + r < rows ? (int32_t)(((int64_t)k * ld + r0 + r) * 2) : kOob;
+    }
+  }
+  __device__ __forceinline__ void fetch(rsrc_t rs, int64_t ld, int k0) {
+    const int32_t soff = (int32_t)((int64_t)k0 * ld * 2);
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) v[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, off[i], soff, 0);
+  }
+  __device__ __forceinline__ void store(uint16_t* S) const {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int c = threadIdx.x + i * NT;
+      *reinterpret_cast<u32x4_t*>(S + (c / CPR) * LROW + (c % CPR) * 8) = v[i];
+    }
+  }
+  template <int P, int NP>
+  __device__ __forceinline__ void cycle(uint16_t* S, rsrc_t rs, int64_t ld, int k0) {
+    const int32_t soff = (int32_t)((int64_t)k0 * ld * 2);
+#pragma unroll
+    for (int i = P * CPT / NP; i < (P + 1) * CPT / NP; ++i) {
+      const int c = threadIdx.x + i * NT;
+      *reinterpret_cast<u32x4_t*>(S + (c / CPR) * LROW + (c % CPR) * 8) = v[i];
+      v[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, off[i], soff, 0);
+    }
+  }
+};
+template <int ROWS, int BK, int NT, bool KCONTIG>
+struct Tile256;
+template <int ROWS, int BK, int NT>
+struct Tile256<ROWS, BK, NT, true> : KTile<ROWS, BK, NT> {};
+template <int ROWS, int BK, int NT>
+struct Tile256<ROWS, BK, NT, false> : MTile<ROWS, BK, NT> {};
+
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
+// MFMA operand (8 consecutive k of one row) from a [k][row] LDS tile: two
+// transposing reads of 4 k each.  Lane l must pass the address of k-row
+// k0 + (l%16)/4 (k0 = 8*(l/32)), element row0 + 16*((l/16)%2) + 4*(l%4);
+// it then receives rows row0 + l%32, k = k0 .. k0+7.
+__device__ __forceinline__ uint4 tr_frag(const uint16_t* p, int lrow) {
+  const u32x2_t lo = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)p));
+  const u32x2_t hi =
+      __builtin_bit_cast(u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(p + 4 * lrow)));
+  return make_uint4(lo.x, lo.y, hi.x, hi.y);
+}
+
 struct GemmArgs {
   const uint16_t* A;
   const uint16_t* B;
@@ -395,8 +460,8 @@ __global__ void __launch_bounds__(256, 1) gemm256_kernel(GemmArgs g) {
   const rsrc_t ra = make_rsrc(g.A, g.a_bytes), rb = make_rsrc(g.B, g.b_bytes);
   // empty ranges: the loads issued past the last k-tile read zeros
   const rsrc_t ra0 = make_rsrc(g.A, 0), rb0 = make_rsrc(g.B, 0);
-  TileLoader<BM, BK, NT, A_K> la;
-  TileLoader<BN, BK, NT, B_K> lb;
+  Tile256<BM, BK, NT, A_K> la;
+  Tile256<BN, BK, NT, B_K> lb;
   la.init(g.lda, m0, g.M);
   lb.init(g.ldb, n0, g.N);
   la.fetch(ra, g.lda, 0);
@@ -409,12 +474,20 @@ __global__ void __launch_bounds__(256, 1) gemm256_kernel(GemmArgs g) {
 
   // fragment of (row block I, k-step KS): lanes 0-31 hold rows, lanes 32-63
   // the second 8 k of the 16
-  const int a_frag = (wm * 128 + lr) * R + lk;
-  const int b_frag = BM * R + (wn * 128 + lr) * R + lk;
+  // K-contiguous tiles: [row][BK + 8], one 16-byte read per fragment;
+  // row-contiguous tiles: [BK][256 + 32], two transposing reads (tr_frag)
+  constexpr int LM = BM + 32;
+  const int trl = ((lane >> 5) * 8 + ((lane & 15) >> 2)) * LM + ((lane >> 4) & 1) * 16 + (lane & 3) * 4;
+  const int a_frag = A_K ? (wm * 128 + lr) * R + lk : trl + wm * 128;
+  const int b_frag = BM * R + (B_K ? (wn * 128 + lr) * R + lk : trl + wn * 128);
   uint4 fa0[4], fb0[4], fa1[4], fb1[4];
 #define SB __builtin_amdgcn_sched_barrier(0);
-#define RD_A(FA, BASE, KS, I) FA[I] = *reinterpret_cast<const uint4*>((BASE) + a_frag + (I) * 32 * R + (KS) * 16);
-#define RD_B(FB, BASE, KS, J) FB[J] = *reinterpret_cast<const uint4*>((BASE) + b_frag + (J) * 32 * R + (KS) * 16);
+#define RD_A(FA, BASE, KS, I)                                                              \
+  FA[I] = A_K ? *reinterpret_cast<const uint4*>((BASE) + a_frag + (I) * 32 * R + (KS) * 16) \
+              : tr_frag((BASE) + a_frag + (I) * 32 + (KS) * 16 * LM, LM);
+#define RD_B(FB, BASE, KS, J)                                                              \
+  FB[J] = B_K ? *reinterpret_cast<const uint4*>((BASE) + b_frag + (J) * 32 * R + (KS) * 16) \
+              : tr_frag((BASE) + b_frag + (J) * 32 + (KS) * 16 * LM, LM);
 // B fragment as the MFMA's first operand: the lane then holds 4 consecutive
 // output columns (r % 4) of one output row (lane % 32)
 #define MMA2(FA, FB, I, J0)                                         \
