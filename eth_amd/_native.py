@@ -58,6 +58,7 @@ SIGNATURES = {
     "eth_grad_norm_finalize": [_P, _I64, _F64, _P, _P],
     "eth_adam_step": [_P, _P, _I64, _F64, _F64, _F64, _I64, _I32, _P, _P, _P],
     "eth_gemm": [_P, _I64, _I32, _P, _I64, _I32, _P, _I64, _I32, _P, _I64, _I64, _I64, _I32, _I32, _F32, _P],
+    "eth_gemm_splitk": [_P, _I64, _I32, _P, _I64, _I32, _P, _I64, _I64, _I64, _I64, _I32, _I32, _P, _P],
     "eth_ln_fwd": [_P, _P, _P, _P, _P, _P, _I64, _I64, _F32, _I32, _P],
     "eth_ln_bwd": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I32, _I32, _P],
     "eth_bias_gelu_fwd": [_P, _P, _P, _I64, _I64, _I32, _P],
@@ -99,6 +100,7 @@ class AttnDesc(ctypes.Structure):
 VALUE_SIGNATURES = {
     "eth_ln_bwd_workspace": ([_I64, _I64], _I64),
     "eth_col_sum_workspace": ([_I64, _I64], _I64),
+    "eth_gemm_splitk_workspace": ([_I64, _I64, _I32], _I64),
 }
 GEMM_ACCUMULATE, GEMM_BIAS = 1, 2
 

@@ -33,6 +33,8 @@
 //
 // Replaces the F.linear / cuBLAS calls of mpu/layers.py:357-370,452-470 and
 // the main_grad.add_ hook of model/distributed.py:116-123.
+#include <algorithm>
+
 #include "common.h"
 
 namespace eth {
@@ -311,6 +313,8 @@ struct GemmArgs {
   int flags;
   float alpha;
   uint32_t c_bytes;  // extent of C (gemm256_kernel's store range)
+  int k_split;              // split-K: k extent per split (0: one split of K)
+  int64_t c_split_stride;   // split-K: elements between the splits' C slices
 };
 
 template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, bool A_K, bool B_K, bool FP16>
@@ -431,8 +435,12 @@ __global__ void __launch_bounds__(256, 1) gemm256_kernel(GemmArgs g) {
   __shared__ __attribute__((aligned(16))) uint16_t smem[2 * STAGE];
 
   const int tiles_m = (g.M + BM - 1) / BM, tiles_n = (g.N + BN - 1) / BN;
+  // split-K launches tiles * splits workgroups: split = blockIdx.x / tiles
+  const int tiles = tiles_m * tiles_n;
+  const int split = blockIdx.x / tiles;
+  const int kb = split * g.k_split;
   int tm, tn;
-  tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  tile_coords(blockIdx.x - split * tiles, tiles_m, tiles_n, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int wm = wid >> 1, wn = wid & 1;
@@ -456,7 +464,7 @@ __global__ void __launch_bounds__(256, 1) gemm256_kernel(GemmArgs g) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  const int nk = g.K / BK;
+  const int nk = (g.k_split ? g.k_split : g.K) / BK;
   const rsrc_t ra = make_rsrc(g.A, g.a_bytes), rb = make_rsrc(g.B, g.b_bytes);
   // empty ranges: the loads issued past the last k-tile read zeros
   const rsrc_t ra0 = make_rsrc(g.A, 0), rb0 = make_rsrc(g.B, 0);
@@ -464,12 +472,12 @@ __global__ void __launch_bounds__(256, 1) gemm256_kernel(GemmArgs g) {
   Tile256<BN, BK, NT, B_K> lb;
   la.init(g.lda, m0, g.M);
   lb.init(g.ldb, n0, g.N);
-  la.fetch(ra, g.lda, 0);
-  lb.fetch(rb, g.ldb, 0);
+  la.fetch(ra, g.lda, kb);
+  lb.fetch(rb, g.ldb, kb);
   la.store(smem);
   lb.store(smem + BM * R);
-  la.fetch(ra, g.lda, BK);
-  lb.fetch(rb, g.ldb, BK);
+  la.fetch(ra, g.lda, kb + BK);
+  lb.fetch(rb, g.ldb, kb + BK);
   __syncthreads();
 
   // fragment of (row block I, k-step KS): lanes 0-31 hold rows, lanes 32-63
@@ -523,7 +531,7 @@ __global__ void __launch_bounds__(256, 1) gemm256_kernel(GemmArgs g) {
   {                                                     \
     uint16_t* const cur = (CUR);                        \
     uint16_t* const nxt = (NXT);                        \
-    const int k2 = ((KT) + 2) * BK;                     \
+    const int k2 = kb + ((KT) + 2) * BK;                \
     const rsrc_t rsa = (KT) + 2 < nk ? ra : ra0;        \
     const rsrc_t rsb = (KT) + 2 < nk ? rb : rb0;        \
     KSTEP(fa0, fb0, fa1, fb1, cur, 1, CYC_A)            \
@@ -568,7 +576,7 @@ __global__ void __launch_bounds__(256, 1) gemm256_kernel(GemmArgs g) {
   float* stage = reinterpret_cast<float*>(smem) + wid * 32 * ER;
   const int esz = g.c_dtype == ETH_F32 ? 4 : 2;
   const int mode = g.c_dtype == ETH_BF16 ? 0 : g.c_dtype == ETH_F16 ? 1 : (g.flags & ETH_GEMM_ACCUMULATE) ? 3 : 2;
-  const rsrc_t rc = make_rsrc(g.C, g.c_bytes);
+  const rsrc_t rc = make_rsrc(reinterpret_cast<float*>(g.C) + split * g.c_split_stride, g.c_bytes);
   const int32_t row2 = (int32_t)(2 * g.ldc * esz);
   auto write_slab = [&](const int i) __attribute__((always_inline)) {
     // the slab is private to this wave, whose LDS accesses complete in order
@@ -639,8 +647,8 @@ __global__ void __launch_bounds__(256, 1) gemm256_kernel(GemmArgs g) {
 }
 
 template <bool FP16>
-static int launch_256(const GemmArgs& a, int a_k, int b_k, hipStream_t s) {
-  const int tiles = ((a.M + 255) / 256) * ((a.N + 255) / 256);
+static int launch_256(const GemmArgs& a, int a_k, int b_k, hipStream_t s, int splits = 1) {
+  const int tiles = ((a.M + 255) / 256) * ((a.N + 255) / 256) * splits;
   if (a_k && b_k)
     gemm256_kernel<true, true, FP16><<<tiles, 256, 0, s>>>(a);
   else if (a_k && !b_k)
@@ -719,6 +727,8 @@ extern "C" int eth_gemm(const void* A, int64_t lda, int a_kcontig, const void* B
   const int esz = c_dtype == ETH_F32 ? 4 : 2;
   const int64_t c_extent = ((M - 1) * ldc + N) * esz;
   const bool c_vec = ldc % 4 == 0 && N % 4 == 0 && ((uintptr_t)C % (4 * esz)) == 0;
+  a.k_split = 0;
+  a.c_split_stride = 0;
   if (K % 128 == 0 && c_vec && big_tiles >= 128 && c_extent + 256 * ldc * esz < (1LL << 31)) {
     a.c_bytes = (uint32_t)c_extent;
     return in_dtype == ETH_BF16 ? launch_256<false>(a, a_kcontig, b_kcontig, s)
@@ -733,4 +743,86 @@ extern "C" int eth_gemm(const void* A, int64_t lda, int a_kcontig, const void* B
                : launch_layout<128, 128, 64, 2, 2, false>(a, a_kcontig, b_kcontig, s);
   return big ? launch_layout<256, 256, 64, 2, 4, true>(a, a_kcontig, b_kcontig, s)
              : launch_layout<128, 128, 64, 2, 2, true>(a, a_kcontig, b_kcontig, s);
+}
+
+namespace eth {
+// C[m, n] += sum_s W[s][m*N + n], splits added in order (deterministic)
+__global__ void splitk_reduce_kernel(const float* __restrict__ W, int splits, int64_t stride, float* __restrict__ C,
+                                     int64_t ldc, int M, int N) {
+  const int nq = N / 4;
+  const int64_t total = (int64_t)M * nq;
+  for (int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; q < total; q += (int64_t)gridDim.x * blockDim.x) {
+    const int m = (int)(q / nq), n = (int)(q % nq) * 4;
+    float4 acc = *reinterpret_cast<const float4*>(W + (int64_t)m * N + n);
+    for (int sp = 1; sp < splits; ++sp) {
+      const float4 w = *reinterpret_cast<const float4*>(W + sp * stride + (int64_t)m * N + n);
+      acc.x += w.x;
+      acc.y += w.y;
+      acc.z += w.z;
+      acc.w += w.w;
+    }
+    float4* c = reinterpret_cast<float4*>(C + (int64_t)m * ldc + n);
+    float4 o = *c;
+    o.x += acc.x;
+    o.y += acc.y;
+    o.z += acc.z;
+    o.w += acc.w;
+    *c = o;
+  }
+}
+}  // namespace eth
+
+extern "C" int64_t eth_gemm_splitk_workspace(int64_t M, int64_t N, int splits) {
+  return splits > 0 && M > 0 && N > 0 ? (int64_t)splits * M * N * 4 : 0;
+}
+
+extern "C" int eth_gemm_splitk(const void* A, int64_t lda, int a_kcontig, const void* B, int64_t ldb, int b_kcontig,
+                               float* C, int64_t ldc, int64_t M, int64_t N, int64_t K, int in_dtype, int splits,
+                               float* workspace, void* stream) {
+  ETH_CHECK_ARG(in_dtype == ETH_BF16 || in_dtype == ETH_F16, "eth_gemm_splitk: inputs must be bf16 or fp16");
+  ETH_CHECK_ARG(A && B && C && workspace, "eth_gemm_splitk: null operand");
+  ETH_CHECK_ARG(splits >= 1 && splits <= 16, "eth_gemm_splitk: splits must be in [1, 16] (got %d)", splits);
+  ETH_CHECK_ARG(M > 0 && N > 0 && K > 0 && M < (1LL << 31) && N < (1LL << 31) && K < (1LL << 31),
+                "eth_gemm_splitk: bad shape %lld x %lld x %lld", (long long)M, (long long)N, (long long)K);
+  ETH_CHECK_ARG(K % (128LL * splits) == 0, "eth_gemm_splitk: K (%lld) must be a multiple of 128 * splits",
+                (long long)K);
+  ETH_CHECK_ARG(N % 4 == 0 && ldc % 4 == 0 && ldc >= N && ((uintptr_t)C & 15) == 0 && ((uintptr_t)workspace & 15) == 0,
+                "eth_gemm_splitk: C and the workspace need 16-byte aligned rows (N %% 4 == 0)");
+  ETH_CHECK_ARG(lda % 8 == 0 && ldb % 8 == 0, "eth_gemm_splitk: lda/ldb must be multiples of 8");
+  ETH_CHECK_ARG(((uintptr_t)A & 15) == 0 && ((uintptr_t)B & 15) == 0, "eth_gemm_splitk: A/B must be 16-byte aligned");
+  ETH_CHECK_ARG(a_kcontig ? lda >= K : (M % 8 == 0 && lda >= M), "eth_gemm_splitk: bad A layout");
+  ETH_CHECK_ARG(b_kcontig ? ldb >= K : (N % 8 == 0 && ldb >= N), "eth_gemm_splitk: bad B layout");
+  const int64_t a_elems = a_kcontig ? (M - 1) * lda + K : (K - 1) * lda + M;
+  const int64_t b_elems = b_kcontig ? (N - 1) * ldb + K : (K - 1) * ldb + N;
+  const int64_t slice = M * N;
+  ETH_CHECK_ARG(a_elems * 2 < (1LL << 31) && b_elems * 2 < (1LL << 31) && (slice + 256 * N) * 4 < (1LL << 31),
+                "eth_gemm_splitk: operands above 2 GiB are not supported");
+  GemmArgs a{};
+  a.A = (const uint16_t*)A;
+  a.B = (const uint16_t*)B;
+  a.a_bytes = (uint32_t)(a_elems * 2);
+  a.b_bytes = (uint32_t)(b_elems * 2);
+  a.C = workspace;
+  a.bias = nullptr;
+  a.M = (int)M;
+  a.N = (int)N;
+  a.K = (int)K;
+  a.lda = lda;
+  a.ldb = ldb;
+  a.ldc = N;
+  a.c_dtype = ETH_F32;
+  a.flags = 0;
+  a.alpha = 1.0f;
+  a.c_bytes = (uint32_t)(slice * 4);
+  a.k_split = (int)(K / splits);
+  a.c_split_stride = slice;
+  hipStream_t s = (hipStream_t)stream;
+  const int rc = in_dtype == ETH_BF16 ? launch_256<false>(a, a_kcontig, b_kcontig, s, splits)
+                                      : launch_256<true>(a, a_kcontig, b_kcontig, s, splits);
+  if (rc != ETH_OK) return rc;
+  const int64_t quads = M * (N / 4);
+  const int grid = (int)std::min<int64_t>((quads + 255) / 256, 2048);
+  splitk_reduce_kernel<<<grid, 256, 0, s>>>(workspace, splits, slice, C, ldc, (int)M, (int)N);
+  ETH_CHECK_LAUNCH("eth_gemm_splitk");
+  return ETH_OK;
 }

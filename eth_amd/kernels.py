@@ -59,6 +59,31 @@ def set_gemm_observer(fn):
     _gemm_observer = fn
 
 
+def _splitk_splits(M, N, K, out):
+    """Split-K factor for an fp32 accumulate whose 256x256 tile grid is too
+    small to fill the chip (fewer than 128 tiles): enough k-splits for about
+    one workgroup per CU, each split a multiple of 128 deep."""
+    tiles = -(-M // 256) * -(-N // 256)
+    if tiles >= 128 or N % 4 or out.stride(0) % 4 or out.data_ptr() % 16:
+        return 1
+    splits = 1
+    while splits < 16 and tiles * splits * 2 <= 256 and K % (128 * splits * 2) == 0 and K // (splits * 2) >= 1024:
+        splits *= 2
+    return splits
+
+
+_scratch = {}
+
+
+def _scratch_f32(numel, device):
+    """A per-device fp32 workspace reused across calls (grown on demand)."""
+    buf = _scratch.get(device)
+    if buf is None or buf.numel() < numel:
+        buf = torch.empty(numel, dtype=torch.float32, device=device)
+        _scratch[device] = buf
+    return buf[:numel]
+
+
 def gemm(a, b, out=None, bias=None, accumulate=False, out_dtype=None, alpha=1.0):
     """out (+)= alpha * a @ b (+ bias), a: [M, K], b: [K, N] (any row/column-
     major 2-D views), out: [M, N] row-major.  fp32 `out` with accumulate=True
@@ -89,6 +114,19 @@ def gemm(a, b, out=None, bias=None, accumulate=False, out_dtype=None, alpha=1.0)
     obs = _gemm_observer
     if obs is not None:
         obs("begin", M, N, K)
+    splits = _splitk_splits(M, N, K, out) if accumulate and alpha == 1.0 and bias is None else 1
+    if splits > 1:
+        ws = _scratch_f32(nat.value("eth_gemm_splitk_workspace", M, N, splits) // 4, a.device)
+        nat.call(
+            "eth_gemm_splitk",
+            nat.ptr(a), lda, a_kcontig,
+            nat.ptr(b), ldb, b_kcontig,
+            nat.ptr(out), out.stride(0), M, N, K, code, splits, nat.ptr(ws),
+            nat.stream_ptr(a.device),
+        )
+        if obs is not None:
+            obs("end", M, N, K)
+        return out
     nat.call(
         "eth_gemm",
         nat.ptr(a), lda, a_kcontig,

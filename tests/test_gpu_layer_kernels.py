@@ -87,6 +87,39 @@ def test_gemm_pipelined_kernel_layouts(cuda, dtype, a_k, b_k):
     assert err <= 1e-4 * ref2.abs().max().item(), f"accumulate err {err}"
 
 
+@pytest.mark.parametrize("a_k,b_k", [(True, True), (True, False), (False, False), (False, True)])
+def test_gemm_splitk_accumulate(cuda, a_k, b_k):
+    """Small-grid fp32 accumulation (20 tiles of 256, K 4096) takes the
+    split-K path: 4 k-splits into a workspace, added in order.  Matches the
+    fp32 reference and is bit-identical run to run."""
+    from eth_amd import _native as nat
+
+    M, N, Kd = 1024, 1032, 4096
+    assert K._splitk_splits(M, N, Kd, torch.empty(M, N, device=cuda)) == 4
+    announce(f"gemm split-K a_k={a_k} b_k={b_k} {M}x{N}x{Kd}")
+    gen = torch.Generator().manual_seed(23 + 2 * a_k + b_k)
+    a = _rand((M, Kd), torch.bfloat16, gen)
+    b = _rand((Kd, N), torch.bfloat16, gen, 0.05)
+    ad = a.to(cuda) if a_k else a.t().contiguous().to(cuda).t()
+    bd = b.t().contiguous().to(cuda).t() if b_k else b.to(cuda)
+    ref = 0.25 + a.float() @ b.float()
+    outs = []
+    for _ in range(2):
+        acc = torch.full((M, N), 0.25, dtype=torch.float32, device=cuda)
+        K.gemm(ad, bd, out=acc, accumulate=True)
+        outs.append(acc.cpu())
+    err = (outs[0] - ref).abs().max().item()
+    assert err <= 1e-4 * ref.abs().max().item(), f"split-K err {err}"
+    assert torch.equal(outs[0], outs[1])
+    # the single-pass kernel agrees to fp32 summation-order noise
+    one = torch.full((M, N), 0.25, dtype=torch.float32, device=cuda)
+    lda = ad.stride(0) if a_k else ad.stride(1)
+    ldb = bd.stride(1) if b_k else bd.stride(0)
+    nat.call("eth_gemm", nat.ptr(ad), lda, int(a_k), nat.ptr(bd), ldb, int(b_k), nat.ptr(one), N, nat.ETH_F32,
+             None, M, N, Kd, nat.dtype_code(torch.bfloat16), nat.GEMM_ACCUMULATE, 1.0, nat.stream_ptr(cuda))
+    assert (one.cpu() - outs[0]).abs().max().item() <= 1e-5 * ref.abs().max().item()
+
+
 def test_gemm_rejects_bad_shapes(cuda):
     a = torch.zeros(16, 12, dtype=torch.bfloat16, device=cuda)
     b = torch.zeros(12, 16, dtype=torch.bfloat16, device=cuda)
