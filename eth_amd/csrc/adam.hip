@@ -19,6 +19,8 @@
 namespace eth {
 
 constexpr int kAdamThreads = 256;
+typedef float af32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t au32x2_t __attribute__((ext_vector_type(2)));
 
 struct AdamScalars {
   float beta1, one_minus_beta1, beta2, one_minus_beta2, eps, bc2_sqrt;
@@ -67,24 +69,24 @@ __global__ void __launch_bounds__(kAdamThreads) adam_kernel(const eth_adam_tenso
                    (((uintptr_t)out) & 7u) == 0;
   int i0 = 0;
   if (vec) {
+    // two float4 per thread per trip, all eight loads issued before any use;
+    // nontemporal: every byte is touched once per step
     const int nv = n >> 2;
-    for (int i = threadIdx.x; i < nv; i += kAdamThreads) {
-      float4 pp = reinterpret_cast<float4*>(p)[i];
-      float4 gg = reinterpret_cast<const float4*>(g)[i];
-      float4 mm = reinterpret_cast<float4*>(m)[i];
-      float4 vv = reinterpret_cast<float4*>(v)[i];
-      if (clip != 1.0f) {
-        gg.x *= clip; gg.y *= clip; gg.z *= clip; gg.w *= clip;
+    auto upd = [&](int i, af32x4_t pp, af32x4_t gg, af32x4_t mm, af32x4_t vv) __attribute__((always_inline)) {
+      if (clip != 1.0f) gg *= clip;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float pe = pp[e], me = mm[e], ve = vv[e];
+        adam_elem(pe, gg[e], me, ve, decay, neg_step, s);
+        pp[e] = pe;
+        mm[e] = me;
+        vv[e] = ve;
       }
-      adam_elem(pp.x, gg.x, mm.x, vv.x, decay, neg_step, s);
-      adam_elem(pp.y, gg.y, mm.y, vv.y, decay, neg_step, s);
-      adam_elem(pp.z, gg.z, mm.z, vv.z, decay, neg_step, s);
-      adam_elem(pp.w, gg.w, mm.w, vv.w, decay, neg_step, s);
-      reinterpret_cast<float4*>(p)[i] = pp;
-      reinterpret_cast<float4*>(m)[i] = mm;
-      reinterpret_cast<float4*>(v)[i] = vv;
+      __builtin_nontemporal_store(pp, reinterpret_cast<af32x4_t*>(p) + i);
+      __builtin_nontemporal_store(mm, reinterpret_cast<af32x4_t*>(m) + i);
+      __builtin_nontemporal_store(vv, reinterpret_cast<af32x4_t*>(v) + i);
       if (MODEL_DT != ETH_F32 && out) {
-        uint2 o;
+        au32x2_t o;
         if (MODEL_DT == ETH_BF16) {
           o.x = f2bf_pair(pp.x, pp.y);
           o.y = f2bf_pair(pp.z, pp.w);
@@ -92,9 +94,24 @@ __global__ void __launch_bounds__(kAdamThreads) adam_kernel(const eth_adam_tenso
           o.x = (uint32_t)f2h_bits(pp.x) | ((uint32_t)f2h_bits(pp.y) << 16);
           o.y = (uint32_t)f2h_bits(pp.z) | ((uint32_t)f2h_bits(pp.w) << 16);
         }
-        reinterpret_cast<uint2*>(out)[i] = o;
+        __builtin_nontemporal_store(o, reinterpret_cast<au32x2_t*>(out) + i);
       }
+    };
+    const af32x4_t* p4 = reinterpret_cast<const af32x4_t*>(p);
+    const af32x4_t* g4 = reinterpret_cast<const af32x4_t*>(g);
+    const af32x4_t* m4 = reinterpret_cast<const af32x4_t*>(m);
+    const af32x4_t* v4 = reinterpret_cast<const af32x4_t*>(v);
+    int i = threadIdx.x;
+    for (; i + kAdamThreads < nv; i += 2 * kAdamThreads) {
+      const int j = i + kAdamThreads;
+      const af32x4_t p0 = __builtin_nontemporal_load(p4 + i), g0 = __builtin_nontemporal_load(g4 + i);
+      const af32x4_t m0 = __builtin_nontemporal_load(m4 + i), v0 = __builtin_nontemporal_load(v4 + i);
+      const af32x4_t p1 = __builtin_nontemporal_load(p4 + j), g1 = __builtin_nontemporal_load(g4 + j);
+      const af32x4_t m1 = __builtin_nontemporal_load(m4 + j), v1 = __builtin_nontemporal_load(v4 + j);
+      upd(i, p0, g0, m0, v0);
+      upd(j, p1, g1, m1, v1);
     }
+    if (i < nv) upd(i, p4[i], g4[i], m4[i], v4[i]);
     i0 = nv << 2;
   }
   for (int i = i0 + threadIdx.x; i < n; i += kAdamThreads) {
