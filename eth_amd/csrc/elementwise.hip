@@ -30,14 +30,22 @@ __device__ __forceinline__ uint16_t cout(float v) {
 constexpr float kBeta = 0.7978845608028654f;  // sqrt(2/pi)
 constexpr float kKappa = 0.044715f;
 
+// tanh(u) = 1 - 2 / (1 + e^{2u}) with the hardware exp2 and reciprocal: a
+// few ulp in fp32, far below the 16-bit output rounding, and exact at the
+// saturated ends (e^{2u} = inf -> 1, 0 -> -1).  libm tanhf made these
+// kernels VALU-bound.
+__device__ __forceinline__ float fast_tanh(float u) {
+  const float e = __builtin_amdgcn_exp2f(u * 2.8853900817779268f);  // 2 / ln 2
+  return 1.0f - 2.0f * __builtin_amdgcn_rcpf(1.0f + e);
+}
 __device__ __forceinline__ float gelu_tanh(float x) {
   const float x3 = x * x * x;
   const float inner = kBeta * (x + kKappa * x3);
-  return 0.5f * x * (1.0f + tanhf(inner));
+  return 0.5f * x * (1.0f + fast_tanh(inner));
 }
 __device__ __forceinline__ float gelu_tanh_grad(float x) {
   const float x2 = x * x;
-  const float t = tanhf(kBeta * (x + kKappa * (x2 * x)));
+  const float t = fast_tanh(kBeta * (x + kKappa * (x2 * x)));
   const float left = 0.5f * x, right = 1.0f + t;
   return 0.5f * right + left * (1.0f - t * t) * kBeta * (1.0f + 3.0f * kKappa * x2);
 }
