@@ -63,6 +63,10 @@ constexpr int kPad = 8;  // LDS row padding (elements): 16 B breaks bank aliasin
 __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
+// The same after this wave's direct global->LDS loads have landed.
+__device__ __forceinline__ void dma_barrier() {
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
 
 // Map a linear workgroup id to (tile_m, tile_n): XCD-contiguous, then
 // GROUP_M-row grouped.
@@ -288,6 +292,49 @@ struct Tile256<ROWS, BK, NT, true> : KTile<ROWS, BK, NT> {};
 template <int ROWS, int BK, int NT>
 struct Tile256<ROWS, BK, NT, false> : MTile<ROWS, BK, NT> {};
 
+// Tile moved by direct global->LDS loads (buffer_load_dwordx4 ... lds):
+// lane i of an instruction writes its 16 bytes at the wave's LDS base +
+// 16 i, so the tile's LDS image, row padding included, is covered by
+// consecutive 1 KB pieces, PER_WAVE of them per wave; padding units get an
+// out-of-range offset (they read zeros).  KC: [ROWS][BK + 8] image of a
+// K-contiguous operand; otherwise [BK][ROWS + 32] of a row-contiguous one.
+typedef __attribute__((address_space(3))) void lds_void_t;
+__device__ __forceinline__ void dma16(rsrc_t rs, uint16_t* lds, int32_t voff, int32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)lds, 16, voff, soff, 0, 0);
+}
+template <int ROWS, int BK, bool KC>
+struct DTile {
+  static constexpr int UPR = KC ? BK / 8 + 1 : ROWS / 8 + 4;  // 16-byte units per LDS row
+  static constexpr int DPR = KC ? BK / 8 : ROWS / 8;           // of which data
+  static constexpr int NROW = KC ? ROWS : BK;
+  static constexpr int PER_WAVE = NROW * UPR / 256;
+  static_assert(NROW * UPR % 256 == 0, "tile split");
+  int32_t off[PER_WAVE];
+  int wave;
+  __device__ __forceinline__ void init(int64_t ld, int r0, int rows) {
+    wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int j = 0; j < PER_WAVE; ++j) {
+      const int u = (wave * PER_WAVE + j) * 64 + lane;
+      const int row = u / UPR, c = u % UPR;
+      if (c >= DPR)
+        off[j] = kOob;
+      else if (KC)
+        off[j] = r0 + row < rows ? (int32_t)((((int64_t)(r0 + row)) * ld + c * 8) * 2) : kOob;
+      else
+        off[j] = r0 + c * 8 < rows ? (int32_t)(((int64_t)row * ld + r0 + c * 8) * 2) : kOob;
+    }
+  }
+  // pieces [J0, J1) of k-tile k0 into the LDS image at S
+  template <int J0, int J1>
+  __device__ __forceinline__ void issue(uint16_t* S, rsrc_t rs, int64_t ld, int k0) {
+    const int32_t soff = KC ? k0 * 2 : (int32_t)((int64_t)k0 * ld * 2);
+#pragma unroll
+    for (int j = J0; j < J1; ++j) dma16(rs, S + (wave * PER_WAVE + j) * 512, off[j], soff);
+  }
+};
+
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
 // MFMA operand (8 consecutive k of one row) from a [k][row] LDS tile: two
@@ -432,7 +479,11 @@ template <bool A_K, bool B_K, bool FP16>
 __global__ void __launch_bounds__(256, 1) gemm256_kernel(GemmArgs g) {
   constexpr int BM = 256, BN = 256, BK = 64, NT = 256, R = BK + kPad;
   constexpr int STAGE = (BM + BN) * R;  // one LDS stage: A tile then B tile
-  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * STAGE];
+  // the two stages are separate arrays, so the compiler can tell the direct
+  // loads into one stage from the fragment reads of the other (it would
+  // otherwise wait for the loads before every read)
+  __shared__ __attribute__((aligned(16))) uint16_t smem[STAGE];
+  __shared__ __attribute__((aligned(16))) uint16_t smem1[STAGE];
 
   const int tiles_m = (g.M + BM - 1) / BM, tiles_n = (g.N + BN - 1) / BN;
   // split-K launches tiles * splits workgroups: split = blockIdx.x / tiles
@@ -468,17 +519,13 @@ __global__ void __launch_bounds__(256, 1) gemm256_kernel(GemmArgs g) {
   const rsrc_t ra = make_rsrc(g.A, g.a_bytes), rb = make_rsrc(g.B, g.b_bytes);
   // empty ranges: the loads issued past the last k-tile read zeros
   const rsrc_t ra0 = make_rsrc(g.A, 0), rb0 = make_rsrc(g.B, 0);
-  Tile256<BM, BK, NT, A_K> la;
-  Tile256<BN, BK, NT, B_K> lb;
+  DTile<BM, BK, A_K> la;
+  DTile<BN, BK, B_K> lb;
   la.init(g.lda, m0, g.M);
   lb.init(g.ldb, n0, g.N);
-  la.fetch(ra, g.lda, kb);
-  lb.fetch(rb, g.ldb, kb);
-  la.store(smem);
-  lb.store(smem + BM * R);
-  la.fetch(ra, g.lda, kb + BK);
-  lb.fetch(rb, g.ldb, kb + BK);
-  __syncthreads();
+  la.template issue<0, DTile<BM, BK, A_K>::PER_WAVE>(smem, ra, g.lda, kb);
+  lb.template issue<0, DTile<BN, BK, B_K>::PER_WAVE>(smem + BM * R, rb, g.ldb, kb);
+  dma_barrier();
 
   // fragment of (row block I, k-step KS): lanes 0-31 hold rows, lanes 32-63
   // the second 8 k of the 16
@@ -516,8 +563,8 @@ __global__ void __launch_bounds__(256, 1) gemm256_kernel(GemmArgs g) {
 #define KSTEP_ROW(FA, FB, GA, GB, RB, RK, I, S0, S1, CYC) \
   SB MMA2(FA, FB, I, 0) SB S0(GA, GB, RB, RK) SB MMA2(FA, FB, I, 2) SB S1(GA, GB, RB, RK) SB CYC(I)
 #define NOCYC(P)
-#define CYC_A(P) la.template cycle<P, 4>(nxt, rsa, g.lda, k2);
-#define CYC_B(P) lb.template cycle<P, 4>(nxt + BM * R, rsb, g.ldb, k2);
+#define CYC_A(P) la.template issue<(P) * 2, (P) == 3 ? 9 : (P) * 2 + 2>(nxt, rsa, g.lda, k1);
+#define CYC_B(P) lb.template issue<(P) * 2, (P) == 3 ? 9 : (P) * 2 + 2>(nxt + BM * R, rsb, g.ldb, k1);
 #define KSTEP(FA, FB, GA, GB, RB, RK, CYC)                     \
   KSTEP_ROW(FA, FB, GA, GB, RB, RK, 0, RD_SEQ0, RD_SEQ1, CYC) \
   KSTEP_ROW(FA, FB, GA, GB, RB, RK, 1, RD_SEQ2, RD_SEQ3, CYC) \
@@ -531,13 +578,13 @@ __global__ void __launch_bounds__(256, 1) gemm256_kernel(GemmArgs g) {
   {                                                     \
     uint16_t* const cur = (CUR);                        \
     uint16_t* const nxt = (NXT);                        \
-    const int k2 = kb + ((KT) + 2) * BK;                \
-    const rsrc_t rsa = (KT) + 2 < nk ? ra : ra0;        \
-    const rsrc_t rsb = (KT) + 2 < nk ? rb : rb0;        \
+    const int k1 = kb + ((KT) + 1) * BK;                \
+    const rsrc_t rsa = (KT) + 1 < nk ? ra : ra0;        \
+    const rsrc_t rsb = (KT) + 1 < nk ? rb : rb0;        \
     KSTEP(fa0, fb0, fa1, fb1, cur, 1, CYC_A)            \
     KSTEP(fa1, fb1, fa0, fb0, cur, 2, CYC_B)            \
     KSTEP(fa0, fb0, fa1, fb1, cur, 3, NOCYC)            \
-    lds_barrier();                                      \
+    dma_barrier();                                      \
     KSTEP(fa1, fb1, fa0, fb0, nxt, 0, NOCYC)            \
   }
   SB RD_SEQ0(fa0, fb0, smem, 0) SB RD_SEQ1(fa0, fb0, smem, 0) SB RD_SEQ2(fa0, fb0, smem, 0) SB
@@ -545,8 +592,8 @@ __global__ void __launch_bounds__(256, 1) gemm256_kernel(GemmArgs g) {
   RD_SEQ6(fa0, fb0, smem, 0) SB RD_SEQ7(fa0, fb0, smem, 0) SB
   // two k-tiles per trip, so both LDS stages have fixed addresses
   for (int kt = 0; kt < nk; kt += 2) {
-    ITER(smem, smem + STAGE, kt)
-    ITER(smem + STAGE, smem, kt + 1)
+    ITER(smem, smem1, kt)
+    ITER(smem1, smem, kt + 1)
   }
 #undef ITER
 #undef KSTEP
