@@ -525,6 +525,7 @@ __global__ void __launch_bounds__(256, 1) gemm256_kernel(GemmArgs g) {
   lb.init(g.ldb, n0, g.N);
   la.template issue<0, DTile<BM, BK, A_K>::PER_WAVE>(smem, ra, g.lda, kb);
   lb.template issue<0, DTile<BN, BK, B_K>::PER_WAVE>(smem + BM * R, rb, g.ldb, kb);
+  la.template issue<0, DTile<BM, BK, A_K>::PER_WAVE>(smem1, nk > 1 ? ra : ra0, g.lda, kb + BK);
   dma_barrier();
 
   // fragment of (row block I, k-step KS): lanes 0-31 hold rows, lanes 32-63
@@ -563,29 +564,32 @@ __global__ void __launch_bounds__(256, 1) gemm256_kernel(GemmArgs g) {
 #define KSTEP_ROW(FA, FB, GA, GB, RB, RK, I, S0, S1, CYC) \
   SB MMA2(FA, FB, I, 0) SB S0(GA, GB, RB, RK) SB MMA2(FA, FB, I, 2) SB S1(GA, GB, RB, RK) SB CYC(I)
 #define NOCYC(P)
-#define CYC_A(P) la.template issue<(P) * 2, (P) == 3 ? 9 : (P) * 2 + 2>(nxt, rsa, g.lda, k1);
+#define CYC_A(P) la.template issue<(P) * 2, (P) == 3 ? 9 : (P) * 2 + 2>(cur, rsa, g.lda, k2);
 #define CYC_B(P) lb.template issue<(P) * 2, (P) == 3 ? 9 : (P) * 2 + 2>(nxt + BM * R, rsb, g.ldb, k1);
 #define KSTEP(FA, FB, GA, GB, RB, RK, CYC)                     \
   KSTEP_ROW(FA, FB, GA, GB, RB, RK, 0, RD_SEQ0, RD_SEQ1, CYC) \
   KSTEP_ROW(FA, FB, GA, GB, RB, RK, 1, RD_SEQ2, RD_SEQ3, CYC) \
   KSTEP_ROW(FA, FB, GA, GB, RB, RK, 2, RD_SEQ4, RD_SEQ5, CYC) \
   KSTEP_ROW(FA, FB, GA, GB, RB, RK, 3, RD_SEQ6, RD_SEQ7, CYC) SB
-// k-tile KT: MFMAs from stage CUR; k-tile KT+1 moves from registers into
-// stage NXT (A during k-step 0, B during k-step 1) while k-tile KT+2 is
-// loaded; after k-step 2 every wave is done with CUR and has written NXT,
-// so k-step 3 reads the first fragments of KT+1 from NXT
+// k-tile KT: k-steps 0-2 from stage CUR while the B half of k-tile KT+1 is
+// loaded into NXT (its A half was started one k-step earlier); the barrier
+// (after this wave's direct loads have landed) means every wave is done
+// reading CUR and KT+1 is complete in NXT; k-step 3 then computes from
+// registers, reads the first fragments of KT+1 from NXT and starts the A
+// half of k-tile KT+2 into CUR
 #define ITER(CUR, NXT, KT)                              \
   {                                                     \
     uint16_t* const cur = (CUR);                        \
     uint16_t* const nxt = (NXT);                        \
     const int k1 = kb + ((KT) + 1) * BK;                \
-    const rsrc_t rsa = (KT) + 1 < nk ? ra : ra0;        \
+    const int k2 = kb + ((KT) + 2) * BK;                \
     const rsrc_t rsb = (KT) + 1 < nk ? rb : rb0;        \
-    KSTEP(fa0, fb0, fa1, fb1, cur, 1, CYC_A)            \
-    KSTEP(fa1, fb1, fa0, fb0, cur, 2, CYC_B)            \
+    const rsrc_t rsa = (KT) + 2 < nk ? ra : ra0;        \
+    KSTEP(fa0, fb0, fa1, fb1, cur, 1, CYC_B)            \
+    KSTEP(fa1, fb1, fa0, fb0, cur, 2, NOCYC)            \
     KSTEP(fa0, fb0, fa1, fb1, cur, 3, NOCYC)            \
     dma_barrier();                                      \
-    KSTEP(fa1, fb1, fa0, fb0, nxt, 0, NOCYC)            \
+    KSTEP(fa1, fb1, fa0, fb0, nxt, 0, CYC_A)            \
   }
   SB RD_SEQ0(fa0, fb0, smem, 0) SB RD_SEQ1(fa0, fb0, smem, 0) SB RD_SEQ2(fa0, fb0, smem, 0) SB
   RD_SEQ3(fa0, fb0, smem, 0) SB RD_SEQ4(fa0, fb0, smem, 0) SB RD_SEQ5(fa0, fb0, smem, 0) SB
@@ -678,7 +682,7 @@ __global__ void __launch_bounds__(256, 1) gemm256_kernel(GemmArgs g) {
     }
 #undef OFF
   };
-  lds_barrier();  // every wave is done with the k-loop stages
+  dma_barrier();  // every wave is done with the k-loop stages, no load in flight
 #define STAGE_SLAB(I)                                                                  \
   {                                                                                    \
     _Pragma("unroll") for (int j = 0; j < 4; ++j)                                      \
