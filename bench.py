@@ -34,6 +34,13 @@ if ROOT not in sys.path:
 PEAK_BF16_TFLOPS = 2516.0  # MI355X dense bf16 MFMA (2.5 PFLOP/s)
 PEAK_HBM_GBPS = 8000.0     # MI355X HBM3E
 H, HEADS, FFN, SEQ, MB, LAYERS = 2048, 16, 8192, 2048, 4, 6
+# HBM (L2-miss) bytes per GEMM launch of one stage step, from the FETCH_SIZE /
+# WRITE_SIZE counter runs (each scaled by what it reads for a 1 GiB copy:
+# 2.0 and 1.0) recorded in profiles/gemm_traffic_stage_step_gpt1p3b.md; the
+# algorithmic bytes (A + B + C, plus the fp32 main_grad read and write of a
+# weight gradient) of the same launches for comparison
+GEMM_TRAFFIC_BYTES_PER_LAUNCH = 420.1e6
+GEMM_ALGORITHMIC_BYTES_PER_LAUNCH = 184.5e6
 
 
 def step_flops(layers=LAYERS, s=SEQ, b=MB, h=H, f=FFN):
@@ -232,6 +239,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-hbm-path", action="store_true")
     ap.add_argument("--no-first-last", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="after the timed steps, copy 1 GiB once (the calibration kernel of the "
+                         "FETCH_SIZE / WRITE_SIZE counter runs behind roofline.traffic)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: every GPU box of this build has a single MI355X and no "
@@ -299,13 +309,22 @@ def main():
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": gemm_tflops / PEAK_BF16_TFLOPS,
-            "traffic": None,
+            "traffic": GEMM_TRAFFIC_BYTES_PER_LAUNCH,
+            "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)",
+            "algorithmic_bytes_per_launch": GEMM_ALGORITHMIC_BYTES_PER_LAUNCH,
             "launches": len(meter.events),
             "gemm_ms_per_step": gemm_ms / args.steps,
         },
     }
     del tr, out, dx
     torch.cuda.empty_cache()
+    if args.copy_probe:
+        src = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     if not args.no_hbm_path:
         result["hbm_path"] = hbm_path(torch)
     if not args.no_first_last:
