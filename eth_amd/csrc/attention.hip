@@ -74,6 +74,7 @@ __device__ __forceinline__ int acc_row(int r, int h) { return (r >> 2) * 8 + h *
 struct AttnTensor {
   const uint16_t* p;
   int64_t ss, sb, sh;  // strides of sequence, batch, head (elements); dim contiguous
+  uint32_t bytes;      // extent from p (buffer-load range)
 };
 struct AttnOut {
   uint16_t* p;
@@ -129,6 +130,59 @@ struct RowTile {
 };
 
 
+// ROWS x D tile of a strided tensor through buffer loads: each thread's
+// offsets within the (batch, head) slice are fixed, the row advance is a
+// scalar offset, so a load costs no address arithmetic.  Stored into LDS
+// rows of LROW elements, row index optionally swizzled (SWZ).
+typedef __amdgpu_buffer_rsrc_t a_rsrc_t;
+template <int ROWS, int D, int LROW, bool SWZ>
+struct BufTile {
+  static constexpr int CPR = D / 8;
+  static constexpr int CPT = ROWS * CPR / kAttnThreads;
+  static_assert(ROWS * CPR % kAttnThreads == 0 && CPT >= 1, "tile split");
+  a_u32x4 v[CPT];
+  int32_t voff[CPT];
+  a_rsrc_t rs;
+  int32_t row_bytes;
+  __device__ __forceinline__ void init(const AttnTensor& t, int b, int h) {
+    rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(t.p), (short)0, (int)t.bytes, 0x00020000);
+    row_bytes = (int32_t)(t.ss * 2);
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int c = threadIdx.x + i * kAttnThreads;
+      voff[i] = (int32_t)(((int64_t)b * t.sb + (int64_t)h * t.sh + (int64_t)(c / CPR) * t.ss + (c % CPR) * 8) * 2);
+    }
+  }
+  __device__ __forceinline__ void load(int r0) {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) v[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff[i], r0 * row_bytes, 0);
+  }
+  __device__ __forceinline__ void store(uint16_t* lds) const {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int c = threadIdx.x + i * kAttnThreads;
+      const int r = SWZ ? swz(c / CPR) : c / CPR;
+      *reinterpret_cast<a_u32x4*>(lds + r * LROW + (c % CPR) * 8) = v[i];
+    }
+  }
+};
+
+typedef short a_s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) a_s16x4 a_lds_s16x4;
+typedef uint32_t a_u32x2 __attribute__((ext_vector_type(2)));
+// MFMA operand of 8 consecutive k from a [k][m] LDS tile (row length LROW)
+// by two ds_read_b64_tr_b16: lane l passes the address of k-row
+// k0 + (l%16)/4 (k0 = 8*(l/32)), element m0 + 16*((l/16)%2) + 4*(l%4)
+// (tr_lane gives that offset) and receives m = m0 + l%32, k = k0..k0+7.
+__device__ __forceinline__ int tr_lane(int lane, int lrow) {
+  return ((lane >> 5) * 8 + ((lane & 15) >> 2)) * lrow + ((lane >> 4) & 1) * 16 + (lane & 3) * 4;
+}
+__device__ __forceinline__ uint4 tr_frag(const uint16_t* p, int lrow) {
+  const a_u32x2 lo = __builtin_bit_cast(a_u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((a_lds_s16x4*)p));
+  const a_u32x2 hi = __builtin_bit_cast(a_u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((a_lds_s16x4*)(p + 4 * lrow)));
+  return make_uint4(lo.x, lo.y, hi.x, hi.y);
+}
+
 // ROWS x D tile stored transposed into LDS [D][ROWS+8] (natural row order).
 // The 4-row group index varies fastest across lanes, so a wavefront's 8-byte
 // LDS writes land in distinct banks (LDS rows 8 apart alias).
@@ -180,8 +234,11 @@ template <int D, bool FP16>
 __global__ void __launch_bounds__(kAttnThreads, 2) attn_fwd_kernel(AttnArgs a) {
   constexpr int KS = D / 16;  // k-steps over the head dim
   constexpr int DT = D / 32;  // 32-row tiles over the head dim
+  // K rows swizzled (see the file comment); V rows as they are, padded to
+  // D + 32 so the transposing reads of O^T = V^T P^T hit distinct banks
+  constexpr int VL = D + 32;
   __shared__ __attribute__((aligned(16))) uint16_t Ks[2][kBKV * (D + 8)];
-  __shared__ __attribute__((aligned(16))) uint16_t Vt[2][D * (kBKV + 8)];
+  __shared__ __attribute__((aligned(16))) uint16_t Vs[2][kBKV * VL];
 
   const int BH = a.B * a.H, nqb = a.S / kBQ;
   const int bh = blockIdx.x % BH, qb = nqb - 1 - blockIdx.x / BH;
@@ -205,20 +262,23 @@ __global__ void __launch_bounds__(kAttnThreads, 2) attn_fwd_kernel(AttnArgs a) {
   float m = -1e30f, l = 0.f;  // running max (log2 units) and sum for query q
 
   const int nkv = (qb * kBQ + kBQ) / kBKV;  // blocks up to the diagonal
-  RowTile<kBKV, D> kt;
-  ColTile<kBKV, D> vt;
-  kt.load(a.k, 0, b, h);
-  vt.load(a.v, 0, b, h);
-  kt.template store<true>(Ks[0]);
-  vt.store(Vt[0]);
+  BufTile<kBKV, D, D + 8, true> kt;
+  BufTile<kBKV, D, VL, false> vt;
+  kt.init(a.k, b, h);
+  vt.init(a.v, b, h);
+  kt.load(0);
+  vt.load(0);
+  kt.store(Ks[0]);
+  vt.store(Vs[0]);
+  const int vtr = tr_lane(lane, VL);
   __syncthreads();
 
   for (int j = 0; j < nkv; ++j) {
     const int st = j & 1;
     const bool more = j + 1 < nkv;
     if (more) {
-      kt.load(a.k, (j + 1) * kBKV, b, h);
-      vt.load(a.v, (j + 1) * kBKV, b, h);
+      kt.load((j + 1) * kBKV);
+      vt.load((j + 1) * kBKV);
     }
     const int kv0 = j * kBKV;
     if (kv0 <= q0 + 31) {  // wave has at least one unmasked key in the block
@@ -272,15 +332,14 @@ __global__ void __launch_bounds__(kAttnThreads, 2) attn_fwd_kernel(AttnArgs a) {
         const int t = kk >> 1, e0 = (kk & 1) * 8;
         const uint4 pb = make_uint4(pack2<FP16>(s[t][e0 + 0], s[t][e0 + 1]), pack2<FP16>(s[t][e0 + 2], s[t][e0 + 3]),
                                     pack2<FP16>(s[t][e0 + 4], s[t][e0 + 5]), pack2<FP16>(s[t][e0 + 6], s[t][e0 + 7]));
-        const uint16_t* vp = Vt[st] + (lane & 31) * (kBKV + 8) + kk * 16 + hl * 8;
+        const uint16_t* vp = Vs[st] + vtr + kk * 16 * VL;
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
-          o[dt] = mma<FP16>(*reinterpret_cast<const uint4*>(vp + dt * 32 * (kBKV + 8)), pb, o[dt]);
+        for (int dt = 0; dt < DT; ++dt) o[dt] = mma<FP16>(tr_frag(vp + dt * 32, VL), pb, o[dt]);
       }
     }
     if (more) {
-      kt.template store<true>(Ks[st ^ 1]);
-      vt.store(Vt[st ^ 1]);
+      kt.store(Ks[st ^ 1]);
+      vt.store(Vs[st ^ 1]);
     }
     __syncthreads();
   }
@@ -549,12 +608,15 @@ static int attn_check(const eth_attn_desc_t* d) {
   return ETH_OK;
 }
 
-static AttnTensor tin(const void* p, const int64_t* st) {
+static AttnTensor tin(const void* p, const int64_t* st, const eth_attn_desc_t* d) {
   AttnTensor t;
   t.p = (const uint16_t*)p;
   t.ss = st[0];
   t.sb = st[1];
   t.sh = st[2];
+  const int64_t extent = ((int64_t)(d->seq - 1) * st[0] + (int64_t)(d->batch - 1) * st[1] +
+                          (int64_t)(d->heads - 1) * st[2] + d->head_dim) * 2;
+  t.bytes = extent < (1LL << 31) ? (uint32_t)extent : 0u;
   return t;
 }
 static AttnOut tout(void* p, const int64_t* st) {
@@ -578,10 +640,11 @@ extern "C" int eth_attn_fwd(const eth_attn_desc_t* d, const void* q, const void*
                     aligned_rows(out, d->o_strides),
                 "eth_attn_fwd: rows must be 16-byte aligned");
   AttnArgs a{};
-  a.q = tin(q, d->q_strides);
-  a.k = tin(k, d->k_strides);
-  a.v = tin(v, d->v_strides);
+  a.q = tin(q, d->q_strides, d);
+  a.k = tin(k, d->k_strides, d);
+  a.v = tin(v, d->v_strides, d);
   a.out = tout(out, d->o_strides);
+  ETH_CHECK_ARG(a.q.bytes && a.k.bytes && a.v.bytes, "eth_attn_fwd: tensors above 2 GiB are not supported");
   a.lse = lse;
   a.B = d->batch;
   a.H = d->heads;
@@ -613,14 +676,16 @@ extern "C" int eth_attn_bwd(const eth_attn_desc_t* d, const void* q, const void*
                     aligned_rows(dv, d->dv_strides),
                 "eth_attn_bwd: rows must be 16-byte aligned");
   AttnArgs a{};
-  a.q = tin(q, d->q_strides);
-  a.k = tin(k, d->k_strides);
-  a.v = tin(v, d->v_strides);
-  a.o = tin(out, d->o_strides);
-  a.dout = tin(dout, d->do_strides);
+  a.q = tin(q, d->q_strides, d);
+  a.k = tin(k, d->k_strides, d);
+  a.v = tin(v, d->v_strides, d);
+  a.o = tin(out, d->o_strides, d);
+  a.dout = tin(dout, d->do_strides, d);
   a.dq = tout(dq, d->dq_strides);
   a.dk = tout(dk, d->dk_strides);
   a.dv = tout(dv, d->dv_strides);
+  ETH_CHECK_ARG(a.q.bytes && a.k.bytes && a.v.bytes && a.o.bytes && a.dout.bytes,
+                "eth_attn_bwd: tensors above 2 GiB are not supported");
   a.lse = (float*)lse;
   a.delta = delta;
   a.B = d->batch;
