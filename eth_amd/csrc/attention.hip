@@ -19,7 +19,13 @@
 // mirror image (S = Q K^T, lane = key, query rows swizzled); dQ has its own
 // kernel (recomputing P), so no atomics are needed and results are
 // deterministic.  The dQ kernel runs first and also writes
-// delta = rowsum(dO * O), which the dK/dV kernel reads.  Softmax runs in fp32 base-2 (exp2) with the scale folded.
+// delta = rowsum(dO * O), which the dK/dV kernels read.
+//
+// Tiles arrive through buffer loads (fixed per-thread offsets, a scalar row
+// advance).  Operands that an MFMA needs transposed (V for O^T = V^T P^T, K
+// for dQ^T = K^T dS^T, Q and dO for dK and dV) are kept in LDS in natural
+// row order, padded to D + 32 so four k-rows fall in distinct banks, and
+// read with ds_read_b64_tr_b16.  Softmax runs in fp32 base-2 (exp2) with the scale folded.
 #include "common.h"
 
 namespace eth {
@@ -104,32 +110,6 @@ __device__ __forceinline__ uint16_t* row_ptr(const AttnOut& t, int s, int b, int
   return t.p + (int64_t)s * t.ss + (int64_t)b * t.sb + (int64_t)h * t.sh;
 }
 
-// ROWS x D tile, rows r0.., into LDS [ROWS][D+8], row index optionally swizzled.
-template <int ROWS, int D>
-struct RowTile {
-  static constexpr int CPR = D / 8;
-  static constexpr int CPT = ROWS * CPR / kAttnThreads;
-  static_assert(ROWS * CPR % kAttnThreads == 0 && CPT >= 1, "tile split");
-  a_u32x4 v[CPT];  // native vectors: plain loads/stores, no struct copies
-  __device__ __forceinline__ void load(const AttnTensor& t, int r0, int b, int h) {
-#pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      const int c = threadIdx.x + i * kAttnThreads;
-      v[i] = *reinterpret_cast<const a_u32x4*>(row_ptr(t, r0 + c / CPR, b, h) + (c % CPR) * 8);
-    }
-  }
-  template <bool SWZ>
-  __device__ __forceinline__ void store(uint16_t* lds) const {
-#pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      const int c = threadIdx.x + i * kAttnThreads;
-      const int r = SWZ ? swz(c / CPR) : c / CPR;
-      *reinterpret_cast<a_u32x4*>(lds + r * (D + 8) + (c % CPR) * 8) = v[i];
-    }
-  }
-};
-
-
 // ROWS x D tile of a strided tensor through buffer loads: each thread's
 // offsets within the (batch, head) slice are fixed, the row advance is a
 // scalar offset, so a load costs no address arithmetic.  Stored into LDS
@@ -165,6 +145,15 @@ struct BufTile {
       *reinterpret_cast<a_u32x4*>(lds + r * LROW + (c % CPR) * 8) = v[i];
     }
   }
+  // the same rows in natural order into [ROWS][L2] (for transposing reads)
+  template <int L2>
+  __device__ __forceinline__ void store_natural(uint16_t* lds) const {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int c = threadIdx.x + i * kAttnThreads;
+      *reinterpret_cast<a_u32x4*>(lds + (c / CPR) * L2 + (c % CPR) * 8) = v[i];
+    }
+  }
 };
 
 typedef short a_s16x4 __attribute__((ext_vector_type(4)));
@@ -182,49 +171,6 @@ __device__ __forceinline__ uint4 tr_frag(const uint16_t* p, int lrow) {
   const a_u32x2 hi = __builtin_bit_cast(a_u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((a_lds_s16x4*)(p + 4 * lrow)));
   return make_uint4(lo.x, lo.y, hi.x, hi.y);
 }
-
-// ROWS x D tile stored transposed into LDS [D][ROWS+8] (natural row order).
-// The 4-row group index varies fastest across lanes, so a wavefront's 8-byte
-// LDS writes land in distinct banks (LDS rows 8 apart alias).
-template <int ROWS, int D>
-struct ColTile {
-  static constexpr int DG = D / 8, RG = ROWS / 4;
-  static constexpr int NB = DG * RG;
-  static constexpr int BPT = (NB + kAttnThreads - 1) / kAttnThreads;
-  static_assert(NB % kAttnThreads == 0 || NB < kAttnThreads, "tile split");
-  a_u32x4 v[BPT][4];  // element vectors: word p of row j is v[i][j][p]
-  __device__ __forceinline__ void load(const AttnTensor& t, int r0, int b, int h) {
-#pragma unroll
-    for (int i = 0; i < BPT; ++i) {
-      const int blk = threadIdx.x + i * kAttnThreads;
-      if (NB % kAttnThreads != 0 && blk >= NB) break;
-      const int rg = blk % RG, dg = blk / RG;
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        v[i][j] = *reinterpret_cast<const a_u32x4*>(row_ptr(t, r0 + rg * 4 + j, b, h) + dg * 8);
-    }
-  }
-  __device__ __forceinline__ void store(uint16_t* lds) const {
-#pragma unroll
-    for (int i = 0; i < BPT; ++i) {
-      const int blk = threadIdx.x + i * kAttnThreads;
-      if (NB % kAttnThreads != 0 && blk >= NB) break;
-      const int rg = blk % RG, dg = blk / RG;
-#pragma unroll
-      for (int p = 0; p < 4; ++p) {
-        const uint32_t w0 = v[i][0][p], w1 = v[i][1][p], w2 = v[i][2][p], w3 = v[i][3][p];
-        uint2 lo, hi;
-        lo.x = (w0 & 0xffffu) | (w1 << 16);
-        lo.y = (w2 & 0xffffu) | (w3 << 16);
-        hi.x = (w0 >> 16) | (w1 & 0xffff0000u);
-        hi.y = (w2 >> 16) | (w3 & 0xffff0000u);
-        uint16_t* row = lds + (dg * 8 + 2 * p) * (ROWS + 8) + rg * 4;
-        *reinterpret_cast<uint2*>(row) = lo;
-        *reinterpret_cast<uint2*>(row + (ROWS + 8)) = hi;
-      }
-    }
-  }
-};
 
 // ------------------------------------------------------------------ forward --
 // 4 waves x 32 queries; K/V blocks of 64 keys double-buffered in LDS (the
@@ -366,10 +312,14 @@ template <int D, bool FP16, int PART>
 __global__ void __launch_bounds__(kAttnThreads, PART == 3 ? 1 : 2) attn_bwd_dkdv_kernel(AttnArgs a) {
   constexpr int KS = D / 16, DT = D / 32;
   constexpr bool DV = PART & 1, DK = PART & 2;
+  // Q (and dO) rows swizzled for S (and dP); the B operands of dV += P^T dO
+  // and dK += dS^T Q come from natural-order copies padded to D + 32
+  // through transposing reads
+  constexpr int QN = D + 32;
   __shared__ __attribute__((aligned(16))) uint16_t Qs[kBQ2 * (D + 8)];
   __shared__ __attribute__((aligned(16))) uint16_t dOs[DK ? kBQ2 * (D + 8) : 8];
-  __shared__ __attribute__((aligned(16))) uint16_t Qt[DK ? D * (kBQ2 + 8) : 8];
-  __shared__ __attribute__((aligned(16))) uint16_t dOt[DV ? D * (kBQ2 + 8) : 8];
+  __shared__ __attribute__((aligned(16))) uint16_t Qn[DK ? kBQ2 * QN : 8];
+  __shared__ __attribute__((aligned(16))) uint16_t dOn[DV ? kBQ2 * QN : 8];
   __shared__ float lse_s[kBQ2], del_s[kBQ2];
 
   const int BH = a.B * a.H;
@@ -395,29 +345,22 @@ __global__ void __launch_bounds__(kAttnThreads, PART == 3 ? 1 : 2) attn_bwd_dkdv
 #pragma unroll
     for (int r = 0; r < 16; ++r) dk[t][r] = dv[t][r] = 0.f;
 
-  RowTile<kBQ2, D> qrow, drow;
-  ColTile<kBQ2, D> qcol, dcol;
+  BufTile<kBQ2, D, D + 8, true> qt, dt;
+  qt.init(a.q, b, h);
+  dt.init(a.dout, b, h);
+  const int qtr = tr_lane(lane, QN);
   const int first = (kb * kBKV2) / kBQ2, nq = a.S / kBQ2;
   for (int qb = first; qb < nq; ++qb) {
     const int qs0 = qb * kBQ2;
-    // tiles are staged one at a time (few registers live beside the
-    // accumulators and K, V fragments)
-    qrow.load(a.q, qs0, b, h);
+    qt.load(qs0);
+    dt.load(qs0);
     __syncthreads();  // previous step's LDS readers are done
-    qrow.template store<true>(Qs);
+    qt.store(Qs);
     if constexpr (DK) {
-      __builtin_amdgcn_sched_barrier(0);
-      drow.load(a.dout, qs0, b, h);
-      drow.template store<true>(dOs);
-      __builtin_amdgcn_sched_barrier(0);
-      qcol.load(a.q, qs0, b, h);
-      qcol.store(Qt);
+      qt.template store_natural<QN>(Qn);
+      dt.store(dOs);
     }
-    if constexpr (DV) {
-      __builtin_amdgcn_sched_barrier(0);
-      dcol.load(a.dout, qs0, b, h);
-      dcol.store(dOt);
-    }
+    if constexpr (DV) dt.template store_natural<QN>(dOn);
     if (threadIdx.x < kBQ2) {
       lse_s[threadIdx.x] = a.lse[(int64_t)bh * a.S + qs0 + threadIdx.x];
       if constexpr (DK) del_s[threadIdx.x] = a.delta[(int64_t)bh * a.S + qs0 + threadIdx.x];
@@ -454,18 +397,16 @@ __global__ void __launch_bounds__(kAttnThreads, PART == 3 ? 1 : 2) attn_bwd_dkdv
         if constexpr (DV) {
           const uint4 pa = make_uint4(pack2<FP16>(s[e0 + 0], s[e0 + 1]), pack2<FP16>(s[e0 + 2], s[e0 + 3]),
                                       pack2<FP16>(s[e0 + 4], s[e0 + 5]), pack2<FP16>(s[e0 + 6], s[e0 + 7]));
-          const uint16_t* dop = dOt + (lane & 31) * (kBQ2 + 8) + kk * 16 + hl * 8;
+          const uint16_t* dop = dOn + qtr + kk * 16 * QN;
 #pragma unroll
-          for (int dt = 0; dt < DT; ++dt)
-            dv[dt] = mma<FP16>(pa, *reinterpret_cast<const uint4*>(dop + dt * 32 * (kBQ2 + 8)), dv[dt]);
+          for (int d2 = 0; d2 < DT; ++d2) dv[d2] = mma<FP16>(pa, tr_frag(dop + d2 * 32, QN), dv[d2]);
         }
         if constexpr (DK) {
           const uint4 sa = make_uint4(pack2<FP16>(dp[e0 + 0], dp[e0 + 1]), pack2<FP16>(dp[e0 + 2], dp[e0 + 3]),
                                       pack2<FP16>(dp[e0 + 4], dp[e0 + 5]), pack2<FP16>(dp[e0 + 6], dp[e0 + 7]));
-          const uint16_t* qtp = Qt + (lane & 31) * (kBQ2 + 8) + kk * 16 + hl * 8;
+          const uint16_t* qtp = Qn + qtr + kk * 16 * QN;
 #pragma unroll
-          for (int dt = 0; dt < DT; ++dt)
-            dk[dt] = mma<FP16>(sa, *reinterpret_cast<const uint4*>(qtp + dt * 32 * (kBQ2 + 8)), dk[dt]);
+          for (int d2 = 0; d2 < DT; ++d2) dk[d2] = mma<FP16>(sa, tr_frag(qtp + d2 * 32, QN), dk[d2]);
         }
       }
     }
@@ -486,9 +427,12 @@ __global__ void __launch_bounds__(kAttnThreads, PART == 3 ? 1 : 2) attn_bwd_dkdv
 template <int D, bool FP16>
 __global__ void __launch_bounds__(kAttnThreads, 2) attn_bwd_dq_kernel(AttnArgs a) {
   constexpr int KS = D / 16, DT = D / 32;
+  // K and V rows swizzled for S^T and dP^T; K also in natural order, padded
+  // to D + 32, for the transposing reads of dQ^T = K^T dS^T
+  constexpr int KN = D + 32;
   __shared__ __attribute__((aligned(16))) uint16_t Ks[kBKV * (D + 8)];
   __shared__ __attribute__((aligned(16))) uint16_t Vs[kBKV * (D + 8)];
-  __shared__ __attribute__((aligned(16))) uint16_t Kt[D * (kBKV + 8)];
+  __shared__ __attribute__((aligned(16))) uint16_t Kn[kBKV * KN];
 
   const int BH = a.B * a.H, nqb = a.S / kBQ;
   const int bh = blockIdx.x % BH, qb = nqb - 1 - blockIdx.x / BH;
@@ -534,18 +478,19 @@ __global__ void __launch_bounds__(kAttnThreads, 2) attn_bwd_dq_kernel(AttnArgs a
 #pragma unroll
     for (int r = 0; r < 16; ++r) dq[t][r] = 0.f;
 
-  RowTile<kBKV, D> krow, vrow;
-  ColTile<kBKV, D> kcol;
+  BufTile<kBKV, D, D + 8, true> kt, vt;
+  kt.init(a.k, b, h);
+  vt.init(a.v, b, h);
+  const int ktr = tr_lane(lane, KN);
   const int nkv = (qb * kBQ + kBQ) / kBKV;
   for (int j = 0; j < nkv; ++j) {
     const int kv0 = j * kBKV;
-    krow.load(a.k, kv0, b, h);
-    vrow.load(a.v, kv0, b, h);
-    kcol.load(a.k, kv0, b, h);
+    kt.load(kv0);
+    vt.load(kv0);
     __syncthreads();
-    krow.template store<true>(Ks);
-    vrow.template store<true>(Vs);
-    kcol.store(Kt);
+    kt.store(Ks);
+    kt.template store_natural<KN>(Kn);
+    vt.store(Vs);
     __syncthreads();
     if (kv0 > q0 + 31) continue;
     const bool diag = kv0 + kBKV - 1 > q0;
@@ -574,10 +519,9 @@ __global__ void __launch_bounds__(kAttnThreads, 2) attn_bwd_dq_kernel(AttnArgs a
         const int kk = t * 2 + k2, e0 = k2 * 8;
         const uint4 sb = make_uint4(pack2<FP16>(dp[e0 + 0], dp[e0 + 1]), pack2<FP16>(dp[e0 + 2], dp[e0 + 3]),
                                     pack2<FP16>(dp[e0 + 4], dp[e0 + 5]), pack2<FP16>(dp[e0 + 6], dp[e0 + 7]));
-        const uint16_t* ktp = Kt + (lane & 31) * (kBKV + 8) + kk * 16 + hl * 8;
+        const uint16_t* ktp = Kn + ktr + kk * 16 * KN;
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
-          dq[dt] = mma<FP16>(*reinterpret_cast<const uint4*>(ktp + dt * 32 * (kBKV + 8)), sb, dq[dt]);
+        for (int dt = 0; dt < DT; ++dt) dq[dt] = mma<FP16>(tr_frag(ktp + dt * 32, KN), sb, dq[dt]);
       }
     }
   }
