@@ -350,10 +350,11 @@ __global__ void __launch_bounds__(kAttnThreads, PART == 3 ? 1 : 2) attn_bwd_dkdv
   dt.init(a.dout, b, h);
   const int qtr = tr_lane(lane, QN);
   const int first = (kb * kBKV2) / kBQ2, nq = a.S / kBQ2;
+  // the next step's Q / dO rows are loaded while this step computes
+  qt.load(first * kBQ2);
+  dt.load(first * kBQ2);
   for (int qb = first; qb < nq; ++qb) {
     const int qs0 = qb * kBQ2;
-    qt.load(qs0);
-    dt.load(qs0);
     __syncthreads();  // previous step's LDS readers are done
     qt.store(Qs);
     if constexpr (DK) {
@@ -366,6 +367,10 @@ __global__ void __launch_bounds__(kAttnThreads, PART == 3 ? 1 : 2) attn_bwd_dkdv
       if constexpr (DK) del_s[threadIdx.x] = a.delta[(int64_t)bh * a.S + qs0 + threadIdx.x];
     }
     __syncthreads();
+    if (qb + 1 < nq) {
+      qt.load(qs0 + kBQ2);
+      dt.load(qs0 + kBQ2);
+    }
     if (qs0 + kBQ2 - 1 < k0) continue;  // every query of the step precedes this wave's keys
     const bool diag = qs0 < k0 + 31;
     // one 32-query tile at a time: S = Q K^T and dP = dO V^T (lane = key),
