@@ -488,15 +488,20 @@ __global__ void __launch_bounds__(kAttnThreads, 2) attn_bwd_dq_kernel(AttnArgs a
   vt.init(a.v, b, h);
   const int ktr = tr_lane(lane, KN);
   const int nkv = (qb * kBQ + kBQ) / kBKV;
+  // the next block's K / V rows are loaded while this block computes
+  kt.load(0);
+  vt.load(0);
   for (int j = 0; j < nkv; ++j) {
     const int kv0 = j * kBKV;
-    kt.load(kv0);
-    vt.load(kv0);
     __syncthreads();
     kt.store(Ks);
     kt.template store_natural<KN>(Kn);
     vt.store(Vs);
     __syncthreads();
+    if (j + 1 < nkv) {
+      kt.load(kv0 + kBKV);
+      vt.load(kv0 + kBKV);
+    }
     if (kv0 > q0 + 31) continue;
     const bool diag = kv0 + kBKV - 1 > q0;
     // one 32-key tile at a time: S^T = K Q^T, dP^T = V dO^T (lane = query),
