@@ -66,6 +66,9 @@ SIGNATURES = {
     "eth_bias_dropout_add_fwd": [_P, _P, _P, _P, _I64, _I64, _F32, ctypes.c_uint64, _I32, _P],
     "eth_dropout_bwd": [_P, _P, _I64, _I64, _F32, ctypes.c_uint64, _I32, _P],
     "eth_col_sum": [_P, _I64, _I64, _I64, _P, _P, _I32, _I32, _P],
+    "eth_ln_bwd_residual": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I32, _I32, _P],
+    "eth_bias_gelu_bwd_dbias": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I32, _I32, _P],
+    "eth_reduce_partials": [_P, _I64, _I64, _I64, _P, _I32, _P],
 }
 SIGNATURES["eth_embedding_fwd"] = [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _I32, _P]
 SIGNATURES["eth_embedding_bwd"] = [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I32, _P]
@@ -99,6 +102,8 @@ class AttnDesc(ctypes.Structure):
 # functions returning a value instead of a status
 VALUE_SIGNATURES = {
     "eth_ln_bwd_workspace": ([_I64, _I64], _I64),
+    "eth_ln_bwd_groups": ([_I64, _I64], _I64),
+    "eth_bias_gelu_bwd_workspace": ([_I64, _I64], _I64),
     "eth_col_sum_workspace": ([_I64, _I64], _I64),
     "eth_gemm_splitk_workspace": ([_I64, _I64, _I32], _I64),
 }

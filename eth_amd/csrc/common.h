@@ -49,12 +49,30 @@ __device__ __forceinline__ uint32_t f2bf_pair(float lo, float hi) {
   const eth_f32x2_t v = {lo, hi};
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, eth_bf16x2_t));
 }
+// two floats -> packed fp16 pair (lo in bits 0-15), each rounded to nearest
+// even from its fp32 value.  The empty asm pins the fp32 values in
+// registers: otherwise the compiler may fold the multiply that produced them
+// into a mixed-precision fma with a +0 addend (v_fma_mixlo_f16), which
+// rounds the exact product once and turns a -0 product into +0.
+typedef _Float16 eth_f16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t f2h_pair(float lo, float hi) {
+  eth_f32x2_t v = {lo, hi};
+  asm volatile("" : "+v"(v));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, eth_f16x2_t));
+}
+// the same rounding for one value, returned as fp32
+__device__ __forceinline__ float round_to_f16(float f) {
+  asm volatile("" : "+v"(f));
+  return (float)(_Float16)f;
+}
 __device__ __forceinline__ float bf2f(bf16_t h) {
   return __uint_as_float(((uint32_t)h) << 16);
 }
+// float -> fp16 bits, rounded to nearest even from the fp32 value (pinned
+// in a register for the reason given at f2h_pair)
 __device__ __forceinline__ uint16_t f2h_bits(float f) {
-  f16_t h = (f16_t)f;
-  return *reinterpret_cast<uint16_t*>(&h);
+  asm volatile("" : "+v"(f));
+  return __builtin_bit_cast(uint16_t, (f16_t)f);
 }
 __device__ __forceinline__ float h2f_bits(uint16_t b) {
   f16_t h = *reinterpret_cast<f16_t*>(&b);
@@ -101,11 +119,13 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
   return t;
 }
 
-// out[c] (+)= sum_g part[g*ld + c] for c < cols: 32 columns per workgroup,
-// 8 lanes of groups per column, fixed summation order (deterministic).
+// out[c] (+)= sum_g part[g*ld + c] for c < cols (cols % 4 == 0, part and ld
+// 16-byte aligned): 64 columns per workgroup, one round trip of float4 loads
+// per lane, fixed summation order (deterministic).  With gridDim.y == 2 the
+// second slab (columns [cols, 2 cols) of each partial row) goes to out1.
 __global__ void reduce_partials_kernel(const float* __restrict__ part, int groups, int cols, int64_t ld,
-                                       float* __restrict__ out, int accumulate);
-inline dim3 reduce_partials_grid(int cols) { return dim3((cols + 31) / 32); }
+                                       float* __restrict__ out0, float* __restrict__ out1, int accumulate);
+inline dim3 reduce_partials_grid(int cols, int slabs = 1) { return dim3((cols + 63) / 64, slabs); }
 constexpr int kReducePartialsThreads = 256;
 
 inline int dtype_size(int dtype) { return dtype == ETH_F32 ? 4 : 2; }

@@ -16,6 +16,11 @@
 // All kernels stream 16-byte vectors (8 x 16-bit) and compute in fp32.
 #include "common.h"
 
+// Only fused multiply-adds written as __builtin_fmaf are fused, so that every
+// kernel computing the same element (bias_gelu_bwd_kernel and the fused
+// bias-gradient variant) rounds it alike.
+#pragma clang fp contract(off)
+
 namespace eth {
 
 template <bool FP16>
@@ -36,18 +41,18 @@ constexpr float kKappa = 0.044715f;
 // kernels VALU-bound.
 __device__ __forceinline__ float fast_tanh(float u) {
   const float e = __builtin_amdgcn_exp2f(u * 2.8853900817779268f);  // 2 / ln 2
-  return 1.0f - 2.0f * __builtin_amdgcn_rcpf(1.0f + e);
+  return __builtin_fmaf(-2.0f, __builtin_amdgcn_rcpf(1.0f + e), 1.0f);
 }
 __device__ __forceinline__ float gelu_tanh(float x) {
   const float x3 = x * x * x;
-  const float inner = kBeta * (x + kKappa * x3);
+  const float inner = kBeta * __builtin_fmaf(kKappa, x3, x);
   return 0.5f * x * (1.0f + fast_tanh(inner));
 }
 __device__ __forceinline__ float gelu_tanh_grad(float x) {
   const float x2 = x * x;
-  const float t = fast_tanh(kBeta * (x + kKappa * (x2 * x)));
+  const float t = fast_tanh(kBeta * __builtin_fmaf(kKappa, x2 * x, x));
   const float left = 0.5f * x, right = 1.0f + t;
-  return 0.5f * right + left * (1.0f - t * t) * kBeta * (1.0f + 3.0f * kKappa * x2);
+  return __builtin_fmaf(0.5f, right, left * __builtin_fmaf(-t, t, 1.0f) * kBeta * __builtin_fmaf(3.0f * kKappa, x2, 1.0f));
 }
 
 // 32-bit mix of (seed, index): keep decision for dropout.
@@ -161,27 +166,168 @@ __global__ void __launch_bounds__(kEwThreads) dropout_bwd_kernel(const uint16_t*
   }
 }
 
-// Column sums: workgroup g handles rows [g*rpg, (g+1)*rpg) for a 2048-column
-// slab (256 threads x 8 columns); partials to part[g][cols].
+// Column-strip kernel (column sums): workgroup (g, s) owns the 512 columns [s*512, s*512 + 512) of
+// rows [g*rpg, min(rows, (g+1)*rpg)); wave w takes rows r0+w, r0+w+4, ...,
+// kStripBatch rows per trip with every load issued first.  Each lane keeps
+// fp32 sums of its 8 columns; the 4 waves' sums are added through LDS in
+// fixed order and stored to part[g][cols], which reduce_partials_kernel
+// folds (deterministic end to end).
+constexpr int kStripWaves = 4, kStripBatch = 4;
+typedef uint32_t ew_u32x4 __attribute__((ext_vector_type(4)));
+typedef float ew_f32x4 __attribute__((ext_vector_type(4)));
+
 template <bool FP16>
-__global__ void __launch_bounds__(kEwThreads) col_sum_part_kernel(const uint16_t* __restrict__ x,
-                                                                  int64_t ld, int rows, int cols,
-                                                                  int rpg, float* __restrict__ part) {
-  const int c = (blockIdx.y * kEwThreads + threadIdx.x) * 8;
-  if (c >= cols) return;
+__device__ __forceinline__ float ew_half(const ew_u32x4& v, int j) {
+  const uint32_t w = v[j >> 1];
+  return cin<FP16>((uint16_t)((j & 1) ? (w >> 16) : (w & 0xffffu)));
+}
+
+__device__ __forceinline__ void strip_store(const float (&acc)[8], float* __restrict__ part_row, int cols) {
+  __shared__ float red[kStripWaves][512];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  ew_f32x4* rw = reinterpret_cast<ew_f32x4*>(&red[w][lane * 8]);
+  rw[0] = ew_f32x4{acc[0], acc[1], acc[2], acc[3]};
+  rw[1] = ew_f32x4{acc[4], acc[5], acc[6], acc[7]};
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < 512 / (64 * kStripWaves); ++k) {
+    const int e = threadIdx.x + k * 64 * kStripWaves;
+    const int c = blockIdx.y * 512 + e;
+    if (c < cols) {
+      float a = 0.f;
+#pragma unroll
+      for (int t = 0; t < kStripWaves; ++t) a += red[t][e];
+      part_row[c] = a;
+    }
+  }
+}
+
+template <bool FP16>
+__global__ void __launch_bounds__(64 * kStripWaves) col_sum_part_kernel(const uint16_t* __restrict__ x,
+                                                                        int64_t ld, int rows, int cols,
+                                                                        int rpg, float* __restrict__ part) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int c = blockIdx.y * 512 + lane * 8;
   float acc[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) acc[j] = 0.f;
   const int r0 = blockIdx.x * rpg, r1 = min(rows, r0 + rpg);
-  for (int r = r0; r < r1; ++r) {
-    uint4 xr = *reinterpret_cast<const uint4*>(x + (int64_t)r * ld + c);
-    const uint16_t* xe = reinterpret_cast<const uint16_t*>(&xr);
+  if (c < cols) {
+    const uint16_t* base = x + c;
+    int r = r0 + w;
+    for (; r + (kStripBatch - 1) * kStripWaves < r1; r += kStripBatch * kStripWaves) {
+      ew_u32x4 v[kStripBatch];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) acc[j] += cin<FP16>(xe[j]);
+      for (int b = 0; b < kStripBatch; ++b)
+        v[b] = *reinterpret_cast<const ew_u32x4*>(base + (int64_t)(r + b * kStripWaves) * ld);
+#pragma unroll
+      for (int b = 0; b < kStripBatch; ++b)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] += ew_half<FP16>(v[b], j);
+    }
+    for (; r < r1; r += kStripWaves) {
+      const ew_u32x4 v = *reinterpret_cast<const ew_u32x4*>(base + (int64_t)r * ld);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] += ew_half<FP16>(v, j);
+    }
   }
-  float* p = part + (int64_t)blockIdx.x * cols + c;
+  strip_store(acc, part + (int64_t)blockIdx.x * cols, cols);
+}
+
+// dx = dy * gelu_tanh'(bf16(x + b)) as bias_gelu_bwd_kernel, plus the column
+// sums of the stored (rounded) dx: the bias gradient.
+template <bool FP16>
+__device__ __forceinline__ ew_u32x4 gelu_bwd_vec(const ew_u32x4& d, const ew_u32x4& xv, const float (&bias)[8],
+                                                 float (&acc)[8]) {
+  ew_u32x4 o;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) p[j] = acc[j];
+  for (int j = 0; j < 8; j += 2) {
+    float v[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const float t = cin<FP16>(cout<FP16>(ew_half<FP16>(xv, j + h) + bias[j + h]));
+      v[h] = ew_half<FP16>(d, j + h) * gelu_tanh_grad(t);
+    }
+    const uint32_t w = FP16 ? f2h_pair(v[0], v[1]) : f2bf_pair(v[0], v[1]);
+    o[j >> 1] = w;
+    acc[j] += cin<FP16>((uint16_t)(w & 0xffffu));
+    acc[j + 1] += cin<FP16>((uint16_t)(w >> 16));
+  }
+  return o;
+}
+
+// Sweep mapping for the fused bias gradient: workgroup b covers the 2048
+// columns of column block b % CB (CB = ceil(cols / 2048), 8 per lane) on rows
+// g, g + G, g + 2G, ... of row lane g = b / CB, kGeluBatch rows per trip with
+// every load issued first.  The G row lanes together walk the tensor from
+// top to bottom, so the whole GPU streams through one band of rows at a
+// time; each lane's column sums go to part[g][cols].
+constexpr int kGeluBatch = 8;
+
+template <bool FP16>
+__global__ void __launch_bounds__(256) bias_gelu_bwd_dbias_kernel(
+    const uint16_t* __restrict__ dy, const uint16_t* __restrict__ x, const uint16_t* __restrict__ b,
+    uint16_t* __restrict__ dx, int rows, int cols, int lanes, float* __restrict__ part) {
+  const int cblocks = (cols + 2047) / 2048;
+  const int cb = blockIdx.x % cblocks, g = blockIdx.x / cblocks;
+  const int c = cb * 2048 + threadIdx.x * 8;
+  if (c >= cols) return;
+  float acc[8], bias[8];
+  const ew_u32x4 bv = *reinterpret_cast<const ew_u32x4*>(b + c);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    acc[j] = 0.f;
+    bias[j] = ew_half<FP16>(bv, j);
+  }
+  int r = g;
+  for (; r + (kGeluBatch - 1) * lanes < rows; r += kGeluBatch * lanes) {
+    ew_u32x4 dv[kGeluBatch], xv[kGeluBatch];
+#pragma unroll
+    for (int k = 0; k < kGeluBatch; ++k) {
+      const int64_t o = (int64_t)(r + k * lanes) * cols + c;
+      dv[k] = *reinterpret_cast<const ew_u32x4*>(dy + o);
+      xv[k] = *reinterpret_cast<const ew_u32x4*>(x + o);
+    }
+#pragma unroll
+    for (int k = 0; k < kGeluBatch; ++k) {
+      const int64_t o = (int64_t)(r + k * lanes) * cols + c;
+      *reinterpret_cast<ew_u32x4*>(dx + o) = gelu_bwd_vec<FP16>(dv[k], xv[k], bias, acc);
+    }
+  }
+  for (; r < rows; r += lanes) {
+    const int64_t o = (int64_t)r * cols + c;
+    const ew_u32x4 dv = *reinterpret_cast<const ew_u32x4*>(dy + o);
+    const ew_u32x4 xv = *reinterpret_cast<const ew_u32x4*>(x + o);
+    *reinterpret_cast<ew_u32x4*>(dx + o) = gelu_bwd_vec<FP16>(dv, xv, bias, acc);
+  }
+  ew_f32x4* p = reinterpret_cast<ew_f32x4*>(part + (int64_t)g * cols + c);
+  p[0] = ew_f32x4{acc[0], acc[1], acc[2], acc[3]};
+  p[1] = ew_f32x4{acc[4], acc[5], acc[6], acc[7]};
+}
+
+// Row lanes of the sweep: one workgroup per CU in all (measured best for the
+// [8192, 8192] MLP activation), at least kGeluBatch rows per lane.
+inline int gelu_lanes(int64_t rows, int64_t cols) {
+  const int64_t cblocks = (cols + 2047) / 2048;
+  int64_t g = 256 / cblocks;
+  const int64_t by_rows = rows / kGeluBatch;
+  if (g > by_rows) g = by_rows;
+  if (g < 1) g = 1;
+  return (int)g;
+}
+
+// Row groups of the strip kernels: about 1024 workgroups in all, at most
+// 256 groups (partials stay a few MB), at least 16 rows per group.
+inline int strip_groups(int64_t rows, int64_t cols) {
+  const int64_t slabs = (cols + 511) / 512;
+  int64_t g = 1024 / slabs;
+  if (g > 256) g = 256;
+  if (g < 64) g = 64;
+  const int64_t by_rows = (rows + 15) / 16;
+  if (g > by_rows) g = by_rows;
+  if (g < 1) g = 1;
+  const int64_t rpg = (rows + g - 1) / g;
+  return (int)((rows + rpg - 1) / rpg);
 }
 
 inline int ew_grid(int64_t nvec) {
@@ -279,27 +425,60 @@ extern "C" int eth_dropout_bwd(const void* dy, void* dx, int64_t rows, int64_t c
 }
 
 extern "C" int64_t eth_col_sum_workspace(int64_t rows, int64_t cols) {
-  const int64_t groups = rows < 512 ? (rows + 15) / 16 : 512;
-  return (groups < 1 ? 1 : groups) * cols;
+  if (rows <= 0 || cols <= 0) return 1;
+  return (int64_t)strip_groups(rows, cols) * cols;
 }
 
 extern "C" int eth_col_sum(const void* x, int64_t ld, int64_t rows, int64_t cols, float* out,
                            float* workspace, int accumulate, int dtype, void* stream) {
   ETH_EW_COMMON("eth_col_sum");
   ETH_CHECK_ARG(x && out && workspace && ld >= cols && ld % 8 == 0, "eth_col_sum: bad arguments");
-  const int groups = (int)(rows < 512 ? (rows + 15) / 16 : 512);
+  ETH_CHECK_ARG(rows < (1LL << 31) && cols < (1LL << 31), "eth_col_sum: shape too large");
+  ETH_CHECK_ARG((((uintptr_t)x | (uintptr_t)workspace) & 15u) == 0, "eth_col_sum: operands must be 16-byte aligned");
+  const int groups = strip_groups(rows, cols);
   const int rpg = (int)((rows + groups - 1) / groups);
-  dim3 grid(groups, (unsigned)((cols + 8 * kEwThreads - 1) / (8 * kEwThreads)));
+  dim3 grid(groups, (unsigned)((cols + 511) / 512));
   hipStream_t s = (hipStream_t)stream;
   if (dtype == ETH_BF16)
-    col_sum_part_kernel<false><<<grid, kEwThreads, 0, s>>>((const uint16_t*)x, ld, (int)rows, (int)cols, rpg,
-                                                           workspace);
+    col_sum_part_kernel<false><<<grid, 64 * kStripWaves, 0, s>>>((const uint16_t*)x, ld, (int)rows, (int)cols, rpg,
+                                                                 workspace);
   else
-    col_sum_part_kernel<true><<<grid, kEwThreads, 0, s>>>((const uint16_t*)x, ld, (int)rows, (int)cols, rpg,
-                                                          workspace);
+    col_sum_part_kernel<true><<<grid, 64 * kStripWaves, 0, s>>>((const uint16_t*)x, ld, (int)rows, (int)cols, rpg,
+                                                                workspace);
   ETH_CHECK_LAUNCH("eth_col_sum");
   reduce_partials_kernel<<<reduce_partials_grid((int)cols), kReducePartialsThreads, 0, s>>>(
-      workspace, groups, (int)cols, cols, out, accumulate);
+      workspace, groups, (int)cols, cols, out, nullptr, accumulate);
   ETH_CHECK_LAUNCH("eth_col_sum reduce");
+  return ETH_OK;
+}
+
+extern "C" int64_t eth_bias_gelu_bwd_workspace(int64_t rows, int64_t cols) {
+  if (rows <= 0 || cols <= 0) return 1;
+  return (int64_t)gelu_lanes(rows, cols) * cols;
+}
+
+extern "C" int eth_bias_gelu_bwd_dbias(const void* dy, const void* x, const void* bias, void* dx, float* dbias,
+                                       float* workspace, int64_t rows, int64_t cols, int accumulate, int dtype,
+                                       void* stream) {
+  ETH_EW_COMMON("eth_bias_gelu_bwd_dbias");
+  ETH_CHECK_ARG(dy && x && bias && dx && dbias && workspace, "eth_bias_gelu_bwd_dbias: null pointer");
+  ETH_CHECK_ARG(rows < (1LL << 31) && cols < (1LL << 31), "eth_bias_gelu_bwd_dbias: shape too large");
+  ETH_CHECK_ARG((((uintptr_t)dy | (uintptr_t)x | (uintptr_t)bias | (uintptr_t)dx | (uintptr_t)workspace) & 15u) == 0,
+                "eth_bias_gelu_bwd_dbias: operands must be 16-byte aligned");
+  const int lanes = gelu_lanes(rows, cols);
+  const dim3 grid((unsigned)(lanes * ((cols + 2047) / 2048)));
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == ETH_BF16)
+    bias_gelu_bwd_dbias_kernel<false><<<grid, 256, 0, s>>>((const uint16_t*)dy, (const uint16_t*)x,
+                                                           (const uint16_t*)bias, (uint16_t*)dx, (int)rows,
+                                                           (int)cols, lanes, workspace);
+  else
+    bias_gelu_bwd_dbias_kernel<true><<<grid, 256, 0, s>>>((const uint16_t*)dy, (const uint16_t*)x,
+                                                          (const uint16_t*)bias, (uint16_t*)dx, (int)rows,
+                                                          (int)cols, lanes, workspace);
+  ETH_CHECK_LAUNCH("eth_bias_gelu_bwd_dbias");
+  reduce_partials_kernel<<<reduce_partials_grid((int)cols), kReducePartialsThreads, 0, s>>>(
+      workspace, lanes, (int)cols, cols, dbias, nullptr, accumulate);
+  ETH_CHECK_LAUNCH("eth_bias_gelu_bwd_dbias reduce");
   return ETH_OK;
 }

@@ -220,23 +220,43 @@ __global__ void __launch_bounds__(1024) finalize_kernel(const double* __restrict
 
 __global__ void __launch_bounds__(kReducePartialsThreads)
     reduce_partials_kernel(const float* __restrict__ part, int groups, int cols, int64_t ld,
-                           float* __restrict__ out, int accumulate) {
-  // 32 columns x 8 group-lanes per workgroup; each lane sums every 8th group
-  __shared__ float red[8][33];
-  const int c = blockIdx.x * 32 + (threadIdx.x & 31);
-  const int lane_g = threadIdx.x >> 5;
-  float a = 0.f;
+                           float* __restrict__ out0, float* __restrict__ out1, int accumulate) {
+  // 64 columns x 16 group-lanes per workgroup: lane (q, gl) sums float4
+  // column quad q over groups gl, gl + 16, ... with four loads in flight,
+  // then the 16 group-lane sums are added in fixed order (deterministic).
+  // blockIdx.y selects the slab: 1 reads columns [cols, 2 cols) of each
+  // partial row and writes out1.
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  __shared__ f4 red[16][17];
+  const int q = threadIdx.x & 15, gl = threadIdx.x >> 4;
+  const int c = blockIdx.x * 64 + q * 4;
+  const float* src = part + (blockIdx.y ? cols : 0);
+  float* out = blockIdx.y ? out1 : out0;
+  f4 a = {0.f, 0.f, 0.f, 0.f};
   if (c < cols) {
-#pragma unroll 8
-    for (int g = lane_g; g < groups; g += 8) a += part[(int64_t)g * ld + c];
+    const f4* p = reinterpret_cast<const f4*>(src + c);
+    const int64_t ld4 = ld / 4;
+    int g = gl;
+    for (; g + 48 < groups; g += 64) {
+      const f4 v0 = p[g * ld4], v1 = p[(g + 16) * ld4], v2 = p[(g + 32) * ld4], v3 = p[(g + 48) * ld4];
+      a += v0;
+      a += v1;
+      a += v2;
+      a += v3;
+    }
+    for (; g < groups; g += 16) a += p[g * ld4];
   }
-  red[lane_g][threadIdx.x & 31] = a;
+  red[gl][q] = a;
   __syncthreads();
-  if (lane_g == 0 && c < cols) {
-    float t = 0.f;
+  if (threadIdx.x < 64) {
+    const int col = blockIdx.x * 64 + threadIdx.x;
+    if (col < cols) {
+      const int qq = threadIdx.x >> 2, e = threadIdx.x & 3;
+      float t = 0.f;
 #pragma unroll
-    for (int w = 0; w < 8; ++w) t += red[w][threadIdx.x];
-    out[c] = accumulate ? out[c] + t : t;
+      for (int w = 0; w < 16; ++w) t += red[w][qq][e];
+      out[col] = accumulate ? out[col] + t : t;
+    }
   }
 }
 
@@ -255,6 +275,19 @@ extern "C" {
 int eth_abi_version(void) { return 1; }
 
 const char* eth_last_error(void) { return g_last_error.c_str(); }
+
+int eth_reduce_partials(const float* part, int64_t groups, int64_t cols, int64_t ld, float* out, int accumulate,
+                        void* stream) {
+  ETH_CHECK_ARG(groups >= 1 && groups < (1LL << 31) && cols > 0 && cols < (1LL << 31) && cols % 4 == 0 &&
+                    ld >= cols && ld % 4 == 0,
+                "eth_reduce_partials: bad shape (groups %lld, cols %lld, ld %lld)", (long long)groups,
+                (long long)cols, (long long)ld);
+  ETH_CHECK_ARG(part && out && ((uintptr_t)part & 15u) == 0, "eth_reduce_partials: bad pointers");
+  reduce_partials_kernel<<<reduce_partials_grid((int)cols), kReducePartialsThreads, 0, (hipStream_t)stream>>>(
+      part, (int)groups, (int)cols, ld, out, nullptr, accumulate);
+  ETH_CHECK_LAUNCH("eth_reduce_partials");
+  return ETH_OK;
+}
 
 int eth_fill_f32(float* dst, int64_t n, float value, void* stream) {
   ETH_CHECK_ARG(n >= 0 && (n == 0 || dst), "eth_fill_f32: bad arguments");

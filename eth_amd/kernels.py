@@ -159,8 +159,13 @@ def layer_norm_fwd(x, gamma, beta, eps=1e-5):
     return y, mean, rstd
 
 
-def layer_norm_bwd(dy, x, mean, rstd, gamma, dgamma, dbeta, accumulate):
-    """dx (returned); dgamma/dbeta fp32 stored or accumulated in place."""
+def layer_norm_bwd(dy, x, mean, rstd, gamma, dgamma, dbeta, accumulate, dresid=None, colsum=False):
+    """dx (returned); dgamma/dbeta fp32 stored or accumulated in place.
+
+    With `dresid` (the gradient of the residual branch that read the same x)
+    the returned dx is bf16(bf16(dx_ln) + dresid).  With `colsum` as well,
+    returns (dx, part): fp32 [groups, cols] column-sum partials of dx, folded
+    by `reduce_partials` into a bias gradient."""
     code = _check_half(dy, x, gamma)
     rows, cols = _rows_cols(x)
     if dy.shape != x.shape or not dy.is_contiguous():
@@ -168,12 +173,34 @@ def layer_norm_bwd(dy, x, mean, rstd, gamma, dgamma, dbeta, accumulate):
     for t in (dgamma, dbeta):
         if t.dtype != torch.float32 or t.numel() != cols or not t.is_contiguous():
             raise ValueError("dgamma/dbeta must be contiguous fp32 [cols]")
+    if dresid is not None:
+        _check_half(dresid)
+        if dresid.dtype != x.dtype or dresid.shape != x.shape or not dresid.is_contiguous():
+            raise ValueError("dresid must be a contiguous tensor like x")
+    elif colsum:
+        raise ValueError("colsum needs dresid")
     ws = torch.empty(nat.value("eth_ln_bwd_workspace", rows, cols), dtype=torch.float32, device=x.device)
+    part = None
+    if colsum:
+        part = torch.empty(nat.value("eth_ln_bwd_groups", rows, cols), cols, dtype=torch.float32, device=x.device)
     dx = torch.empty_like(x)
-    nat.call("eth_ln_bwd", nat.ptr(dy), nat.ptr(x), nat.ptr(mean), nat.ptr(rstd), nat.ptr(gamma), nat.ptr(dx),
-             nat.ptr(dgamma), nat.ptr(dbeta), nat.ptr(ws), rows, cols, 1 if accumulate else 0, code,
+    nat.call("eth_ln_bwd_residual", nat.ptr(dy), nat.ptr(x), nat.ptr(mean), nat.ptr(rstd), nat.ptr(gamma),
+             nat.ptr(dresid), nat.ptr(dx), nat.ptr(dgamma), nat.ptr(dbeta),
+             nat.ptr(part), nat.ptr(ws), rows, cols, 1 if accumulate else 0, code,
              nat.stream_ptr(x.device))
-    return dx
+    return (dx, part) if colsum else dx
+
+
+def reduce_partials(part, out, accumulate):
+    """out[c] (+)= sum_g part[g, c] (fp32), fixed summation order."""
+    if part.dtype != torch.float32 or part.dim() != 2 or not part.is_contiguous():
+        raise ValueError("part must be contiguous fp32 [groups, cols]")
+    groups, cols = part.shape
+    if out.dtype != torch.float32 or out.numel() != cols or not out.is_contiguous():
+        raise ValueError("out must be contiguous fp32 [cols]")
+    nat.call("eth_reduce_partials", nat.ptr(part), groups, cols, cols, nat.ptr(out), 1 if accumulate else 0,
+             nat.stream_ptr(part.device))
+    return out
 
 
 # -------------------------------------------------------------- elementwise --
@@ -187,14 +214,23 @@ def bias_gelu_fwd(x, bias):
     return y
 
 
-def bias_gelu_bwd(dy, x, bias):
+def bias_gelu_bwd(dy, x, bias, dbias=None, accumulate=False):
+    """dx = dy * gelu_tanh'(x + b); with `dbias` (fp32 [cols]) the column
+    sums of dx are stored or added into it in the same pass."""
     code = _check_half(dy, x, bias)
     rows, cols = _rows_cols(x)
     if dy.shape != x.shape or not dy.is_contiguous() or bias.numel() != cols:
         raise ValueError("shape mismatch")
     dx = torch.empty_like(x)
-    nat.call("eth_bias_gelu_bwd", nat.ptr(dy), nat.ptr(x), nat.ptr(bias), nat.ptr(dx), rows, cols, code,
-             nat.stream_ptr(x.device))
+    if dbias is None:
+        nat.call("eth_bias_gelu_bwd", nat.ptr(dy), nat.ptr(x), nat.ptr(bias), nat.ptr(dx), rows, cols, code,
+                 nat.stream_ptr(x.device))
+        return dx
+    if dbias.dtype != torch.float32 or dbias.numel() != cols or not dbias.is_contiguous():
+        raise ValueError("dbias must be contiguous fp32 [cols]")
+    ws = torch.empty(nat.value("eth_bias_gelu_bwd_workspace", rows, cols), dtype=torch.float32, device=x.device)
+    nat.call("eth_bias_gelu_bwd_dbias", nat.ptr(dy), nat.ptr(x), nat.ptr(bias), nat.ptr(dx), nat.ptr(dbias),
+             nat.ptr(ws), rows, cols, 1 if accumulate else 0, code, nat.stream_ptr(x.device))
     return dx
 
 

@@ -93,9 +93,12 @@ class ParallelLayerNormOp(RopalaModule):
         hidden = input_tensors["hidden_states"]
         if self.name == "final-layernorm":
             hidden = hidden.transpose(0, 1).contiguous()
+        if not self.output_extra_tensors_info:
+            return {"hidden_states": self.input_layernorm(hidden)}
+        out, residual = self.input_layernorm.forward_with_residual(hidden)
         for key in sorted(self.output_extra_tensors_info):
-            self._publish(key, hidden, input_extra_tensors, output_extra_tensors)
-        return {"hidden_states": self.input_layernorm(hidden)}
+            self._publish(key, residual, input_extra_tensors, output_extra_tensors)
+        return {"hidden_states": out}
 
 
 class ParallelQKVOp(RopalaModule):

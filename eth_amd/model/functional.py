@@ -87,6 +87,53 @@ class LayerNormFn(torch.autograd.Function):
         return dx.view(x.shape), dg.to(gamma.dtype), db.to(beta.dtype), None
 
 
+class LayerNormResidualFn(torch.autograd.Function):
+    """MixedFusedLayerNorm whose input also feeds a later residual add:
+    returns (LayerNorm(x), x).  The second output is what the op publishes
+    as the residual (hidden_states_1/2, flex_ops.py:488-664), so both
+    gradients of x arrive in one backward call and are added inside the
+    LayerNorm backward kernel instead of by autograd's accumulation.  When x
+    was produced by an op (not a leaf), the backward also leaves the
+    column-sum partials of the returned gradient on it as
+    `_eth_colsum_part`: BiasDropoutAddFn's backward folds them into its bias
+    gradient instead of summing that gradient again."""
+
+    @staticmethod
+    def forward(ctx, x, gamma, beta, eps):
+        ctx.set_materialize_grads(False)
+        xc = x.contiguous()
+        y, mean, rstd = K.layer_norm_fwd(_flat(xc), gamma, beta, eps)
+        ctx.save_for_backward(xc, gamma, beta, mean, rstd)
+        ctx.colsum = x.grad_fn is not None
+        return y.view(x.shape), x.view_as(x)
+
+    @staticmethod
+    def backward(ctx, dy, dres):
+        x, gamma, beta, mean, rstd = ctx.saved_tensors
+        if dy is None:
+            return dres, None, None, None
+        mg_g, mg_b = _fp32_accum_target(gamma), _fp32_accum_target(beta)
+        if mg_g is not None and mg_b is not None:
+            dg, db, acc = mg_g, mg_b, True
+        else:
+            dg = torch.zeros(gamma.shape, dtype=torch.float32, device=x.device)
+            db = torch.zeros(beta.shape, dtype=torch.float32, device=x.device)
+            acc = False
+        part = None
+        if dres is None:
+            dx = K.layer_norm_bwd(_flat(dy.contiguous()), _flat(x), mean, rstd, gamma, dg, db, accumulate=acc)
+        else:
+            out = K.layer_norm_bwd(_flat(dy.contiguous()), _flat(x), mean, rstd, gamma, dg, db, accumulate=acc,
+                                   dresid=_flat(dres.contiguous()), colsum=ctx.colsum)
+            dx, part = out if ctx.colsum else (out, None)
+        dx = dx.view(x.shape)
+        if part is not None:
+            dx._eth_colsum_part = part
+        if acc:
+            return dx, None, None, None
+        return dx, dg.to(gamma.dtype), db.to(beta.dtype), None
+
+
 class BiasGeluFn(torch.autograd.Function):
     """gelu_tanh(x + b) (flex_ops.py:1882-1906)."""
 
@@ -100,16 +147,16 @@ class BiasGeluFn(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dy):
         x, bias = ctx.saved_tensors
-        dx = K.bias_gelu_bwd(_flat(dy.contiguous()), _flat(x), bias)
         db = None
         if ctx.needs_input_grad[1]:
+            # the bias gradient (column sums of dx) comes out of the same pass
             mg = _fp32_accum_target(bias)
-            if mg is not None:
-                K.col_sum(dx, mg, accumulate=True)
-            else:
-                acc = torch.zeros(bias.shape, dtype=torch.float32, device=bias.device)
-                K.col_sum(dx, acc, accumulate=False)
-                db = acc.to(bias.dtype)
+            target = mg if mg is not None else torch.empty(bias.shape, dtype=torch.float32, device=bias.device)
+            dx = K.bias_gelu_bwd(_flat(dy.contiguous()), _flat(x), bias, dbias=target, accumulate=mg is not None)
+            if mg is None:
+                db = target.to(bias.dtype)
+        else:
+            dx = K.bias_gelu_bwd(_flat(dy.contiguous()), _flat(x), bias)
         return dx.view(x.shape), db
 
 
@@ -126,17 +173,21 @@ class BiasDropoutAddFn(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dout):
         (bias,) = ctx.saved_tensors
+        part = getattr(dout, "_eth_colsum_part", None) if ctx.p == 0 else None
         dout = dout.contiguous()
         dx = K.dropout_bwd(_flat(dout), ctx.p, ctx.seed).view(dout.shape) if ctx.p > 0 else dout
         db = None
         if ctx.needs_input_grad[1]:
             mg = _fp32_accum_target(bias)
-            if mg is not None:
-                K.col_sum(_flat(dx), mg, accumulate=True)
+            target = mg if mg is not None else torch.empty(bias.shape, dtype=torch.float32, device=bias.device)
+            if part is not None:
+                # column sums already produced by the LayerNorm backward that
+                # made dout (p == 0: dx is dout)
+                K.reduce_partials(part, target, accumulate=mg is not None)
             else:
-                acc = torch.zeros(bias.shape, dtype=torch.float32, device=bias.device)
-                K.col_sum(_flat(dx), acc, accumulate=False)
-                db = acc.to(bias.dtype)
+                K.col_sum(_flat(dx), target, accumulate=mg is not None)
+            if mg is None:
+                db = target.to(bias.dtype)
         return dx, db, dout, None, None
 
 

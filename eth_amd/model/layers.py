@@ -11,7 +11,7 @@ metadata adapter reads `tensor_model_parallel`, `partition_dim` and
 import torch
 from torch import nn
 
-from .functional import LayerNormFn, LinearFn
+from .functional import LayerNormFn, LayerNormResidualFn, LinearFn
 
 _TP_ATTRS = {"tensor_model_parallel": False, "partition_dim": -1, "partition_stride": 1}
 
@@ -51,6 +51,12 @@ class LayerNorm(nn.Module):
 
     def forward(self, x):
         return LayerNormFn.apply(x, self.weight, self.bias, self.eps)
+
+    def forward_with_residual(self, x):
+        """(LayerNorm(x), x) where the second output is the residual-branch
+        copy of x: its gradient is added to the LayerNorm input gradient by
+        the backward kernel."""
+        return LayerNormResidualFn.apply(x, self.weight, self.bias, self.eps)
 
 
 class ColumnParallelLinear(nn.Module):

@@ -188,6 +188,22 @@ int64_t eth_ln_bwd_workspace(int64_t rows, int64_t cols);
 int eth_ln_bwd(const void* dy, const void* x, const float* mean, const float* rstd,
                const void* gamma, void* dx, float* dgamma, float* dbeta, float* workspace,
                int64_t rows, int64_t cols, int accumulate, int dtype, void* stream);
+/* LayerNorm backward fused with the residual branch that read the same
+ * input: dx = bf16(bf16(dx_ln) + dresid), the sum autograd forms when a
+ * tensor feeds both the LayerNorm and the later residual add
+ * (ParallelLayerNormOp publishing hidden_states_1/2, flex_ops.py:488-664,
+ * consumed by bias_dropout_add, flex_ops.py:104-134).  With colsum_part
+ * non-NULL it also stores per-row-group column sums of the stored dx,
+ * colsum_part[eth_ln_bwd_groups(rows, cols)][cols] (fp32): folded by
+ * eth_reduce_partials they are the bias gradient of the bias-dropout-add at
+ * p == 0 that produced this LayerNorm's input (the sum over the broadcast
+ * dimensions that autograd of `x + bias` forms there).  dresid == NULL is
+ * eth_ln_bwd. */
+int64_t eth_ln_bwd_groups(int64_t rows, int64_t cols);
+int eth_ln_bwd_residual(const void* dy, const void* x, const float* mean, const float* rstd,
+                        const void* gamma, const void* dresid, void* dx, float* dgamma,
+                        float* dbeta, float* colsum_part, float* workspace, int64_t rows,
+                        int64_t cols, int accumulate, int dtype, void* stream);
 
 /* ------------------------------------------------------------------------
  * Elementwise ops of the GPT block ([rows, cols] row-major, cols % 8 == 0).
@@ -212,6 +228,22 @@ int eth_dropout_bwd(const void* dy, void* dx, int64_t rows, int64_t cols, float 
 int64_t eth_col_sum_workspace(int64_t rows, int64_t cols);
 int eth_col_sum(const void* x, int64_t ld, int64_t rows, int64_t cols, float* out,
                 float* workspace, int accumulate, int dtype, void* stream);
+/* Bias-GELU backward with its bias gradient in the same pass: dx as
+ * eth_bias_gelu_bwd, and dbias (+)= column sums of the stored dx (fp32) --
+ * what ParallelMlpGeLUOp's backward (flex_ops.py:1882-1906 with
+ * model/fused_bias_gelu.py:39-45, bias grad = the same tensor as the input
+ * grad, summed by the caller) followed by eth_col_sum computes, without
+ * reading dx back.  `workspace` holds eth_bias_gelu_bwd_workspace(rows,
+ * cols) floats. */
+int64_t eth_bias_gelu_bwd_workspace(int64_t rows, int64_t cols);
+int eth_bias_gelu_bwd_dbias(const void* dy, const void* x, const void* bias, void* dx,
+                            float* dbias, float* workspace, int64_t rows, int64_t cols,
+                            int accumulate, int dtype, void* stream);
+/* out[c] (+)= sum_g part[g * ld + c] (fp32, cols % 4 == 0, ld % 4 == 0, part
+ * 16-byte aligned), summed in a fixed order: folds the column-sum partials
+ * of eth_ln_bwd_residual into a bias gradient. */
+int eth_reduce_partials(const float* part, int64_t groups, int64_t cols, int64_t ld, float* out,
+                        int accumulate, void* stream);
 
 /* ------------------------------------------------------------------------
  * Causal attention (softmax(Q K^T / sqrt(hn) + causal -inf) V per batch and

@@ -130,7 +130,7 @@ def test_gemm_rejects_bad_shapes(cuda):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("rows,cols", [(300, 256), (64, 2048), (33, 4096), (5, 8)])
+@pytest.mark.parametrize("rows,cols", [(300, 256), (64, 2048), (33, 4096), (5, 8), (40, 1536), (17, 6144), (9, 8192)])
 def test_layer_norm_fwd_bwd(cuda, dtype, rows, cols):
     announce(f"layernorm {dtype} {rows}x{cols}")
     gen = torch.Generator().manual_seed(rows + cols)
@@ -152,6 +152,59 @@ def test_layer_norm_fwd_bwd(cuda, dtype, rows, cols):
     _close(dx, xr.grad, dtype, "ln dx")
     assert torch.allclose(dg.cpu() - 1.0, gr.grad, rtol=1e-3, atol=1e-3 * gr.grad.abs().max().item())
     assert torch.allclose(db.cpu(), br.grad, rtol=1e-3, atol=1e-3 * br.grad.abs().max().item())
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("rows,cols", [(300, 256), (1000, 2048), (33, 4096), (5, 8), (40, 1536), (17, 8192)])
+def test_layer_norm_bwd_residual_colsum(cuda, dtype, rows, cols):
+    """LayerNorm backward fused with the residual gradient: dx equals the
+    plain backward's dx plus dresid, rounded as two 16-bit tensors and a
+    16-bit add (bit-exact); dgamma/dbeta equal the plain path's to fp32
+    summation-order noise; the column-sum partials fold to the fp32 column
+    sums of the returned dx."""
+    announce(f"layernorm residual {dtype} {rows}x{cols}")
+    gen = torch.Generator().manual_seed(rows * 3 + cols)
+    x = (_rand((rows, cols), dtype, gen, 2.0) + 0.5).to(cuda)
+    g = (1 + _rand((cols,), torch.float32, gen, 0.1)).to(dtype).to(cuda)
+    b = _rand((cols,), dtype, gen, 0.1).to(cuda)
+    dy = _rand((rows, cols), dtype, gen).to(cuda)
+    dres = _rand((rows, cols), dtype, gen).to(cuda)
+    _, mean, rstd = K.layer_norm_fwd(x, g, b)
+    dg0, db0 = torch.zeros(cols, device=cuda), torch.zeros(cols, device=cuda)
+    dx0 = K.layer_norm_bwd(dy, x, mean, rstd, g, dg0, db0, accumulate=False)
+    dg, db = torch.full((cols,), 2.0, device=cuda), torch.full((cols,), -1.0, device=cuda)
+    dx, part = K.layer_norm_bwd(dy, x, mean, rstd, g, dg, db, accumulate=True, dresid=dres, colsum=True)
+    assert torch.equal(dx.cpu(), (dx0 + dres).cpu())  # torch's 16-bit add: fp32 sum, one rounding
+    scale = dg0.abs().max().item() + db0.abs().max().item()
+    assert (dg - 2.0 - dg0).abs().max().item() <= 1e-5 * scale
+    assert (db + 1.0 - db0).abs().max().item() <= 1e-5 * scale
+    cs = torch.full((cols,), 0.5, device=cuda)
+    K.reduce_partials(part, cs, accumulate=True)
+    ref = 0.5 + dx.cpu().double().sum(0)
+    assert (cs.cpu().double() - ref).abs().max().item() <= 1e-5 * (ref.abs().max().item() + rows)
+    dx2 = K.layer_norm_bwd(dy, x, mean, rstd, g, dg0, db0, accumulate=False, dresid=dres)
+    assert torch.equal(dx2.cpu(), dx.cpu())
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("rows,cols", [(96, 1024), (1000, 8192), (37, 520), (3, 8)])
+def test_bias_gelu_bwd_fused_dbias(cuda, dtype, rows, cols):
+    """The fused bias gradient: dx bit-identical to the plain kernel, dbias
+    the fp32 column sums of that dx (stored, then accumulated)."""
+    announce(f"bias-gelu dbias {dtype} {rows}x{cols}")
+    gen = torch.Generator().manual_seed(rows + 5 * cols)
+    x = _rand((rows, cols), dtype, gen, 2.0).to(cuda)
+    b = _rand((cols,), dtype, gen).to(cuda)
+    dy = _rand((rows, cols), dtype, gen).to(cuda)
+    dx0 = K.bias_gelu_bwd(dy, x, b)
+    dbias = torch.full((cols,), 7.0, device=cuda)
+    dx = K.bias_gelu_bwd(dy, x, b, dbias=dbias, accumulate=False)
+    assert torch.equal(dx.cpu(), dx0.cpu())
+    ref = dx0.cpu().double().sum(0)
+    tol = 1e-5 * (ref.abs().max().item() + rows)
+    assert (dbias.cpu().double() - ref).abs().max().item() <= tol
+    K.bias_gelu_bwd(dy, x, b, dbias=dbias, accumulate=True)
+    assert (dbias.cpu().double() - 2 * ref).abs().max().item() <= 2 * tol
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
@@ -185,6 +238,13 @@ def test_bias_dropout_add_and_col_sum(cuda, dtype):
     K.col_sum(x.to(cuda), acc, accumulate=True)
     ref = 1.0 + x.float().sum(0)
     assert torch.allclose(acc.cpu(), ref, rtol=1e-5, atol=1e-4)
+    # wide and ragged column sums (several 512-column strips, row groups)
+    for rows, cols in ((8192, 6144), (4099, 1032), (7, 16)):
+        xw = _rand((rows, cols), dtype, gen).to(cuda)
+        out = torch.full((cols,), 3.0, device=cuda)
+        K.col_sum(xw, out, accumulate=False)
+        ref = xw.cpu().double().sum(0)
+        assert (out.cpu().double() - ref).abs().max().item() <= 1e-5 * (ref.abs().max().item() + rows), (rows, cols)
     # dropout p=0.25: kept fraction, scaling, and backward uses the same mask
     outp = K.bias_dropout_add_fwd(x.to(cuda), b.to(cuda), torch.zeros_like(r).to(cuda), p=0.25, seed=123)
     kept = (outp.cpu().float() != 0)
