@@ -58,7 +58,7 @@ SIGNATURES = {
     "eth_grad_norm_finalize": [_P, _I64, _F64, _P, _P],
     "eth_adam_step": [_P, _P, _I64, _F64, _F64, _F64, _I64, _I32, _P, _P, _P],
     "eth_gemm": [_P, _I64, _I32, _P, _I64, _I32, _P, _I64, _I32, _P, _I64, _I64, _I64, _I32, _I32, _F32, _P],
-    "eth_gemm_splitk": [_P, _I64, _I32, _P, _I64, _I32, _P, _I64, _I64, _I64, _I64, _I32, _I32, _P, _P],
+    "eth_gemm_splitk": [_P, _I64, _I32, _P, _I64, _I32, _P, _I64, _I64, _I64, _I64, _I32, _I32, _I32, _P, _P],
     "eth_ln_fwd": [_P, _P, _P, _P, _P, _P, _I64, _I64, _F32, _I32, _P],
     "eth_ln_bwd": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I32, _I32, _P],
     "eth_bias_gelu_fwd": [_P, _P, _P, _I64, _I64, _I32, _P],

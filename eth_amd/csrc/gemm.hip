@@ -799,7 +799,7 @@ extern "C" int eth_gemm(const void* A, int64_t lda, int a_kcontig, const void* B
 namespace eth {
 // C[m, n] += sum_s W[s][m*N + n], splits added in order (deterministic)
 __global__ void splitk_reduce_kernel(const float* __restrict__ W, int splits, int64_t stride, float* __restrict__ C,
-                                     int64_t ldc, int M, int N) {
+                                     int64_t ldc, int M, int N, int accumulate) {
   const int nq = N / 4;
   const int64_t total = (int64_t)M * nq;
   for (int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; q < total; q += (int64_t)gridDim.x * blockDim.x) {
@@ -813,12 +813,14 @@ __global__ void splitk_reduce_kernel(const float* __restrict__ W, int splits, in
       acc.w += w.w;
     }
     float4* c = reinterpret_cast<float4*>(C + (int64_t)m * ldc + n);
-    float4 o = *c;
-    o.x += acc.x;
-    o.y += acc.y;
-    o.z += acc.z;
-    o.w += acc.w;
-    *c = o;
+    if (accumulate) {
+      const float4 o = *c;
+      acc.x = o.x + acc.x;
+      acc.y = o.y + acc.y;
+      acc.z = o.z + acc.z;
+      acc.w = o.w + acc.w;
+    }
+    *c = acc;
   }
 }
 }  // namespace eth
@@ -829,7 +831,7 @@ extern "C" int64_t eth_gemm_splitk_workspace(int64_t M, int64_t N, int splits) {
 
 extern "C" int eth_gemm_splitk(const void* A, int64_t lda, int a_kcontig, const void* B, int64_t ldb, int b_kcontig,
                                float* C, int64_t ldc, int64_t M, int64_t N, int64_t K, int in_dtype, int splits,
-                               float* workspace, void* stream) {
+                               int accumulate, float* workspace, void* stream) {
   ETH_CHECK_ARG(in_dtype == ETH_BF16 || in_dtype == ETH_F16, "eth_gemm_splitk: inputs must be bf16 or fp16");
   ETH_CHECK_ARG(A && B && C && workspace, "eth_gemm_splitk: null operand");
   ETH_CHECK_ARG(splits >= 1 && splits <= 16, "eth_gemm_splitk: splits must be in [1, 16] (got %d)", splits);
@@ -873,7 +875,7 @@ extern "C" int eth_gemm_splitk(const void* A, int64_t lda, int a_kcontig, const 
   if (rc != ETH_OK) return rc;
   const int64_t quads = M * (N / 4);
   const int grid = (int)std::min<int64_t>((quads + 255) / 256, 2048);
-  splitk_reduce_kernel<<<grid, 256, 0, s>>>(workspace, splits, slice, C, ldc, (int)M, (int)N);
+  splitk_reduce_kernel<<<grid, 256, 0, s>>>(workspace, splits, slice, C, ldc, (int)M, (int)N, accumulate);
   ETH_CHECK_LAUNCH("eth_gemm_splitk");
   return ETH_OK;
 }

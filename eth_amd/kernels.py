@@ -60,7 +60,7 @@ def set_gemm_observer(fn):
 
 
 def _splitk_splits(M, N, K, out):
-    """Split-K factor for an fp32 accumulate whose 256x256 tile grid is too
+    """Split-K factor for an fp32 product whose 256x256 tile grid is too
     small to fill the chip (fewer than 128 tiles): enough k-splits for about
     one workgroup per CU, each split a multiple of 128 deep."""
     tiles = -(-M // 256) * -(-N // 256)
@@ -114,14 +114,15 @@ def gemm(a, b, out=None, bias=None, accumulate=False, out_dtype=None, alpha=1.0)
     obs = _gemm_observer
     if obs is not None:
         obs("begin", M, N, K)
-    splits = _splitk_splits(M, N, K, out) if accumulate and alpha == 1.0 and bias is None else 1
+    fp32_product = out.dtype == torch.float32 and alpha == 1.0 and bias is None
+    splits = _splitk_splits(M, N, K, out) if fp32_product else 1
     if splits > 1:
         ws = _scratch_f32(nat.value("eth_gemm_splitk_workspace", M, N, splits) // 4, a.device)
         nat.call(
             "eth_gemm_splitk",
             nat.ptr(a), lda, a_kcontig,
             nat.ptr(b), ldb, b_kcontig,
-            nat.ptr(out), out.stride(0), M, N, K, code, splits, nat.ptr(ws),
+            nat.ptr(out), out.stride(0), M, N, K, code, splits, 1 if accumulate else 0, nat.ptr(ws),
             nat.stream_ptr(a.device),
         )
         if obs is not None:

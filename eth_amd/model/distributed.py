@@ -8,12 +8,49 @@ module.parameters() order, `param.main_grad` views, a hook that folds any
 autograd Functions accumulate straight into main_grad, so the hook only
 fires for gradients produced outside them.  Zeroing uses a fill kernel (no
 hipMemsetAsync).
+
+zero_grad_buffer(defer=True) zeroes nothing: it marks every parameter's
+main_grad stale, the first kernel to contribute a gradient then stores
+instead of adding (`main_grad_target`), and settle_grad_buffer() zero-fills
+whatever received no gradient before the buffer is read.  The values are
+those of zero-then-accumulate (0 + g == g); the fill of the whole buffer and
+the first read of every accumulation are saved.
 """
 
 import torch
 from torch import nn
 
 from .. import _native as nat
+
+
+def main_grad_target(param):
+    """(main_grad, accumulate) for a kernel about to write param's gradient:
+    accumulate is False for the first contribution after a deferred
+    zero_grad_buffer() (the buffer then holds stale values and the kernel
+    stores), True afterwards.  (None, False) without a main_grad."""
+    mg = getattr(param, "main_grad", None)
+    if mg is None:
+        return None, False
+    if getattr(param, "_eth_main_grad_stale", False):
+        param._eth_main_grad_stale = False
+        return mg, False
+    return mg, True
+
+
+def materialize_main_grad(param):
+    """param.main_grad with real values: zero-filled now if it is stale."""
+    mg = getattr(param, "main_grad", None)
+    if mg is not None and getattr(param, "_eth_main_grad_stale", False):
+        _zero(mg)
+        param._eth_main_grad_stale = False
+    return mg
+
+
+def _zero(t):
+    if t.dtype == torch.float32 and t.is_cuda and t.is_contiguous():
+        nat.call("eth_fill_f32", nat.ptr(t), t.numel(), 0.0, nat.stream_ptr(t.device))
+    else:
+        t.zero_()
 
 
 class MemoryBuffer:
@@ -23,10 +60,7 @@ class MemoryBuffer:
         self.data = torch.zeros(numel, dtype=dtype, device=device)
 
     def zero(self):
-        if self.dtype == torch.float32 and self.data.is_cuda:
-            nat.call("eth_fill_f32", nat.ptr(self.data), self.numel, 0.0, nat.stream_ptr(self.data.device))
-        else:
-            self.data.zero_()
+        _zero(self.data)
 
     def get(self, shape, start_index):
         end = start_index + torch.Size(shape).numel()
@@ -65,6 +99,7 @@ class DistributedDataParallel(nn.Module):
             dt = self._grad_dtype(p)
             remaining[dt] -= p.numel()
             p.main_grad = self._grad_buffers[dt].get(p.shape, remaining[dt])
+        self._grad_params = [p for p in self.module.parameters() if p.requires_grad]
         self.grad_accs = []
         for p in self.module.parameters():
             if not p.requires_grad:
@@ -77,14 +112,31 @@ class DistributedDataParallel(nn.Module):
     def _make_param_hook(param):
         def hook(*unused):
             if param.grad is not None:
-                param.main_grad.add_(param.grad.data)
+                mg, accumulate = main_grad_target(param)
+                if accumulate:
+                    mg.add_(param.grad.data)
+                else:
+                    mg.copy_(param.grad.data)
                 param.grad = None
 
         return hook
 
-    def zero_grad_buffer(self):
+    def zero_grad_buffer(self, defer=False):
+        if defer:
+            for p in self._grad_params:
+                p._eth_main_grad_stale = True
+            return
         for buf in self._grad_buffers.values():
             buf.zero()
+        for p in self._grad_params:
+            p._eth_main_grad_stale = False
+
+    def settle_grad_buffer(self):
+        """Zero-fill the main_grad of every parameter that received no
+        gradient since a deferred zero_grad_buffer(); afterwards the whole
+        buffer holds the step's gradients."""
+        for p in self._grad_params:
+            materialize_main_grad(p)
 
     @property
     def grad_buffers(self):

@@ -12,13 +12,37 @@ gradient is returned in the parameter's dtype.
 import torch
 
 from .. import kernels as K
+from .distributed import main_grad_target, materialize_main_grad
 
 
 def _fp32_accum_target(param):
+    """(main_grad, accumulate): the fp32 buffer the kernel writes param's
+    gradient into, and whether it adds (False for the first contribution
+    after a deferred zero_grad_buffer(), when it stores)."""
     mg = getattr(param, "main_grad", None)
     if mg is not None and mg.dtype != torch.float32:
         raise ValueError("main_grad must be fp32 for the fused accumulation")
-    return mg
+    return main_grad_target(param)
+
+
+def _pair_target(p1, p2):
+    """(main_grad 1, main_grad 2, accumulate) for two gradients one kernel
+    call writes under one accumulate flag (LayerNorm gamma and beta).  If
+    only one of them is stale, that one is zeroed now and both accumulate;
+    (None, None, False) unless both have a main_grad (stale flags are then
+    left as they were)."""
+    for p in (p1, p2):
+        mg = getattr(p, "main_grad", None)
+        if mg is None:
+            return None, None, False
+        if mg.dtype != torch.float32:
+            raise ValueError("main_grad must be fp32 for the fused accumulation")
+    s1 = getattr(p1, "_eth_main_grad_stale", False)
+    s2 = getattr(p2, "_eth_main_grad_stale", False)
+    if s1 and s2:
+        p1._eth_main_grad_stale = p2._eth_main_grad_stale = False
+        return p1.main_grad, p2.main_grad, False
+    return materialize_main_grad(p1), materialize_main_grad(p2), True
 
 
 def _flat(x):
@@ -43,19 +67,19 @@ class LinearFn(torch.autograd.Function):
         dx = K.gemm(dy2, weight).view(ctx.in_shape) if ctx.needs_input_grad[0] else None
         dw = db = None
         if ctx.needs_input_grad[1]:
-            mg = _fp32_accum_target(weight)
+            mg, accumulate = _fp32_accum_target(weight)
             if mg is not None:
-                K.gemm(dy2.t(), x2, out=mg, accumulate=True)
+                K.gemm(dy2.t(), x2, out=mg, accumulate=accumulate)
             else:
-                acc = torch.zeros(weight.shape, dtype=torch.float32, device=weight.device)
-                K.gemm(dy2.t(), x2, out=acc, accumulate=True)
+                acc = torch.empty(weight.shape, dtype=torch.float32, device=weight.device)
+                K.gemm(dy2.t(), x2, out=acc)
                 dw = acc.to(weight.dtype)
         if bias is not None and ctx.needs_input_grad[2]:
-            mg = _fp32_accum_target(bias)
+            mg, accumulate = _fp32_accum_target(bias)
             if mg is not None:
-                K.col_sum(dy2, mg, accumulate=True)
+                K.col_sum(dy2, mg, accumulate=accumulate)
             else:
-                acc = torch.zeros(bias.shape, dtype=torch.float32, device=bias.device)
+                acc = torch.empty(bias.shape, dtype=torch.float32, device=bias.device)
                 K.col_sum(dy2, acc, accumulate=False)
                 db = acc.to(bias.dtype)
         return dx, dw, db
@@ -74,15 +98,13 @@ class LayerNormFn(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dy):
         x, gamma, beta, mean, rstd = ctx.saved_tensors
-        mg_g, mg_b = _fp32_accum_target(gamma), _fp32_accum_target(beta)
-        if mg_g is not None and mg_b is not None:
-            dg, db, acc = mg_g, mg_b, True
-        else:
-            dg = torch.zeros(gamma.shape, dtype=torch.float32, device=x.device)
-            db = torch.zeros(beta.shape, dtype=torch.float32, device=x.device)
-            acc = False
+        dg, db, acc = _pair_target(gamma, beta)
+        own = dg is None
+        if own:
+            dg = torch.empty(gamma.shape, dtype=torch.float32, device=x.device)
+            db = torch.empty(beta.shape, dtype=torch.float32, device=x.device)
         dx = K.layer_norm_bwd(_flat(dy.contiguous()), _flat(x), mean, rstd, gamma, dg, db, accumulate=acc)
-        if acc:
+        if not own:
             return dx.view(x.shape), None, None, None
         return dx.view(x.shape), dg.to(gamma.dtype), db.to(beta.dtype), None
 
@@ -112,13 +134,11 @@ class LayerNormResidualFn(torch.autograd.Function):
         x, gamma, beta, mean, rstd = ctx.saved_tensors
         if dy is None:
             return dres, None, None, None
-        mg_g, mg_b = _fp32_accum_target(gamma), _fp32_accum_target(beta)
-        if mg_g is not None and mg_b is not None:
-            dg, db, acc = mg_g, mg_b, True
-        else:
-            dg = torch.zeros(gamma.shape, dtype=torch.float32, device=x.device)
-            db = torch.zeros(beta.shape, dtype=torch.float32, device=x.device)
-            acc = False
+        dg, db, acc = _pair_target(gamma, beta)
+        own = dg is None
+        if own:
+            dg = torch.empty(gamma.shape, dtype=torch.float32, device=x.device)
+            db = torch.empty(beta.shape, dtype=torch.float32, device=x.device)
         part = None
         if dres is None:
             dx = K.layer_norm_bwd(_flat(dy.contiguous()), _flat(x), mean, rstd, gamma, dg, db, accumulate=acc)
@@ -129,7 +149,7 @@ class LayerNormResidualFn(torch.autograd.Function):
         dx = dx.view(x.shape)
         if part is not None:
             dx._eth_colsum_part = part
-        if acc:
+        if not own:
             return dx, None, None, None
         return dx, dg.to(gamma.dtype), db.to(beta.dtype), None
 
@@ -150,9 +170,9 @@ class BiasGeluFn(torch.autograd.Function):
         db = None
         if ctx.needs_input_grad[1]:
             # the bias gradient (column sums of dx) comes out of the same pass
-            mg = _fp32_accum_target(bias)
+            mg, accumulate = _fp32_accum_target(bias)
             target = mg if mg is not None else torch.empty(bias.shape, dtype=torch.float32, device=bias.device)
-            dx = K.bias_gelu_bwd(_flat(dy.contiguous()), _flat(x), bias, dbias=target, accumulate=mg is not None)
+            dx = K.bias_gelu_bwd(_flat(dy.contiguous()), _flat(x), bias, dbias=target, accumulate=accumulate)
             if mg is None:
                 db = target.to(bias.dtype)
         else:
@@ -178,14 +198,14 @@ class BiasDropoutAddFn(torch.autograd.Function):
         dx = K.dropout_bwd(_flat(dout), ctx.p, ctx.seed).view(dout.shape) if ctx.p > 0 else dout
         db = None
         if ctx.needs_input_grad[1]:
-            mg = _fp32_accum_target(bias)
+            mg, accumulate = _fp32_accum_target(bias)
             target = mg if mg is not None else torch.empty(bias.shape, dtype=torch.float32, device=bias.device)
             if part is not None:
                 # column sums already produced by the LayerNorm backward that
                 # made dout (p == 0: dx is dout)
-                K.reduce_partials(part, target, accumulate=mg is not None)
+                K.reduce_partials(part, target, accumulate=accumulate)
             else:
-                K.col_sum(_flat(dx), target, accumulate=mg is not None)
+                K.col_sum(_flat(dx), target, accumulate=accumulate)
             if mg is None:
                 db = target.to(bias.dtype)
         return dx, db, dout, None, None
@@ -250,7 +270,12 @@ class EmbeddingFn(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dout):
         tokens, positions, word, pos = ctx.saved_tensors
-        mw, mp = _fp32_accum_target(word), _fp32_accum_target(pos)
+        # the scatter-add needs real values underneath: stale buffers are
+        # zeroed first
+        for p in (word, pos):
+            if getattr(p, "main_grad", None) is not None and p.main_grad.dtype != torch.float32:
+                raise ValueError("main_grad must be fp32 for the fused accumulation")
+        mw, mp = materialize_main_grad(word), materialize_main_grad(pos)
         gw = mw if mw is not None else torch.zeros(word.shape, dtype=torch.float32, device=word.device)
         gp = mp if mp is not None else torch.zeros(pos.shape, dtype=torch.float32, device=pos.device)
         K.embedding_bwd(tokens, positions, dout.contiguous(), gw, gp)

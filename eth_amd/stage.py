@@ -83,8 +83,10 @@ class MiddleStageTrainer:
         return hidden.detach(), x.grad
 
     def train_step(self, x, dy, normalization_scale=1.0):
-        self.ddp.zero_grad_buffer()
+        # deferred: the first gradient written into each main_grad stores
+        self.ddp.zero_grad_buffer(defer=True)
         out, dx = self.forward_backward(x, dy)
+        self.ddp.settle_grad_buffer()
         self.grad_sync.execute(normalization_scale)
         ok, norm, zeros = self.optimizer.step()
         return out, dx, ok, norm
@@ -156,8 +158,9 @@ class FirstLastStageTrainer:
         K.tied_grad_sum(self.embedding.word_embeddings.weight.main_grad, self.post.word_embeddings.weight.main_grad)
 
     def train_step(self, sample_ids, labels=None):
-        self.ddp.zero_grad_buffer()
+        self.ddp.zero_grad_buffer(defer=True)
         losses, lo = self.forward_backward(sample_ids, labels)
+        self.ddp.settle_grad_buffer()
         self.grad_sync.execute(global_normalization_scale(self.nominal, lo.local_loss_weight))
         self.tie_gradients()
         ok, norm, zeros = self.optimizer.step()

@@ -160,18 +160,19 @@ int eth_gemm(const void* A, int64_t lda, int a_kcontig, const void* B, int64_t l
              int64_t M, int64_t N, int64_t K, int in_dtype, int flags, float alpha,
              void* stream);
 
-/* Split-K form of the fp32 accumulate (C += A B, alpha 1, no bias) for grids
- * too small to fill the chip, such as the [h, h] weight gradient of the
- * attention projection: `splits` k-ranges (K % (128 * splits) == 0) write
- * fp32 partial products into the caller's workspace of
- * eth_gemm_splitk_workspace(M, N, splits) bytes, which a second kernel adds
- * into C in split order (deterministic).  N % 4 == 0, 16-byte aligned C rows.
+/* Split-K form of the fp32 product (C += A B with accumulate != 0, else
+ * C = A B; alpha 1, no bias) for grids too small to fill the chip, such as
+ * the [h, h] weight gradient of the attention projection: `splits` k-ranges
+ * (K % (128 * splits) == 0) write fp32 partial products into the caller's
+ * workspace of eth_gemm_splitk_workspace(M, N, splits) bytes, which a second
+ * kernel sums in split order (deterministic) and adds into or stores to C.
+ * N % 4 == 0, 16-byte aligned C rows.
  * Same reference seam as eth_gemm's ETH_GEMM_ACCUMULATE form
  * (model/distributed.py:116-123 over mpu/layers.py:452-470). */
 int64_t eth_gemm_splitk_workspace(int64_t M, int64_t N, int splits);
 int eth_gemm_splitk(const void* A, int64_t lda, int a_kcontig, const void* B, int64_t ldb, int b_kcontig,
                     float* C, int64_t ldc, int64_t M, int64_t N, int64_t K, int in_dtype, int splits,
-                    float* workspace, void* stream);
+                    int accumulate, float* workspace, void* stream);
 
 /* ------------------------------------------------------------------------
  * LayerNorm (bf16/fp16 rows of `cols` elements, cols % 8 == 0, <= 8192).

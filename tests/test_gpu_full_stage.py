@@ -107,6 +107,18 @@ def test_first_last_stage_matches_fp64_oracle(cuda, dtype):
     assert ok and norm is not None and np.isfinite(norm)
     # the tied copies stay identical after the update
     assert torch.equal(tr.embedding.word_embeddings.weight, tr.post.word_embeddings.weight)
+    # deferred zeroing (what train_step uses) over a garbage buffer gives the
+    # eager buffer bit for bit: embedding scatter-add, LM head and layers
+    (buf,) = tr.ddp.grad_buffers.values()
+    tr.ddp.zero_grad_buffer()
+    tr.forward_backward(sample_ids)
+    eager = buf.data.clone()
+    buf.data.fill_(-7.0)
+    tr.ddp.zero_grad_buffer(defer=True)
+    tr.forward_backward(sample_ids)
+    tr.ddp.settle_grad_buffer()
+    torch.cuda.synchronize()
+    assert torch.equal(buf.data, eager)
 
 
 def tr_layer_params(tr):

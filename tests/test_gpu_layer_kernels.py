@@ -111,6 +111,10 @@ def test_gemm_splitk_accumulate(cuda, a_k, b_k):
     err = (outs[0] - ref).abs().max().item()
     assert err <= 1e-4 * ref.abs().max().item(), f"split-K err {err}"
     assert torch.equal(outs[0], outs[1])
+    # store form (C = A B): the same partial sums, written over garbage
+    st = torch.full((M, N), 9.0, dtype=torch.float32, device=cuda)
+    K.gemm(ad, bd, out=st, accumulate=False)
+    assert torch.equal(st.cpu() + 0.25, outs[0])  # one fp32 add of the same sum, either order
     # the single-pass kernel agrees to fp32 summation-order noise
     one = torch.full((M, N), 0.25, dtype=torch.float32, device=cuda)
     lda = ad.stride(0) if a_k else ad.stride(1)

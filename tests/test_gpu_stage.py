@@ -64,6 +64,37 @@ def test_middle_stage_matches_fp32_oracle(cuda, dtype):
             assert _rel(g, ref[k]) < 5e-2, f"layer {li} {k}: rel err {_rel(g, ref[k])}"
 
 
+def test_deferred_zero_matches_eager_zero(cuda):
+    """zero_grad_buffer(defer=True) over a buffer full of garbage, then two
+    micro-batches (the first gradient into each main_grad stores, the
+    second adds) and settle: every main_grad equals zero-then-accumulate of
+    the same two micro-batches bit for bit."""
+    announce("deferred main-grad zero vs eager zero")
+    cfg = GPTConfig(hidden_size=256, num_attention_heads=4, ffn_hidden_size=1024, num_layers=2,
+                    seq_length=128, micro_batch_size=2, params_dtype=torch.bfloat16, device="cuda", seed=21)
+    tr = MiddleStageTrainer(cfg, lr=1e-4, weight_decay=0.1, clip_grad=1.0)
+    gen = torch.Generator().manual_seed(8)
+    xs = [torch.randn(128, 2, 256, generator=gen).to(torch.bfloat16).to(cuda) for _ in range(2)]
+    dys = [(torch.randn(128, 2, 256, generator=gen) * 1e-2).to(torch.bfloat16).to(cuda) for _ in range(2)]
+    (buf,) = tr.ddp.grad_buffers.values()
+    tr.ddp.zero_grad_buffer()
+    for x, dy in zip(xs, dys):
+        tr.forward_backward(x, dy)
+    eager = buf.data.clone()
+    buf.data.fill_(123.0)
+    tr.ddp.zero_grad_buffer(defer=True)
+    for x, dy in zip(xs, dys):
+        tr.forward_backward(x, dy)
+    tr.ddp.settle_grad_buffer()
+    torch.cuda.synchronize()
+    assert torch.equal(buf.data, eager)
+    # a parameter no kernel wrote is zero-filled by settle
+    buf.data.fill_(5.0)
+    tr.ddp.zero_grad_buffer(defer=True)
+    tr.ddp.settle_grad_buffer()
+    assert torch.count_nonzero(buf.data).item() == 0
+
+
 def test_middle_stage_training_step(cuda):
     """zero -> fwd/bwd -> grad sync (fused stats) -> clip -> AdamW -> bf16
     copy; the update must equal the oracle AdamW applied to the GPU's own
