@@ -25,6 +25,8 @@ void set_error(const char* fmt, ...) {
 }
 
 constexpr int kThreads = 256;
+constexpr int kPipe = 8;  // 16-byte vectors in flight per thread in the contiguous paths
+typedef uint32_t gs_v4 __attribute__((ext_vector_type(4)));
 
 template <typename T>
 struct Elem;
@@ -61,19 +63,38 @@ __global__ void __launch_bounds__(kThreads) pack_kernel(const eth_chunk_t* __res
   constexpr int VW = Elem<T>::kVec;
   typedef typename Elem<T>::V V;
   if (c.rows == 1 && aligned16(src) && aligned16(dst)) {
-    const int64_t nv = n / VW;
-    const V* s = reinterpret_cast<const V*>(src);
-    V* d = reinterpret_cast<V*>(dst);
-    for (int64_t i = threadIdx.x; i < nv; i += kThreads) {
-      V x = s[i];
+    // kPipe 16-byte loads in flight per thread; main_grad is read once
+    // (nontemporal), the payload stays cacheable for the collective and the
+    // unpack that follow
+    const int nv = (int)(n / VW);
+    const gs_v4* s = reinterpret_cast<const gs_v4*>(src);
+    gs_v4* d = reinterpret_cast<gs_v4*>(dst);
+    auto scale_vec = [&](gs_v4& x) __attribute__((always_inline)) {
       if (scaled) {
-        T* e = reinterpret_cast<T*>(&x);
+        V y = __builtin_bit_cast(V, x);
+        T* e = reinterpret_cast<T*>(&y);
 #pragma unroll
         for (int j = 0; j < VW; ++j) e[j] = Elem<T>::put(Elem<T>::get(e[j], dtype) * scale, dtype);
+        x = __builtin_bit_cast(gs_v4, y);
       }
+    };
+    int i = threadIdx.x;
+    for (; i + (kPipe - 1) * kThreads < nv; i += kPipe * kThreads) {
+      gs_v4 x[kPipe];
+#pragma unroll
+      for (int u = 0; u < kPipe; ++u) x[u] = __builtin_nontemporal_load(s + i + u * kThreads);
+#pragma unroll
+      for (int u = 0; u < kPipe; ++u) {
+        scale_vec(x[u]);
+        d[i + u * kThreads] = x[u];
+      }
+    }
+    for (; i < nv; i += kThreads) {
+      gs_v4 x = __builtin_nontemporal_load(s + i);
+      scale_vec(x);
       d[i] = x;
     }
-    for (int64_t i = nv * VW + threadIdx.x; i < n; i += kThreads) {
+    for (int64_t i = (int64_t)nv * VW + threadIdx.x; i < n; i += kThreads) {
       T x = src[i];
       dst[i] = scaled ? Elem<T>::put(Elem<T>::get(x, dtype) * scale, dtype) : x;
     }
@@ -121,19 +142,34 @@ __global__ void __launch_bounds__(kThreads) unpack_kernel(const eth_chunk_t* __r
   float sq = 0.f;
   bool bad = false;
   if (c.rows == 1 && aligned16(dstp) && aligned16(pay)) {
-    const int64_t nv = n / VW;
-    V* p = reinterpret_cast<V*>(pay);
-    V* d = reinterpret_cast<V*>(dstp);
-    for (int64_t i = threadIdx.x; i < nv; i += kThreads) {
-      V x = p[i], y;
+    // kPipe 16-byte loads in flight per thread; main_grad is not read again
+    // before the optimizer, after every bucket (nontemporal stores)
+    const int nv = (int)(n / VW);
+    gs_v4* p = reinterpret_cast<gs_v4*>(pay);
+    gs_v4* d = reinterpret_cast<gs_v4*>(dstp);
+    const bool wb = (flags & ETH_UNPACK_WRITEBACK) && norm != 1.0f;
+    auto one_vec = [&](gs_v4& xv, int idx) __attribute__((always_inline)) {
+      V x = __builtin_bit_cast(V, xv), y;
       T* xe = reinterpret_cast<T*>(&x);
       T* ye = reinterpret_cast<T*>(&y);
 #pragma unroll
       for (int j = 0; j < VW; ++j) sq += unpack_one<T>(xe[j], ye[j], norm, inv, flags, dtype, bad);
-      if ((flags & ETH_UNPACK_WRITEBACK) && norm != 1.0f) p[i] = x;
-      d[i] = y;
+      if (wb) p[idx] = __builtin_bit_cast(gs_v4, x);
+      __builtin_nontemporal_store(__builtin_bit_cast(gs_v4, y), d + idx);
+    };
+    int i = threadIdx.x;
+    for (; i + (kPipe - 1) * kThreads < nv; i += kPipe * kThreads) {
+      gs_v4 x[kPipe];
+#pragma unroll
+      for (int u = 0; u < kPipe; ++u) x[u] = p[i + u * kThreads];
+#pragma unroll
+      for (int u = 0; u < kPipe; ++u) one_vec(x[u], i + u * kThreads);
     }
-    for (int64_t i = nv * VW + threadIdx.x; i < n; i += kThreads)
+    for (; i < nv; i += kThreads) {
+      gs_v4 x = p[i];
+      one_vec(x, i);
+    }
+    for (int64_t i = (int64_t)nv * VW + threadIdx.x; i < n; i += kThreads)
       sq += unpack_one<T>(pay[i], dstp[i], norm, inv, flags, dtype, bad);
   } else {
     for (int64_t i = threadIdx.x; i < n; i += kThreads) {
