@@ -26,6 +26,8 @@
 // for dQ^T = K^T dS^T, Q and dO for dK and dV) are kept in LDS in natural
 // row order, padded to D + 32 so four k-rows fall in distinct banks, and
 // read with ds_read_b64_tr_b16.  Softmax runs in fp32 base-2 (exp2) with the scale folded.
+#include <type_traits>
+
 #include "common.h"
 
 namespace eth {
@@ -189,7 +191,8 @@ __global__ void __launch_bounds__(kAttnThreads, 2) attn_fwd_kernel(AttnArgs a) {
   const int BH = a.B * a.H, nqb = a.S / kBQ;
   const int bh = blockIdx.x % BH, qb = nqb - 1 - blockIdx.x / BH;
   const int b = bh / a.H, h = bh % a.H;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, hl = lane >> 5;
+  const int lane = threadIdx.x & 63, hl = lane >> 5;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int q0 = qb * kBQ + w * 32;
   const int q = q0 + (lane & 31);
   const float sl2 = a.scale_log2;
@@ -325,7 +328,8 @@ __global__ void __launch_bounds__(kAttnThreads, PART == 3 ? 1 : 2) attn_bwd_dkdv
   const int BH = a.B * a.H;
   const int bh = blockIdx.x % BH, kb = blockIdx.x / BH;
   const int b = bh / a.H, h = bh % a.H;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, hl = lane >> 5;
+  const int lane = threadIdx.x & 63, hl = lane >> 5;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int k0 = kb * kBKV2 + w * 32;
   const int key = k0 + (lane & 31);
 
@@ -387,15 +391,24 @@ __global__ void __launch_bounds__(kAttnThreads, PART == 3 ? 1 : 2) attn_bwd_dkdv
         s = mma<FP16>(*reinterpret_cast<const uint4*>(qp + ks * 16), kf[ks], s);
         if constexpr (DK) dp = mma<FP16>(*reinterpret_cast<const uint4*>(op + ks * 16), vf[ks], dp);
       }
-      // P and dS (fp32); query index of register r = t*32 + swz_row(r, hl)
+      // P and dS (fp32); query index of register r = t*32 + swz_row(r, hl).
+      // The causal mask is applied only on the steps that cross the
+      // diagonal (a wave-uniform branch): elsewhere its compares and selects
+      // would cost more VALU time than the exponentials.
+      auto probs = [&](auto masked) __attribute__((always_inline)) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int qi = t * 32 + swz_row(r, hl);
-        float p = fast_exp2(__builtin_fmaf(s[r], a.scale_log2, -lse_s[qi]));
-        if (diag && key > qs0 + qi) p = 0.f;
-        s[r] = p;
-        if constexpr (DK) dp[r] = p * (dp[r] - del_s[qi]);
-      }
+        for (int r = 0; r < 16; ++r) {
+          const int qi = t * 32 + swz_row(r, hl);
+          float p = fast_exp2(__builtin_fmaf(s[r], a.scale_log2, -lse_s[qi]));
+          if (decltype(masked)::value && key > qs0 + qi) p = 0.f;
+          s[r] = p;
+          if constexpr (DK) dp[r] = p * (dp[r] - del_s[qi]);
+        }
+      };
+      if (diag)
+        probs(std::true_type{});
+      else
+        probs(std::false_type{});
 #pragma unroll
       for (int k2 = 0; k2 < 2; ++k2) {
         const int kk = t * 2 + k2, e0 = k2 * 8;
@@ -442,7 +455,8 @@ __global__ void __launch_bounds__(kAttnThreads, 2) attn_bwd_dq_kernel(AttnArgs a
   const int BH = a.B * a.H, nqb = a.S / kBQ;
   const int bh = blockIdx.x % BH, qb = nqb - 1 - blockIdx.x / BH;
   const int b = bh / a.H, h = bh % a.H;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, hl = lane >> 5;
+  const int lane = threadIdx.x & 63, hl = lane >> 5;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int q0 = qb * kBQ + w * 32;
   const int q = q0 + (lane & 31);
 
@@ -518,12 +532,19 @@ __global__ void __launch_bounds__(kAttnThreads, 2) attn_bwd_dq_kernel(AttnArgs a
         s = mma<FP16>(*reinterpret_cast<const uint4*>(kp + ks * 16), qf[ks], s);
         dp = mma<FP16>(*reinterpret_cast<const uint4*>(vp + ks * 16), of[ks], dp);
       }
+      // causal mask only on the blocks that cross the diagonal (see dK/dV)
+      auto dsoft = [&](auto masked) __attribute__((always_inline)) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float p = fast_exp2(__builtin_fmaf(s[r], a.scale_log2, -lse));
-        if (diag && kv0 + t * 32 + swz_row(r, hl) > q) p = 0.f;
-        dp[r] = p * (dp[r] - del);
-      }
+        for (int r = 0; r < 16; ++r) {
+          float p = fast_exp2(__builtin_fmaf(s[r], a.scale_log2, -lse));
+          if (decltype(masked)::value && kv0 + t * 32 + swz_row(r, hl) > q) p = 0.f;
+          dp[r] = p * (dp[r] - del);
+        }
+      };
+      if (diag)
+        dsoft(std::true_type{});
+      else
+        dsoft(std::false_type{});
 #pragma unroll
       for (int k2 = 0; k2 < 2; ++k2) {
         const int kk = t * 2 + k2, e0 = k2 * 8;
