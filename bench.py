@@ -63,12 +63,19 @@ def step_flops(layers=LAYERS, s=SEQ, b=MB, h=H, f=FFN):
 
 
 class GemmMeter:
-    """Records HIP events around every GEMM launch and sums FLOPs."""
+    """Records HIP events around every GEMM launch, on the stream the launch
+    goes to, and sums FLOPs.  The weight-gradient GEMMs of the timed steps
+    run on a side stream, overlapped with the data-gradient chain, so
+    launches can overlap in time: `busy_ms` is the length of the union of
+    the launch intervals (time during which at least one GEMM ran), and
+    `total_ms` the plain sum of launch durations."""
 
     def __init__(self, torch):
         self.torch = torch
         self.events = []
         self.flops = 0.0
+        self.base = torch.cuda.Event(enable_timing=True)
+        self.base.record()
 
     def __call__(self, phase, M, N, K):
         if phase == "begin":
@@ -83,6 +90,20 @@ class GemmMeter:
 
     def total_ms(self):
         return sum(a.elapsed_time(b) for a, b in self.events)
+
+    def busy_ms(self):
+        spans = sorted((self.base.elapsed_time(a), self.base.elapsed_time(b)) for a, b in self.events)
+        busy, cur0, cur1 = 0.0, None, None
+        for t0, t1 in spans:
+            if cur1 is None or t0 > cur1:
+                if cur1 is not None:
+                    busy += cur1 - cur0
+                cur0, cur1 = t0, t1
+            else:
+                cur1 = max(cur1, t1)
+        if cur1 is not None:
+            busy += cur1 - cur0
+        return busy
 
 
 def cpu_baseline(budget_s=20.0):
@@ -289,7 +310,8 @@ def main():
     ms = 1e3 * elapsed / args.steps
     tokens = SEQ * MB
     value = tokens * args.steps / elapsed
-    gemm_ms = meter.total_ms()
+    gemm_ms = meter.busy_ms()
+    gemm_sum_ms = meter.total_ms()
     gemm_tflops = meter.flops / (gemm_ms * 1e-3) / 1e12 if gemm_ms > 0 else 0.0
     step_tflops = step_flops() / (ms * 1e-3) / 1e12
 
@@ -328,6 +350,10 @@ def main():
             "algorithmic_bytes_per_launch": GEMM_ALGORITHMIC_BYTES_PER_LAUNCH,
             "launches": len(meter.events),
             "gemm_ms_per_step": gemm_ms / args.steps,
+            "time_basis": "union of the GEMM launch intervals (weight-gradient GEMMs run on a side stream, "
+                          "overlapped with the data-gradient chain)",
+            "launch_sum_ms_per_step": gemm_sum_ms / args.steps,
+            "achieved_over_launch_sum": meter.flops / (gemm_sum_ms * 1e-3) / 1e12 if gemm_sum_ms > 0 else 0.0,
         },
     }
     del tr, out, dx

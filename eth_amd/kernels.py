@@ -76,12 +76,34 @@ _scratch = {}
 
 
 def _scratch_f32(numel, device):
-    """A per-device fp32 workspace reused across calls (grown on demand)."""
-    buf = _scratch.get(device)
+    """An fp32 workspace per (device, stream), reused across calls and grown
+    on demand: launches on one stream are ordered, so they may share it."""
+    key = (device, torch.cuda.current_stream(device).cuda_stream)
+    buf = _scratch.get(key)
     if buf is None or buf.numel() < numel:
         buf = torch.empty(numel, dtype=torch.float32, device=device)
-        _scratch[device] = buf
+        _scratch[key] = buf
     return buf[:numel]
+
+
+_side = {}
+
+
+def side_stream(device):
+    """The stream the weight-gradient GEMMs run on when overlapped with the
+    data-gradient chain (default priority, one per device)."""
+    st = _side.get(device)
+    if st is None:
+        st = torch.cuda.Stream(device=device)
+        _side[device] = st
+    return st
+
+
+def join_side_streams():
+    """Make the current stream wait for all side-stream work (before main
+    grads are read)."""
+    for dev, st in _side.items():
+        torch.cuda.current_stream(dev).wait_stream(st)
 
 
 def gemm(a, b, out=None, bias=None, accumulate=False, out_dtype=None, alpha=1.0):

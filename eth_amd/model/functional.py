@@ -15,6 +15,27 @@ from .. import kernels as K
 from .distributed import main_grad_target, materialize_main_grad
 
 
+_overlap = {"wgrad": False}
+
+
+class overlapped_wgrad:
+    """Within this context, LinearFn's weight-gradient GEMMs into main_grad
+    run on a side stream, overlapped with the data-gradient chain; on exit
+    the current stream waits for them, so main_grad is complete for
+    whatever runs next."""
+
+    def __enter__(self):
+        self._prev = _overlap["wgrad"]
+        _overlap["wgrad"] = True
+        return self
+
+    def __exit__(self, *exc):
+        _overlap["wgrad"] = self._prev
+        K.join_side_streams()
+        return False
+
+
+
 def _fp32_accum_target(param):
     """(main_grad, accumulate): the fp32 buffer the kernel writes param's
     gradient into, and whether it adds (False for the first contribution
@@ -68,7 +89,18 @@ class LinearFn(torch.autograd.Function):
         dw = db = None
         if ctx.needs_input_grad[1]:
             mg, accumulate = _fp32_accum_target(weight)
-            if mg is not None:
+            if mg is not None and _overlap["wgrad"] and dy2.is_cuda:
+                # the weight gradient only feeds main_grad: it runs on a side
+                # stream, overlapped with the data-gradient chain, and is
+                # joined before the gradient sync reads the buffer
+                main = torch.cuda.current_stream(dy2.device)
+                side = K.side_stream(dy2.device)
+                side.wait_stream(main)
+                with torch.cuda.stream(side):
+                    K.gemm(dy2.t(), x2, out=mg, accumulate=accumulate)
+                dy2.record_stream(side)
+                x2.record_stream(side)
+            elif mg is not None:
                 K.gemm(dy2.t(), x2, out=mg, accumulate=accumulate)
             else:
                 acc = torch.empty(weight.shape, dtype=torch.float32, device=weight.device)

@@ -22,6 +22,7 @@ from .loss import global_normalization_scale, gpt_loss_output, synthetic_gpt_bat
 from .grad_sync.manager import initialize_gradient_sync
 from .model.distributed import DistributedDataParallel
 from .model.flex_model import FlexGPTModel, middle_stage
+from .model.functional import overlapped_wgrad
 from .model.flex_ops import GPTConfig
 from .optimizer.optimizer import get_megatron_optimizer
 
@@ -79,7 +80,8 @@ class MiddleStageTrainer:
         self.model.set_input_tensor({"hidden_states": x})
         out, _extra = self.model(None, {})
         hidden = out["hidden_states"]
-        torch.autograd.backward(hidden, dy)
+        with overlapped_wgrad():
+            torch.autograd.backward(hidden, dy)
         return hidden.detach(), x.grad
 
     def train_step(self, x, dy, normalization_scale=1.0):
@@ -151,7 +153,8 @@ class FirstLastStageTrainer:
         losses = out["output"]
         lo = gpt_loss_output(losses, mask, self.nominal)
         output_tensor = lo.local_loss_sum / lo.nominal_global_loss_scale
-        torch.autograd.backward(self.optimizer.scale_loss(output_tensor))
+        with overlapped_wgrad():
+            torch.autograd.backward(self.optimizer.scale_loss(output_tensor))
         return losses.detach(), lo
 
     def tie_gradients(self):

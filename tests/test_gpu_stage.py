@@ -95,6 +95,32 @@ def test_deferred_zero_matches_eager_zero(cuda):
     assert torch.count_nonzero(buf.data).item() == 0
 
 
+def test_overlapped_weight_gradients_match_single_stream(cuda):
+    """forward_backward runs the weight-gradient GEMMs on a side stream
+    (joined before it returns); the buffer equals a plain single-stream
+    backward of the same micro-batch bit for bit."""
+    announce("side-stream weight gradients vs single stream")
+    cfg = GPTConfig(hidden_size=256, num_attention_heads=4, ffn_hidden_size=1024, num_layers=2,
+                    seq_length=128, micro_batch_size=2, params_dtype=torch.bfloat16, device="cuda", seed=33)
+    tr = MiddleStageTrainer(cfg, lr=1e-4, weight_decay=0.1, clip_grad=1.0)
+    gen = torch.Generator().manual_seed(4)
+    x = torch.randn(128, 2, 256, generator=gen).to(torch.bfloat16).to(cuda)
+    dy = (torch.randn(128, 2, 256, generator=gen) * 1e-2).to(torch.bfloat16).to(cuda)
+    (buf,) = tr.ddp.grad_buffers.values()
+    tr.ddp.zero_grad_buffer()
+    xi = x.detach().requires_grad_(True)
+    tr.model.set_input_tensor({"hidden_states": xi})
+    out, _ = tr.model(None, {})
+    torch.autograd.backward(out["hidden_states"], dy)
+    single = buf.data.clone()
+    tr.ddp.zero_grad_buffer()
+    _, dx = tr.forward_backward(x, dy)
+    overlapped = buf.data.clone()
+    torch.cuda.synchronize()
+    assert torch.equal(overlapped, single)
+    assert torch.equal(dx, xi.grad)
+
+
 def test_middle_stage_training_step(cuda):
     """zero -> fwd/bwd -> grad sync (fused stats) -> clip -> AdamW -> bf16
     copy; the update must equal the oracle AdamW applied to the GPU's own
