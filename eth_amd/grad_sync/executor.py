@@ -131,6 +131,7 @@ class GradientBucketExecutor:
         self._tables = self._build_tables()
         self._statistics = None
         self._inv_scale = 1.0
+        self._pass = None
 
     # ------------------------------------------------------------ contract --
     @staticmethod
@@ -289,9 +290,28 @@ class GradientBucketExecutor:
         self._inv_scale = float(inv_scale)
 
     # ------------------------------------------------------------ execute --
-    def execute(self, normalization_scale=1.0):
+    def bucket_parameters(self):
+        """Per bucket, in execution order, the parameters whose main_grad it
+        reads (each once)."""
+        out = []
+        for bucket, _table, _n, _base in self._tables:
+            seen = {}
+            for placement in bucket.placements:
+                binding = self._binding_specs[placement.fragment_id]
+                param = self._runtime_bindings[binding.logical_param_id].parameter
+                seen.setdefault(id(param), param)
+            out.append(list(seen.values()))
+        return out
+
+    @property
+    def n_buckets(self):
+        return len(self._tables)
+
+    def begin(self, normalization_scale=1.0):
+        """Start a pass over the buckets on the current stream: resets the
+        bound statistics; run_bucket(i) then syncs bucket i, in any order,
+        each once, on the current stream, and end() closes the pass."""
         stats = self._statistics
-        stream = nat.stream_ptr(self._device) if self._device is not None else None
         flags = 0
         if stats is not None:
             stats.reset()
@@ -300,28 +320,46 @@ class GradientBucketExecutor:
                 flags |= nat.UNPACK_UNSCALE
         if normalization_scale != 1.0:
             flags |= nat.UNPACK_WRITEBACK
-        for bucket, table, n_chunks, base in self._tables:
-            payload = self._scratch[bucket.grad_dtype][: bucket.exact_numel]
-            dcode = nat.dtype_code(payload.dtype)
-            if n_chunks:
-                nat.call("eth_bucket_pack", nat.ptr(table), n_chunks, nat.ptr(payload), dcode, stream)
-            self._all_reduce_sum(payload, self._registry.handle(bucket.process_group_id))
-            if n_chunks:
-                f = flags if (dcode == nat.ETH_F32 or not (flags & nat.UNPACK_UNSCALE)) else flags & ~nat.UNPACK_UNSCALE
-                nat.call(
-                    "eth_bucket_unpack",
-                    nat.ptr(table),
-                    n_chunks,
-                    nat.ptr(payload),
-                    dcode,
-                    float(normalization_scale),
-                    float(self._inv_scale),
-                    f,
-                    nat.ptr(stats.found_inf) if stats is not None else None,
-                    nat.ptr(stats.partials) if stats is not None else None,
-                    base,
-                    stream,
-                )
+        self._pass = (float(normalization_scale), flags)
+
+    def run_bucket(self, i):
+        """pack -> all_reduce_sum seam -> fused unpack of bucket i
+        (executor.py:199-261) on the current stream."""
+        normalization_scale, flags = self._pass
+        stats = self._statistics
+        stream = nat.stream_ptr(self._device) if self._device is not None else None
+        bucket, table, n_chunks, base = self._tables[i]
+        payload = self._scratch[bucket.grad_dtype][: bucket.exact_numel]
+        dcode = nat.dtype_code(payload.dtype)
+        if n_chunks:
+            nat.call("eth_bucket_pack", nat.ptr(table), n_chunks, nat.ptr(payload), dcode, stream)
+        self._all_reduce_sum(payload, self._registry.handle(bucket.process_group_id))
+        if n_chunks:
+            f = flags if (dcode == nat.ETH_F32 or not (flags & nat.UNPACK_UNSCALE)) else flags & ~nat.UNPACK_UNSCALE
+            nat.call(
+                "eth_bucket_unpack",
+                nat.ptr(table),
+                n_chunks,
+                nat.ptr(payload),
+                dcode,
+                normalization_scale,
+                float(self._inv_scale),
+                f,
+                nat.ptr(stats.found_inf) if stats is not None else None,
+                nat.ptr(stats.partials) if stats is not None else None,
+                base,
+                stream,
+            )
+
+    def end(self):
+        stats = self._statistics
         if stats is not None:
             stats.fresh = True
             stats.inv_scale_used = self._inv_scale
+        self._pass = None
+
+    def execute(self, normalization_scale=1.0):
+        self.begin(normalization_scale)
+        for i in range(len(self._tables)):
+            self.run_bucket(i)
+        self.end()

@@ -37,6 +37,15 @@ def main_grad_target(param):
     return mg, True
 
 
+def grad_written(param):
+    """Called once the kernels that write param's gradient for the current
+    backward have all been launched: a streamed gradient sync registered as
+    `param._eth_on_grad` may then sync the buckets holding it."""
+    cb = getattr(param, "_eth_on_grad", None)
+    if cb is not None:
+        cb(param)
+
+
 def materialize_main_grad(param):
     """param.main_grad with real values: zero-filled now if it is stale."""
     mg = getattr(param, "main_grad", None)
@@ -118,6 +127,7 @@ class DistributedDataParallel(nn.Module):
                 else:
                     mg.copy_(param.grad.data)
                 param.grad = None
+                grad_written(param)
 
         return hook
 

@@ -12,7 +12,7 @@ gradient is returned in the parameter's dtype.
 import torch
 
 from .. import kernels as K
-from .distributed import main_grad_target, materialize_main_grad
+from .distributed import grad_written, main_grad_target, materialize_main_grad
 
 
 _overlap = {"wgrad": False}
@@ -100,8 +100,10 @@ class LinearFn(torch.autograd.Function):
                     K.gemm(dy2.t(), x2, out=mg, accumulate=accumulate)
                 dy2.record_stream(side)
                 x2.record_stream(side)
+                grad_written(weight)
             elif mg is not None:
                 K.gemm(dy2.t(), x2, out=mg, accumulate=accumulate)
+                grad_written(weight)
             else:
                 acc = torch.empty(weight.shape, dtype=torch.float32, device=weight.device)
                 K.gemm(dy2.t(), x2, out=acc)
@@ -110,6 +112,7 @@ class LinearFn(torch.autograd.Function):
             mg, accumulate = _fp32_accum_target(bias)
             if mg is not None:
                 K.col_sum(dy2, mg, accumulate=accumulate)
+                grad_written(bias)
             else:
                 acc = torch.empty(bias.shape, dtype=torch.float32, device=bias.device)
                 K.col_sum(dy2, acc, accumulate=False)
@@ -137,6 +140,8 @@ class LayerNormFn(torch.autograd.Function):
             db = torch.empty(beta.shape, dtype=torch.float32, device=x.device)
         dx = K.layer_norm_bwd(_flat(dy.contiguous()), _flat(x), mean, rstd, gamma, dg, db, accumulate=acc)
         if not own:
+            grad_written(gamma)
+            grad_written(beta)
             return dx.view(x.shape), None, None, None
         return dx.view(x.shape), dg.to(gamma.dtype), db.to(beta.dtype), None
 
@@ -182,6 +187,8 @@ class LayerNormResidualFn(torch.autograd.Function):
         if part is not None:
             dx._eth_colsum_part = part
         if not own:
+            grad_written(gamma)
+            grad_written(beta)
             return dx, None, None, None
         return dx, dg.to(gamma.dtype), db.to(beta.dtype), None
 
@@ -207,6 +214,8 @@ class BiasGeluFn(torch.autograd.Function):
             dx = K.bias_gelu_bwd(_flat(dy.contiguous()), _flat(x), bias, dbias=target, accumulate=accumulate)
             if mg is None:
                 db = target.to(bias.dtype)
+            else:
+                grad_written(bias)
         else:
             dx = K.bias_gelu_bwd(_flat(dy.contiguous()), _flat(x), bias)
         return dx.view(x.shape), db
@@ -240,6 +249,8 @@ class BiasDropoutAddFn(torch.autograd.Function):
                 K.col_sum(_flat(dx), target, accumulate=accumulate)
             if mg is None:
                 db = target.to(bias.dtype)
+            else:
+                grad_written(bias)
         return dx, db, dout, None, None
 
 
@@ -311,6 +322,9 @@ class EmbeddingFn(torch.autograd.Function):
         gw = mw if mw is not None else torch.zeros(word.shape, dtype=torch.float32, device=word.device)
         gp = mp if mp is not None else torch.zeros(pos.shape, dtype=torch.float32, device=pos.device)
         K.embedding_bwd(tokens, positions, dout.contiguous(), gw, gp)
+        for p, m in ((word, mw), (pos, mp)):
+            if m is not None:
+                grad_written(p)
         return (None if mw is not None else gw.to(word.dtype), None if mp is not None else gp.to(pos.dtype), None,
                 None, None)
 

@@ -121,6 +121,34 @@ def test_overlapped_weight_gradients_match_single_stream(cuda):
     assert torch.equal(dx, xi.grad)
 
 
+def test_streamed_grad_sync_matches_sync_after_backward(cuda):
+    """Two identical stages, two steps each: buckets synced during the
+    backward (streamed, the default) and the whole sync after it (the
+    reference order) give bit-identical norms, master weights and bf16
+    weights."""
+    announce("streamed grad sync vs sync after backward")
+    cfg = GPTConfig(hidden_size=256, num_attention_heads=4, ffn_hidden_size=1024, num_layers=2,
+                    seq_length=128, micro_batch_size=2, params_dtype=torch.bfloat16, device="cuda", seed=41)
+    trs = [MiddleStageTrainer(cfg, lr=1e-3, weight_decay=0.1, clip_grad=0.5, bucket_cap_bytes=1 << 19) for _ in range(2)]
+    assert trs[0].grad_sync.executor.n_buckets > 4
+    gen = torch.Generator().manual_seed(6)
+    batches = [(torch.randn(128, 2, 256, generator=gen).to(torch.bfloat16).to(cuda),
+                (torch.randn(128, 2, 256, generator=gen) * 1e-1).to(torch.bfloat16).to(cuda)) for _ in range(2)]
+    norms = [[], []]
+    for x, dy in batches:
+        for i, tr in enumerate(trs):
+            _, _, ok, norm = tr.train_step(x, dy, streamed_sync=(i == 0))
+            assert ok
+            norms[i].append(norm)
+    torch.cuda.synchronize()
+    assert norms[0] == norms[1]
+    for pa, pb in zip(trs[0].model.parameters(), trs[1].model.parameters()):
+        assert torch.equal(pa, pb)
+        ma = trs[0].optimizer.optimizer_parameter_for_model_parameter(pa)
+        mb = trs[1].optimizer.optimizer_parameter_for_model_parameter(pb)
+        assert torch.equal(ma, mb)
+
+
 def test_middle_stage_training_step(cuda):
     """zero -> fwd/bwd -> grad sync (fused stats) -> clip -> AdamW -> bf16
     copy; the update must equal the oracle AdamW applied to the GPU's own
