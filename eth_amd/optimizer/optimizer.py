@@ -53,6 +53,7 @@ class MegatronOptimizer:
         self._stats_tables = None
         self._stats_key = None
         self._model_to_optimizer_param = {}
+        self._host_flags = None
 
     # ----------------------------------------------------------- plumbing --
     @property
@@ -182,21 +183,44 @@ class MegatronOptimizer:
                 nat.ptr(st.stats),
                 nat.stream_ptr(self._device()),
             )
+        # the host reads the norm and the inf flag from a pinned copy queued
+        # before the update kernel, so it waits for the statistics only, not
+        # for the update (the next step's launches overlap the update)
+        host = None
+        if st is not None and (need_norm or scaler is not None):
+            host = self._read_back(st)
         self.optimizer.step(
             stats=st.stats if need_norm else None,
             found_inf=st.found_inf if scaler is not None else None,
         )
+        if host is not None:
+            host[1].synchronize()
         if scaler is not None:
-            found = bool(st.found_inf.item() > 0)
+            found = bool(host[0][1].item() > 0)
             scaler.update(found)
             self.optimizer.commit_step(not found)
             if self._executor is not None:
                 self._executor.set_inv_loss_scale(self._inv_scale())
             if found:
                 return False, None, None
-        grad_norm = float(st.stats[1].item()) if need_norm else None
+        grad_norm = float(host[0][0].item()) if need_norm else None
         num_zeros = self.count_zeros() if self.log_num_zeros_in_grad else None
         return True, grad_norm, num_zeros
+
+    def _read_back(self, st):
+        """Queue a copy of [‖g‖, found_inf] into pinned host memory on the
+        current stream; returns (host tensor, event marking the copy)."""
+        dev = self._device()
+        if self._host_flags is None:
+            self._host_flags = (torch.empty(2, dtype=torch.float64, pin_memory=True),
+                                torch.empty(2, dtype=torch.float64, device=dev))
+        host, staging = self._host_flags
+        staging[0:1].copy_(st.stats[1:2])
+        staging[1:2].copy_(st.found_inf.reshape(-1)[0:1])
+        host.copy_(staging, non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record(torch.cuda.current_stream(dev))
+        return host, ev
 
     def zero_grad(self, set_to_none=True):
         for p in self.get_parameters():
