@@ -100,6 +100,7 @@ struct AttnArgs {
 };
 
 constexpr int kAttnThreads = 256;
+constexpr float kRescaleLog2 = 8.0f;  // forward: tolerated growth of the running max (log2 units)
 constexpr int kBQ = 128;   // forward / dQ: queries per workgroup (4 waves x 32)
 constexpr int kBKV = 64;   // forward / dQ: keys per step
 constexpr int kBKV2 = 128; // dK/dV: keys per workgroup (4 waves x 32)
@@ -256,7 +257,12 @@ __global__ void __launch_bounds__(kAttnThreads, 2) attn_fwd_kernel(AttnArgs a) {
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[t][r]);
       mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
       const float mnew = fmaxf(m, mx * sl2);
-      if (__any(mnew != m)) {  // rescale only when some running max moved
+      // m is the exponent offset, kept within kRescaleLog2 below the running
+      // max: O and l are rescaled only when some row's max grew past that,
+      // so p = exp2(s - m) stays <= 2^kRescaleLog2 (exact in fp32, the same
+      // relative precision in 16 bits) and most blocks skip the rescale;
+      // O / l and lse = m + log2(l) do not depend on the offset
+      if (__any(mnew > m + kRescaleLog2)) {
         const float alpha = fast_exp2(m - mnew);
         l *= alpha;
 #pragma unroll
