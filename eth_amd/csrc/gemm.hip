@@ -10,21 +10,24 @@
 //   dgrad    dX = dY W      : A K-contiguous, B N-contiguous
 //   wgrad    dW += dY^T X   : A M-contiguous, B N-contiguous, fp32 C += (the
 //                             Megatron main_grad accumulation, fused)
-// M-contiguous / N-contiguous operands are transposed in registers on their
-// way into LDS (4 k-rows x 8 columns per thread), so every LDS tile is stored
-// K-contiguous and each MFMA operand is one 16-byte LDS read.
+// In the fallback kernel, M-contiguous / N-contiguous operands are
+// transposed in registers on their way into LDS (4 k-rows x 8 columns per
+// thread), so every LDS tile is stored K-contiguous and each MFMA operand is
+// one 16-byte LDS read.
 //
 // Two kernels:
 //  * gemm256_kernel, the main one: 256x256x64 tiles, 4 waves (one per SIMD)
-//    of 128x128 each, 256 accumulator registers per lane held in AGPRs.  The
-//    k loop is software-pipelined by hand: while the MFMAs of k-tile t run,
-//    the registers holding k-tile t+1 are written to the other LDS stage and
-//    refilled with k-tile t+2, and the fragments of the next k-step are read
-//    from LDS, each spread between MFMA pairs (sched_barrier fixes the
-//    order).  One LDS-only barrier per k-tile.  The epilogue stages each
-//    32-row slab through LDS and writes whole rows with buffer stores.
-//    Needs K % 128 == 0, 16-byte aligned C rows and enough tiles to fill
-//    the chip.
+//    of 128x128 each, 256 accumulator registers per lane held in AGPRs.
+//    Operands go global -> LDS with direct loads (buffer_load ... lds) into
+//    two stages.  The k loop is software-pipelined by hand: while the MFMAs
+//    of k-tile t run, k-tile t+1 streams into the other stage, one 1 KB
+//    load per MFMA gap, and the fragments of the next k-step are read from
+//    LDS between the MFMAs (sched_barrier fixes the order).  One barrier
+//    per k-tile.  Row-contiguous operands land as they are in memory and
+//    their fragments come out of LDS through ds_read_b64_tr_b16.  The
+//    epilogue stages each 32-row slab through LDS and writes whole rows
+//    with buffer stores.  Needs K % 128 == 0, 16-byte aligned C rows and
+//    enough tiles to fill the chip.
 //  * gemm_kernel, the general fallback: 256x256 (8 waves) or 128x128 (4
 //    waves) tiles, register-staged double buffering, any K % 8 == 0.
 // Tiles are assigned XCD-aware (consecutive workgroups land on different
@@ -521,11 +524,14 @@ __global__ void __launch_bounds__(256, 1) gemm256_kernel(GemmArgs g) {
   const rsrc_t ra0 = make_rsrc(g.A, 0), rb0 = make_rsrc(g.B, 0);
   DTile<BM, BK, A_K> la;
   DTile<BN, BK, B_K> lb;
+  static_assert(DTile<BM, BK, A_K>::PER_WAVE == 9 && DTile<BN, BK, B_K>::PER_WAVE == 9,
+                "the k loop's load slots issue 9 pieces per half per wave");
   la.init(g.lda, m0, g.M);
   lb.init(g.ldb, n0, g.N);
   la.template issue<0, DTile<BM, BK, A_K>::PER_WAVE>(smem, ra, g.lda, kb);
   lb.template issue<0, DTile<BN, BK, B_K>::PER_WAVE>(smem + BM * R, rb, g.ldb, kb);
-  la.template issue<0, DTile<BM, BK, A_K>::PER_WAVE>(smem1, nk > 1 ? ra : ra0, g.lda, kb + BK);
+  // A pieces 0-7 of k-tile 1; the loop's first k-step issues piece 8
+  la.template issue<0, 8>(smem1, nk > 1 ? ra : ra0, g.lda, kb + BK);
   dma_barrier();
 
   // fragment of (row block I, k-step KS): lanes 0-31 hold rows, lanes 32-63
@@ -559,22 +565,36 @@ __global__ void __launch_bounds__(256, 1) gemm256_kernel(GemmArgs g) {
 #define RD_SEQ5(GA, GB, RB, RK) RD_A(GA, RB, RK, 1)
 #define RD_SEQ6(GA, GB, RB, RK) RD_A(GA, RB, RK, 2)
 #define RD_SEQ7(GA, GB, RB, RK) RD_A(GA, RB, RK, 3)
-// one row block of a k-step: 4 MFMAs on (FA, FB), two fragment reads of the
-// next k-step into (GA, GB) and part I of a tile cycle between them
-#define KSTEP_ROW(FA, FB, GA, GB, RB, RK, I, S0, S1, CYC) \
-  SB MMA2(FA, FB, I, 0) SB S0(GA, GB, RB, RK) SB MMA2(FA, FB, I, 2) SB S1(GA, GB, RB, RK) SB CYC(I)
+#define MMA1(FA, FB, I, J) acc[I][J] = mfma32<FP16>(FB[J], FA[I], acc[I][J]);
+// one row block of a k-step: 4 MFMAs, with two fragment reads of the next
+// k-step into (GA, GB) and two direct-load slots of a tile cycle between them
+#define KSTEP_ROW(FA, FB, GA, GB, RB, RK, I, S0, S1, CYC)                                        \
+  SB MMA1(FA, FB, I, 0) SB S0(GA, GB, RB, RK) SB MMA1(FA, FB, I, 1) SB CYC(2 * (I)) SB MMA1(FA, FB, I, 2) \
+  SB S1(GA, GB, RB, RK) SB MMA1(FA, FB, I, 3) SB CYC(2 * (I) + 1) SB
 #define NOCYC(P)
-#define CYC_A(P) la.template issue<(P) * 2, (P) == 3 ? 9 : (P) * 2 + 2>(cur, rsa, g.lda, k2);
-#define CYC_B(P) lb.template issue<(P) * 2, (P) == 3 ? 9 : (P) * 2 + 2>(nxt + BM * R, rsb, g.ldb, k1);
+// direct-load slot S (0-7) of a k-step issues one 1 KB piece (9 per half
+// per wave): pieces 0-7 of the A half of k-tile t+2 in the k-step after the
+// barrier, then piece 8 and B pieces 0-6 in the next, B pieces 7-8 in the
+// one after -- one load per slot, so no slot stalls the MFMA issue on a
+// burst of loads (spreading them this way measured 3% faster than two
+// bursts of 9)
+#define CYC_A(S) la.template issue<(S), (S) + 1>(cur, rsa, g.lda, k2);
+#define CYC_AB(S)                                                   \
+  if constexpr ((S) == 0)                                           \
+    la.template issue<8, 9>(nxt, rsa1, g.lda, k1);                  \
+  else                                                              \
+    lb.template issue<(S) - 1, (S)>(nxt + BM * R, rsb, g.ldb, k1);
+#define CYC_B2(S) \
+  if constexpr ((S) < 2) lb.template issue<(S) + 7, (S) + 8>(nxt + BM * R, rsb, g.ldb, k1);
 #define KSTEP(FA, FB, GA, GB, RB, RK, CYC)                     \
   KSTEP_ROW(FA, FB, GA, GB, RB, RK, 0, RD_SEQ0, RD_SEQ1, CYC) \
   KSTEP_ROW(FA, FB, GA, GB, RB, RK, 1, RD_SEQ2, RD_SEQ3, CYC) \
   KSTEP_ROW(FA, FB, GA, GB, RB, RK, 2, RD_SEQ4, RD_SEQ5, CYC) \
   KSTEP_ROW(FA, FB, GA, GB, RB, RK, 3, RD_SEQ6, RD_SEQ7, CYC) SB
-// k-tile KT: k-steps 0-2 from stage CUR while the B half of k-tile KT+1 is
-// loaded into NXT (its A half was started one k-step earlier); the barrier
-// (after this wave's direct loads have landed) means every wave is done
-// reading CUR and KT+1 is complete in NXT; k-step 3 then computes from
+// k-tile KT: k-steps 0-2 from stage CUR while the rest of k-tile KT+1 is
+// loaded into NXT (most of its A half was started one k-step earlier); the
+// barrier (after this wave's direct loads have landed) means every wave is
+// done reading CUR and KT+1 is complete in NXT; k-step 3 then computes from
 // registers, reads the first fragments of KT+1 from NXT and starts the A
 // half of k-tile KT+2 into CUR
 #define ITER(CUR, NXT, KT)                              \
@@ -585,8 +605,9 @@ __global__ void __launch_bounds__(256, 1) gemm256_kernel(GemmArgs g) {
     const int k2 = kb + ((KT) + 2) * BK;                \
     const rsrc_t rsb = (KT) + 1 < nk ? rb : rb0;        \
     const rsrc_t rsa = (KT) + 2 < nk ? ra : ra0;        \
-    KSTEP(fa0, fb0, fa1, fb1, cur, 1, CYC_B)            \
-    KSTEP(fa1, fb1, fa0, fb0, cur, 2, NOCYC)            \
+    const rsrc_t rsa1 = (KT) + 1 < nk ? ra : ra0;       \
+    KSTEP(fa0, fb0, fa1, fb1, cur, 1, CYC_AB)           \
+    KSTEP(fa1, fb1, fa0, fb0, cur, 2, CYC_B2)           \
     KSTEP(fa0, fb0, fa1, fb1, cur, 3, NOCYC)            \
     dma_barrier();                                      \
     KSTEP(fa1, fb1, fa0, fb0, nxt, 0, CYC_A)            \
@@ -602,7 +623,9 @@ __global__ void __launch_bounds__(256, 1) gemm256_kernel(GemmArgs g) {
 #undef ITER
 #undef KSTEP
 #undef CYC_A
-#undef CYC_B
+#undef CYC_AB
+#undef CYC_B2
+#undef MMA1
 #undef NOCYC
 #undef KSTEP_ROW
 #undef RD_SEQ0
