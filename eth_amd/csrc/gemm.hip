@@ -297,21 +297,31 @@ struct Tile256<ROWS, BK, NT, false> : MTile<ROWS, BK, NT> {};
 
 // Tile moved by direct global->LDS loads (buffer_load_dwordx4 ... lds):
 // lane i of an instruction writes its 16 bytes at the wave's LDS base +
-// 16 i, so the tile's LDS image, row padding included, is covered by
-// consecutive 1 KB pieces, PER_WAVE of them per wave; padding units get an
-// out-of-range offset (they read zeros).  KC: [ROWS][BK + 8] image of a
-// K-contiguous operand; otherwise [BK][ROWS + 32] of a row-contiguous one.
+// 16 i, so the tile's LDS image is covered by consecutive 1 KB pieces,
+// PER_WAVE of them per wave.
+//  * KC (K-contiguous operand): [ROWS][BK] image without padding; the
+//    16-byte unit p of row r holds k-chunk p ^ kc_swizzle(r) (the lane that
+//    fills unit p loads that chunk), so the fragment reads -- 16 lanes on
+//    16 consecutive rows, one chunk -- hit 16 distinct bank groups.
+//  * otherwise (row-contiguous operand): [BK][ROWS + 32] image as it is in
+//    memory; the padding units get an out-of-range offset (they read zeros).
 typedef __attribute__((address_space(3))) void lds_void_t;
 __device__ __forceinline__ void dma16(rsrc_t rs, uint16_t* lds, int32_t voff, int32_t soff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)lds, 16, voff, soff, 0, 0);
 }
+// injective on rows 0-7 and on the even and the odd rows of 0-15 (the rows
+// one 128-byte and one 256-byte bank sweep of a fragment read cover), and
+// periodic in 16 rows, so every 32-row fragment block shares it
+__device__ __forceinline__ int kc_swizzle(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 template <int ROWS, int BK, bool KC>
 struct DTile {
-  static constexpr int UPR = KC ? BK / 8 + 1 : ROWS / 8 + 4;  // 16-byte units per LDS row
-  static constexpr int DPR = KC ? BK / 8 : ROWS / 8;           // of which data
+  static constexpr int UPR = KC ? BK / 8 : ROWS / 8 + 4;  // 16-byte units per LDS row
+  static constexpr int DPR = KC ? BK / 8 : ROWS / 8;      // of which data
   static constexpr int NROW = KC ? ROWS : BK;
   static constexpr int PER_WAVE = NROW * UPR / 256;
+  static constexpr int IMG = NROW * UPR * 8;  // image size in elements
   static_assert(NROW * UPR % 256 == 0, "tile split");
+  static_assert(!KC || BK == 64, "the swizzle covers 8 chunks per row");
   int32_t off[PER_WAVE];
   int wave;
   __device__ __forceinline__ void init(int64_t ld, int r0, int rows) {
@@ -321,10 +331,10 @@ struct DTile {
     for (int j = 0; j < PER_WAVE; ++j) {
       const int u = (wave * PER_WAVE + j) * 64 + lane;
       const int row = u / UPR, c = u % UPR;
-      if (c >= DPR)
+      if (KC)
+        off[j] = r0 + row < rows ? (int32_t)((((int64_t)(r0 + row)) * ld + (c ^ kc_swizzle(row)) * 8) * 2) : kOob;
+      else if (c >= DPR)
         off[j] = kOob;
-      else if (KC)
-        off[j] = r0 + row < rows ? (int32_t)((((int64_t)(r0 + row)) * ld + c * 8) * 2) : kOob;
       else
         off[j] = r0 + c * 8 < rows ? (int32_t)(((int64_t)row * ld + r0 + c * 8) * 2) : kOob;
     }
@@ -480,12 +490,18 @@ __global__ void __launch_bounds__(64 * WAVES_M * WAVES_N) gemm_kernel(GemmArgs g
 // 256x256x64 tiles, 4 waves of 128x128 (one per SIMD), K % 128 == 0.
 template <bool A_K, bool B_K, bool FP16>
 __global__ void __launch_bounds__(256, 1) gemm256_kernel(GemmArgs g) {
-  constexpr int BM = 256, BN = 256, BK = 64, NT = 256, R = BK + kPad;
-  constexpr int STAGE = (BM + BN) * R;  // one LDS stage: A tile then B tile
+  constexpr int BM = 256, BN = 256, BK = 64;
+  typedef DTile<BM, BK, A_K> ATile;
+  typedef DTile<BN, BK, B_K> BTile;
+  constexpr int A_IMG = ATile::IMG;           // elements of the A image in a stage
+  constexpr int STAGE = A_IMG + BTile::IMG;   // one LDS stage: A image then B image
+  constexpr int ER = 128 + 4;                 // epilogue staging row (fp32, padded)
+  constexpr int EPI = 4 * 32 * ER * 2;        // epilogue staging in elements
   // the two stages are separate arrays, so the compiler can tell the direct
   // loads into one stage from the fragment reads of the other (it would
-  // otherwise wait for the loads before every read)
-  __shared__ __attribute__((aligned(16))) uint16_t smem[STAGE];
+  // otherwise wait for the loads before every read); the first also holds
+  // the epilogue's staging
+  __shared__ __attribute__((aligned(16))) uint16_t smem[STAGE > EPI ? STAGE : EPI];
   __shared__ __attribute__((aligned(16))) uint16_t smem1[STAGE];
 
   const int tiles_m = (g.M + BM - 1) / BM, tiles_n = (g.N + BN - 1) / BN;
@@ -522,34 +538,43 @@ __global__ void __launch_bounds__(256, 1) gemm256_kernel(GemmArgs g) {
   const rsrc_t ra = make_rsrc(g.A, g.a_bytes), rb = make_rsrc(g.B, g.b_bytes);
   // empty ranges: the loads issued past the last k-tile read zeros
   const rsrc_t ra0 = make_rsrc(g.A, 0), rb0 = make_rsrc(g.B, 0);
-  DTile<BM, BK, A_K> la;
-  DTile<BN, BK, B_K> lb;
-  static_assert(DTile<BM, BK, A_K>::PER_WAVE == 9 && DTile<BN, BK, B_K>::PER_WAVE == 9,
-                "the k loop's load slots issue 9 pieces per half per wave");
+  ATile la;
+  BTile lb;
+  // pieces per half per wave: 8 for a K-contiguous image, 9 for a padded one
+  constexpr int NA = ATile::PER_WAVE, NB = BTile::PER_WAVE;
+  static_assert((NA == 8 || NA == 9) && (NB == 8 || NB == 9), "the k loop's load slots");
   la.init(g.lda, m0, g.M);
   lb.init(g.ldb, n0, g.N);
-  la.template issue<0, DTile<BM, BK, A_K>::PER_WAVE>(smem, ra, g.lda, kb);
-  lb.template issue<0, DTile<BN, BK, B_K>::PER_WAVE>(smem + BM * R, rb, g.ldb, kb);
-  // A pieces 0-7 of k-tile 1; the loop's first k-step issues piece 8
+  la.template issue<0, NA>(smem, ra, g.lda, kb);
+  lb.template issue<0, NB>(smem + A_IMG, rb, g.ldb, kb);
+  // A pieces 0-7 of k-tile 1; the loop's first k-step issues a piece 8
   la.template issue<0, 8>(smem1, nk > 1 ? ra : ra0, g.lda, kb + BK);
   dma_barrier();
 
   // fragment of (row block I, k-step KS): lanes 0-31 hold rows, lanes 32-63
   // the second 8 k of the 16
-  // K-contiguous tiles: [row][BK + 8], one 16-byte read per fragment;
+  // K-contiguous tiles: [row][64] swizzled, one 16-byte read per fragment
+  // (the unit of k-chunk 2 KS + lane / 32 depends on KS through the
+  // swizzle, so each k-step has its own lane offset; row block I is a
+  // constant 32 rows further, with the same swizzle);
   // row-contiguous tiles: [BK][256 + 32], two transposing reads (tr_frag)
   constexpr int LM = BM + 32;
   const int trl = ((lane >> 5) * 8 + ((lane & 15) >> 2)) * LM + ((lane >> 4) & 1) * 16 + (lane & 3) * 4;
-  const int a_frag = A_K ? (wm * 128 + lr) * R + lk : trl + wm * 128;
-  const int b_frag = BM * R + (B_K ? (wn * 128 + lr) * R + lk : trl + wn * 128);
+  int a_frag[4], b_frag[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    const int ra_ = wm * 128 + lr, rb_ = wn * 128 + lr;
+    a_frag[ks] = A_K ? ra_ * BK + ((2 * ks + (lane >> 5)) ^ kc_swizzle(ra_)) * 8 : trl + wm * 128 + ks * 16 * LM;
+    b_frag[ks] = A_IMG + (B_K ? rb_ * BK + ((2 * ks + (lane >> 5)) ^ kc_swizzle(rb_)) * 8 : trl + wn * 128 + ks * 16 * LM);
+  }
   uint4 fa0[4], fb0[4], fa1[4], fb1[4];
 #define SB __builtin_amdgcn_sched_barrier(0);
-#define RD_A(FA, BASE, KS, I)                                                              \
-  FA[I] = A_K ? *reinterpret_cast<const uint4*>((BASE) + a_frag + (I) * 32 * R + (KS) * 16) \
-              : tr_frag((BASE) + a_frag + (I) * 32 + (KS) * 16 * LM, LM);
-#define RD_B(FB, BASE, KS, J)                                                              \
-  FB[J] = B_K ? *reinterpret_cast<const uint4*>((BASE) + b_frag + (J) * 32 * R + (KS) * 16) \
-              : tr_frag((BASE) + b_frag + (J) * 32 + (KS) * 16 * LM, LM);
+#define RD_A(FA, BASE, KS, I)                                                         \
+  FA[I] = A_K ? *reinterpret_cast<const uint4*>((BASE) + a_frag[KS] + (I) * 32 * BK) \
+              : tr_frag((BASE) + a_frag[KS] + (I) * 32, LM);
+#define RD_B(FB, BASE, KS, J)                                                         \
+  FB[J] = B_K ? *reinterpret_cast<const uint4*>((BASE) + b_frag[KS] + (J) * 32 * BK) \
+              : tr_frag((BASE) + b_frag[KS] + (J) * 32, LM);
 // B fragment as the MFMA's first operand: the lane then holds 4 consecutive
 // output columns (r % 4) of one output row (lane % 32)
 #define MMA2(FA, FB, I, J0)                                         \
@@ -572,20 +597,20 @@ __global__ void __launch_bounds__(256, 1) gemm256_kernel(GemmArgs g) {
   SB MMA1(FA, FB, I, 0) SB S0(GA, GB, RB, RK) SB MMA1(FA, FB, I, 1) SB CYC(2 * (I)) SB MMA1(FA, FB, I, 2) \
   SB S1(GA, GB, RB, RK) SB MMA1(FA, FB, I, 3) SB CYC(2 * (I) + 1) SB
 #define NOCYC(P)
-// direct-load slot S (0-7) of a k-step issues one 1 KB piece (9 per half
-// per wave): pieces 0-7 of the A half of k-tile t+2 in the k-step after the
-// barrier, then piece 8 and B pieces 0-6 in the next, B pieces 7-8 in the
-// one after -- one load per slot, so no slot stalls the MFMA issue on a
-// burst of loads (spreading them this way measured 3% faster than two
-// bursts of 9)
+// direct-load slot S (0-7) of a k-step issues one 1 KB piece: pieces 0-7
+// of the A half of k-tile t+2 in the k-step after the barrier, then, one
+// per slot over the next k-step and a half, the rest of k-tile t+2 (queue
+// position Q: A piece 8 first when the A image has 9 pieces, then the B
+// pieces) -- one load per slot, so no slot stalls the MFMA issue on a burst
+// of loads (measured 3% faster than two bursts of 9)
 #define CYC_A(S) la.template issue<(S), (S) + 1>(cur, rsa, g.lda, k2);
-#define CYC_AB(S)                                                   \
-  if constexpr ((S) == 0)                                           \
-    la.template issue<8, 9>(nxt, rsa1, g.lda, k1);                  \
-  else                                                              \
-    lb.template issue<(S) - 1, (S)>(nxt + BM * R, rsb, g.ldb, k1);
-#define CYC_B2(S) \
-  if constexpr ((S) < 2) lb.template issue<(S) + 7, (S) + 8>(nxt + BM * R, rsb, g.ldb, k1);
+#define LOAD_Q(Q)                                                                            \
+  if constexpr (NA == 9 && (Q) == 0)                                                         \
+    la.template issue<8, 9>(nxt, rsa1, g.lda, k1);                                           \
+  else if constexpr ((Q) - (NA - 8) < NB)                                                    \
+    lb.template issue<(Q) - (NA - 8), (Q) - (NA - 8) + 1>(nxt + A_IMG, rsb, g.ldb, k1);
+#define CYC_AB(S) LOAD_Q(S)
+#define CYC_B2(S) LOAD_Q((S) + 8)
 #define KSTEP(FA, FB, GA, GB, RB, RK, CYC)                     \
   KSTEP_ROW(FA, FB, GA, GB, RB, RK, 0, RD_SEQ0, RD_SEQ1, CYC) \
   KSTEP_ROW(FA, FB, GA, GB, RB, RK, 1, RD_SEQ2, RD_SEQ3, CYC) \
@@ -625,6 +650,7 @@ __global__ void __launch_bounds__(256, 1) gemm256_kernel(GemmArgs g) {
 #undef CYC_A
 #undef CYC_AB
 #undef CYC_B2
+#undef LOAD_Q
 #undef MMA1
 #undef NOCYC
 #undef KSTEP_ROW
@@ -646,7 +672,6 @@ __global__ void __launch_bounds__(256, 1) gemm256_kernel(GemmArgs g) {
   // whole rows, two rows per store instruction.  C goes through a buffer
   // resource spanning exactly its extent, so rows past M are dropped by the
   // hardware; lanes whose columns are past N get an out-of-range offset.
-  constexpr int ER = 128 + 4;
   float* stage = reinterpret_cast<float*>(smem) + wid * 32 * ER;
   const int esz = g.c_dtype == ETH_F32 ? 4 : 2;
   const int mode = g.c_dtype == ETH_BF16 ? 0 : g.c_dtype == ETH_F16 ? 1 : (g.flags & ETH_GEMM_ACCUMULATE) ? 3 : 2;
