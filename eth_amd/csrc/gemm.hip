@@ -15,19 +15,23 @@
 // thread), so every LDS tile is stored K-contiguous and each MFMA operand is
 // one 16-byte LDS read.
 //
-// Two kernels:
-//  * gemm256_kernel, the main one: 256x256x64 tiles, 4 waves (one per SIMD)
-//    of 128x128 each, 256 accumulator registers per lane held in AGPRs.
-//    Operands go global -> LDS with direct loads (buffer_load ... lds) into
-//    two stages.  The k loop is software-pipelined by hand: while the MFMAs
-//    of k-tile t run, k-tile t+1 streams into the other stage, one 1 KB
-//    load per MFMA gap, and the fragments of the next k-step are read from
-//    LDS between the MFMAs (sched_barrier fixes the order).  One barrier
-//    per k-tile.  Row-contiguous operands land as they are in memory and
-//    their fragments come out of LDS through ds_read_b64_tr_b16.  The
-//    epilogue stages each 32-row slab through LDS and writes whole rows
-//    with buffer stores.  Needs K % 128 == 0, 16-byte aligned C rows and
-//    enough tiles to fill the chip.
+// Kernels:
+//  * gemm256_m16_kernel / gemm256_m32_kernel, the main ones: 256x256x64
+//    tiles, 4 waves (one per SIMD) of 128x128 each, 256 accumulator
+//    registers per lane held in AGPRs.  Operands go global -> LDS with
+//    direct loads (buffer_load ... lds) into two stages.  The k loop is
+//    software-pipelined by hand: while the MFMAs of k-tile t run, k-tile
+//    t+1 streams into the other stage, one 1 KB load per few MFMA gaps,
+//    and the next fragments are read from LDS between the MFMAs
+//    (sched_barrier fixes the order).  One barrier per k-tile.
+//    Row-contiguous operands land as they are in memory and their
+//    fragments come out of LDS through ds_read_b64_tr_b16.  The epilogue
+//    stages each 32-row slab through LDS and writes whole rows with buffer
+//    stores.  m16 (v_mfma_f32_16x16x32, single-buffered fragments) serves a
+//    K-contiguous A (forward and data-gradient products), m32
+//    (v_mfma_f32_32x32x16) a row-contiguous A (weight gradients).  Both
+//    need K % 128 == 0, 16-byte aligned C rows and enough tiles to fill
+//    the chip.
 //  * gemm_kernel, the general fallback: 256x256 (8 waves) or 128x128 (4
 //    waves) tiles, register-staged double buffering, any K % 8 == 0.
 // Tiles are assigned XCD-aware (consecutive workgroups land on different
@@ -45,6 +49,7 @@ namespace eth {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
@@ -361,6 +366,11 @@ __device__ __forceinline__ uint4 tr_frag(const uint16_t* p, int lrow) {
   return make_uint4(lo.x, lo.y, hi.x, hi.y);
 }
 
+// The same for the 16x16x32 layout: lane l passes the address of k-row
+// k0 + (l%16)/4 (k0 = 8*(l/16)), element row0 + 4*(l%4); it receives row
+// row0 + l%16, k = k0 .. k0+7.
+__device__ __forceinline__ uint4 tr_frag16(const uint16_t* p, int lrow) { return tr_frag(p, lrow); }
+
 struct GemmArgs {
   const uint16_t* A;
   const uint16_t* B;
@@ -372,7 +382,7 @@ struct GemmArgs {
   int c_dtype;
   int flags;
   float alpha;
-  uint32_t c_bytes;  // extent of C (gemm256_kernel's store range)
+  uint32_t c_bytes;  // extent of C (the gemm256 kernels' store range)
   int k_split;              // split-K: k extent per split (0: one split of K)
   int64_t c_split_stride;   // split-K: elements between the splits' C slices
 };
@@ -488,8 +498,299 @@ __global__ void __launch_bounds__(64 * WAVES_M * WAVES_N) gemm_kernel(GemmArgs g
 }
 
 // 256x256x64 tiles, 4 waves of 128x128 (one per SIMD), K % 128 == 0.
+//
+// MFMA v_mfma_f32_16x16x32: a 128x128 wave tile is 8 x 8 blocks of 16x16,
+// 4 fp32 accumulators per lane each (256 in all, AGPRs).  A k-tile of 64 is
+// two k-steps of 32; a k-step is 64 MFMAs, preceded by the 16 fragment reads
+// (8 A row blocks, 8 B column blocks) that feed it.  The 16x16x32 shape
+// (twice the MFMA instructions of 32x32x16 for the same work) leaves more
+// issue gaps between MFMAs for the fragment reads and direct loads: the same
+// tile with 32x32x16 MFMAs ran 6% slower.
+template <bool FP16>
+__device__ __forceinline__ f32x4_t mfma16(const uint4& a, const uint4& b, const f32x4_t& c) {
+  if constexpr (FP16) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b),
+                                                  c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  }
+}
+
 template <bool A_K, bool B_K, bool FP16>
-__global__ void __launch_bounds__(256, 1) gemm256_kernel(GemmArgs g) {
+__global__ void __launch_bounds__(256, 1) gemm256_m16_kernel(GemmArgs g) {
+  constexpr int BM = 256, BN = 256, BK = 64;
+  typedef DTile<BM, BK, A_K> ATile;
+  typedef DTile<BN, BK, B_K> BTile;
+  constexpr int A_IMG = ATile::IMG;           // elements of the A image in a stage
+  constexpr int STAGE = A_IMG + BTile::IMG;   // one LDS stage: A image then B image
+  constexpr int ER = 128 + 4;                 // epilogue staging row (fp32, padded)
+  constexpr int EPI = 4 * 32 * ER * 2;        // epilogue staging in elements
+  // the two stages are separate arrays, so the compiler can tell the direct
+  // loads into one stage from the fragment reads of the other (it would
+  // otherwise wait for the loads before every read); the first also holds
+  // the epilogue's staging
+  __shared__ __attribute__((aligned(16))) uint16_t smem[STAGE > EPI ? STAGE : EPI];
+  __shared__ __attribute__((aligned(16))) uint16_t smem1[STAGE];
+
+  const int tiles_m = (g.M + BM - 1) / BM, tiles_n = (g.N + BN - 1) / BN;
+  // split-K launches tiles * splits workgroups: split = blockIdx.x / tiles
+  const int tiles = tiles_m * tiles_n;
+  const int split = blockIdx.x / tiles;
+  const int kb = split * g.k_split;
+  int tm, tn;
+  tile_coords(blockIdx.x - split * tiles, tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int wm = wid >> 1, wn = wid & 1;
+  const int l16 = lane & 15, lg = lane >> 4;
+  // the 4 output columns this lane writes in the epilogue, and their bias
+  // (read now so its latency is hidden behind the k loop)
+  const int col = (lane & 31) * 4;
+  const int n = n0 + wn * 128 + col;
+  float bn[4] = {0.f, 0.f, 0.f, 0.f};
+  if ((g.flags & ETH_GEMM_BIAS) && g.bias) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (n + e < g.N) bn[e] = FP16 ? h2f_bits(g.bias[n + e]) : bf2f(g.bias[n + e]);
+  }
+
+  // acc[I][J]: C rows I*16 + lane%16, columns J*16 + 4*(lane/16) + 0..3 of
+  // the wave's block (B fragment as the MFMA's first operand)
+  f32x4_t acc[8][8];
+  // pinned to AGPRs where they start, so the register allocator keeps each
+  // block in one AGPR tuple and every MFMA accumulates in place (unpinned,
+  // it parks some blocks in VGPRs and copies them around the MFMAs)
+#define PIN_ACC                                          \
+  _Pragma("unroll") for (int i = 0; i < 8; ++i)          \
+    _Pragma("unroll") for (int j = 0; j < 8; ++j) asm volatile("" : "+a"(acc[i][j]));
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  PIN_ACC
+
+  const int nk = (g.k_split ? g.k_split : g.K) / BK;
+  const rsrc_t ra = make_rsrc(g.A, g.a_bytes), rb = make_rsrc(g.B, g.b_bytes);
+  // empty ranges: the loads issued past the last k-tile read zeros
+  const rsrc_t ra0 = make_rsrc(g.A, 0), rb0 = make_rsrc(g.B, 0);
+  ATile la;
+  BTile lb;
+  // pieces per half per wave: 8 for a K-contiguous image, 9 for a padded one
+  constexpr int NA = ATile::PER_WAVE, NB = BTile::PER_WAVE;
+  static_assert((NA == 8 || NA == 9) && (NB == 8 || NB == 9), "the k loop's load slots");
+  la.init(g.lda, m0, g.M);
+  lb.init(g.ldb, n0, g.N);
+  la.template issue<0, NA>(smem, ra, g.lda, kb);
+  lb.template issue<0, NB>(smem + A_IMG, rb, g.ldb, kb);
+
+  // queue item Q of a k-tile (the A pieces, then the B pieces) into stage S
+#define LOAD_Q(Q, S, RSA, RSB, KK)                                      \
+  if constexpr ((Q) < NA) {                                             \
+    la.template issue<(Q), (Q) + 1>(S, RSA, g.lda, KK);                 \
+  } else if constexpr ((Q) < NA + NB) {                                 \
+    lb.template issue<(Q) - NA, (Q) - NA + 1>((S) + A_IMG, RSB, g.ldb, KK); \
+  }
+  // queue items 0-11 of k-tile 1 (the loop's first k-step issues the rest)
+  {
+    const rsrc_t rsa = nk > 1 ? ra : ra0, rsb = nk > 1 ? rb : rb0;
+#define PRO_Q(Q) LOAD_Q(Q, smem1, rsa, rsb, kb + BK)
+    PRO_Q(0) PRO_Q(1) PRO_Q(2) PRO_Q(3) PRO_Q(4) PRO_Q(5)
+    PRO_Q(6) PRO_Q(7) PRO_Q(8) PRO_Q(9) PRO_Q(10) PRO_Q(11)
+#undef PRO_Q
+  }
+  dma_barrier();
+
+  // Fragment of row block I (16 rows) for k-step KS (32 k): lane l holds row
+  // l%16, k 8*(l/16) .. +7.
+  // K-contiguous images ([row][64], swizzled): one 16-byte read; the unit of
+  // k-chunk 4 KS + l/16 depends on KS through the swizzle, so each k-step has
+  // its own lane offset, and row block I is a constant 16 rows further (the
+  // swizzle has period 16).
+  // Row-contiguous images ([64][256 + 32]): two transposing reads of 4 k.
+  constexpr int LM = BM + 32;
+  int a_frag[2], b_frag[2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    const int trl = (32 * ks + 8 * lg + (l16 >> 2)) * LM + (l16 & 3) * 4;
+    const int kc = ((4 * ks + lg) ^ kc_swizzle(l16)) * 8;
+    a_frag[ks] = A_K ? (wm * 128 + l16) * BK + kc : trl + wm * 128;
+    b_frag[ks] = A_IMG + (B_K ? (wn * 128 + l16) * BK + kc : trl + wn * 128);
+  }
+  // One set of fragments, each re-read as soon as its last MFMA of the
+  // k-step has issued.  A k-step's 64 MFMAs run the (row block, column
+  // block) pairs column-major, first over row blocks 0-3, then over 4-7:
+  //  * A0-A3 die at MFMA 31 and are re-read (next k-step) right after it;
+  //  * Bj dies at MFMA 35 + 4j (row block 7) and is re-read right after it,
+  //    29 MFMAs before the next k-step's first use (MFMA 4j);
+  //  * A4-A7 die at MFMA 63 and are read in the next k-step's first four
+  //    gaps, 28 MFMAs before their first use (MFMA 32).
+  // The barrier comes 12 MFMAs into the second k-step of a k-tile, after
+  // that k-step's own A4-A7 reads from the stage; then direct loads, one
+  // every fourth MFMA gap, refill the stage with k-tile t+2 (12 pieces in
+  // this k-step, the other 4-6 in the next).
+  uint4 fa[8], fb[8];
+#define SB __builtin_amdgcn_sched_barrier(0);
+#define RD_A(BASE, KS, I)                                                             \
+  fa[I] = A_K ? *reinterpret_cast<const uint4*>((BASE) + a_frag[KS] + (I) * 16 * BK) \
+              : tr_frag((BASE) + a_frag[KS] + (I) * 16, LM);
+#define RD_B(BASE, KS, J)                                                             \
+  fb[J] = B_K ? *reinterpret_cast<const uint4*>((BASE) + b_frag[KS] + (J) * 16 * BK) \
+              : tr_frag((BASE) + b_frag[KS] + (J) * 16, LM);
+#define MM(I, J) acc[I][J] = mfma16<FP16>(fb[J], fa[I], acc[I][J]);
+  // items 0-11 of k-tile t+2 in the barrier k-step of k-tile t, the rest
+  // in the first k-step of k-tile t+1
+#define LOAD_CUR(Q) LOAD_Q(Q, cur, rsa2, rsb2, k2)
+#define LOAD_NXT(Q) LOAD_Q(Q, nxt, rsa1, rsb1, k1)
+#define KSTEP_A(OB, OK, NB, NK)    \
+  SB MM(0, 0) SB RD_A(OB, OK, 4) SB MM(1, 0) SB RD_A(OB, OK, 5) SB MM(2, 0) SB RD_A(OB, OK, 6) SB    \
+  LOAD_NXT(12) SB MM(3, 0) SB RD_A(OB, OK, 7) SB MM(0, 1) SB MM(1, 1) SB MM(2, 1) SB LOAD_NXT(13) SB \
+  MM(3, 1) SB MM(0, 2) SB MM(1, 2) SB MM(2, 2) SB LOAD_NXT(14) SB MM(3, 2) SB MM(0, 3) SB            \
+  MM(1, 3) SB MM(2, 3) SB LOAD_NXT(15) SB MM(3, 3) SB MM(0, 4) SB MM(1, 4) SB MM(2, 4) SB            \
+  LOAD_NXT(16) SB MM(3, 4) SB MM(0, 5) SB MM(1, 5) SB MM(2, 5) SB LOAD_NXT(17) SB MM(3, 5) SB        \
+  MM(0, 6) SB MM(1, 6) SB MM(2, 6) SB MM(3, 6) SB MM(0, 7) SB MM(1, 7) SB MM(2, 7) SB MM(3, 7) SB    \
+  MM(4, 0) SB RD_A(NB, NK, 0) SB MM(5, 0) SB RD_A(NB, NK, 1) SB MM(6, 0) SB RD_A(NB, NK, 2) SB       \
+  MM(7, 0) SB RD_B(NB, NK, 0) SB MM(4, 1) SB RD_A(NB, NK, 3) SB MM(5, 1) SB MM(6, 1) SB MM(7, 1) SB  \
+  RD_B(NB, NK, 1) SB MM(4, 2) SB MM(5, 2) SB MM(6, 2) SB MM(7, 2) SB RD_B(NB, NK, 2) SB MM(4, 3) SB  \
+  MM(5, 3) SB MM(6, 3) SB MM(7, 3) SB RD_B(NB, NK, 3) SB MM(4, 4) SB MM(5, 4) SB MM(6, 4) SB         \
+  MM(7, 4) SB RD_B(NB, NK, 4) SB MM(4, 5) SB MM(5, 5) SB MM(6, 5) SB MM(7, 5) SB RD_B(NB, NK, 5) SB  \
+  MM(4, 6) SB MM(5, 6) SB MM(6, 6) SB MM(7, 6) SB RD_B(NB, NK, 6) SB MM(4, 7) SB MM(5, 7) SB         \
+  MM(6, 7) SB MM(7, 7) SB RD_B(NB, NK, 7) SB
+#define KSTEP_B(OB, OK, NB, NK)    \
+  SB MM(0, 0) SB RD_A(OB, OK, 4) SB MM(1, 0) SB RD_A(OB, OK, 5) SB MM(2, 0) SB RD_A(OB, OK, 6) SB    \
+  MM(3, 0) SB RD_A(OB, OK, 7) SB MM(0, 1) SB MM(1, 1) SB MM(2, 1) SB MM(3, 1) SB MM(0, 2) SB         \
+  MM(1, 2) SB MM(2, 2) SB MM(3, 2) SB dma_barrier(); SB MM(0, 3) SB LOAD_CUR(0) SB MM(1, 3) SB       \
+  MM(2, 3) SB MM(3, 3) SB MM(0, 4) SB LOAD_CUR(1) SB MM(1, 4) SB MM(2, 4) SB MM(3, 4) SB MM(0, 5) SB \
+  LOAD_CUR(2) SB MM(1, 5) SB MM(2, 5) SB MM(3, 5) SB MM(0, 6) SB LOAD_CUR(3) SB MM(1, 6) SB          \
+  MM(2, 6) SB MM(3, 6) SB MM(0, 7) SB LOAD_CUR(4) SB MM(1, 7) SB MM(2, 7) SB MM(3, 7) SB MM(4, 0) SB \
+  LOAD_CUR(5) SB RD_A(NB, NK, 0) SB MM(5, 0) SB RD_A(NB, NK, 1) SB MM(6, 0) SB RD_A(NB, NK, 2) SB    \
+  MM(7, 0) SB RD_B(NB, NK, 0) SB MM(4, 1) SB LOAD_CUR(6) SB RD_A(NB, NK, 3) SB MM(5, 1) SB           \
+  MM(6, 1) SB MM(7, 1) SB RD_B(NB, NK, 1) SB MM(4, 2) SB LOAD_CUR(7) SB MM(5, 2) SB MM(6, 2) SB      \
+  MM(7, 2) SB RD_B(NB, NK, 2) SB MM(4, 3) SB LOAD_CUR(8) SB MM(5, 3) SB MM(6, 3) SB MM(7, 3) SB      \
+  RD_B(NB, NK, 3) SB MM(4, 4) SB LOAD_CUR(9) SB MM(5, 4) SB MM(6, 4) SB MM(7, 4) SB                  \
+  RD_B(NB, NK, 4) SB MM(4, 5) SB LOAD_CUR(10) SB MM(5, 5) SB MM(6, 5) SB MM(7, 5) SB                 \
+  RD_B(NB, NK, 5) SB MM(4, 6) SB LOAD_CUR(11) SB MM(5, 6) SB MM(6, 6) SB MM(7, 6) SB                 \
+  RD_B(NB, NK, 6) SB MM(4, 7) SB MM(5, 7) SB MM(6, 7) SB MM(7, 7) SB RD_B(NB, NK, 7) SB
+
+#define ITER(CUR, NXT, KT)                                \
+  {                                                       \
+    uint16_t* const cur = (CUR);                          \
+    uint16_t* const nxt = (NXT);                          \
+    const int k1 = kb + ((KT) + 1) * BK;                  \
+    const int k2 = kb + ((KT) + 2) * BK;                  \
+    const rsrc_t rsa1 = (KT) + 1 < nk ? ra : ra0;         \
+    const rsrc_t rsb1 = (KT) + 1 < nk ? rb : rb0;         \
+    const rsrc_t rsa2 = (KT) + 2 < nk ? ra : ra0;         \
+    const rsrc_t rsb2 = (KT) + 2 < nk ? rb : rb0;         \
+    KSTEP_A(cur, 0, cur, 1)                               \
+    KSTEP_B(cur, 1, nxt, 0)                               \
+  }
+  SB RD_A(smem, 0, 0) SB RD_A(smem, 0, 1) SB RD_A(smem, 0, 2) SB RD_A(smem, 0, 3) SB
+#pragma unroll
+  for (int j = 0; j < 8; ++j) { RD_B(smem, 0, j) }
+  SB
+  // two k-tiles per trip, so both LDS stages have fixed addresses
+  for (int kt = 0; kt < nk; kt += 2) {
+    ITER(smem, smem1, kt)
+    ITER(smem1, smem, kt + 1)
+  }
+#undef PIN_ACC
+#undef ITER
+#undef KSTEP_A
+#undef KSTEP_B
+#undef LOAD_Q
+#undef LOAD_CUR
+#undef LOAD_NXT
+#undef MM
+#undef RD_A
+#undef RD_B
+#undef SB
+
+  // Epilogue: each wave stages one 32-row slab of its 128x128 block at a
+  // time in its own LDS region (fp32, padded rows) and writes it back as
+  // whole rows, two rows per store instruction.  C goes through a buffer
+  // resource spanning exactly its extent, so rows past M are dropped by the
+  // hardware; lanes whose columns are past N get an out-of-range offset.
+  float* stage = reinterpret_cast<float*>(smem) + wid * 32 * ER;
+  const int esz = g.c_dtype == ETH_F32 ? 4 : 2;
+  const int mode = g.c_dtype == ETH_BF16 ? 0 : g.c_dtype == ETH_F16 ? 1 : (g.flags & ETH_GEMM_ACCUMULATE) ? 3 : 2;
+  const rsrc_t rc = make_rsrc(reinterpret_cast<float*>(g.C) + split * g.c_split_stride, g.c_bytes);
+  const int32_t row2 = (int32_t)(2 * g.ldc * esz);
+  auto write_slab = [&](const int i) __attribute__((always_inline)) {
+    // the slab is private to this wave, whose LDS accesses complete in order
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    float4 v[16];
+#pragma unroll
+    for (int it = 0; it < 16; ++it) {
+      v[it] = *reinterpret_cast<const float4*>(stage + (it * 2 + (lane >> 5)) * ER + col);
+      v[it].x = v[it].x * g.alpha + bn[0];
+      v[it].y = v[it].y * g.alpha + bn[1];
+      v[it].z = v[it].z * g.alpha + bn[2];
+      v[it].w = v[it].w * g.alpha + bn[3];
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    const int mrow = m0 + wm * 128 + i * 32 + (lane >> 5);
+    const int32_t voff = n < g.N ? (int32_t)(((int64_t)mrow * g.ldc + n) * esz) : kOob;
+#define OFF(IT) (voff == kOob ? kOob : voff + (IT) * row2)
+    if (mode == 0) {
+#pragma unroll
+      for (int it = 0; it < 16; ++it) {
+        u32x2_t o;
+        o.x = f2bf_pair(v[it].x, v[it].y);
+        o.y = f2bf_pair(v[it].z, v[it].w);
+        __builtin_amdgcn_raw_buffer_store_b64(o, rc, OFF(it), 0, 0);
+      }
+    } else if (mode == 1) {
+#pragma unroll
+      for (int it = 0; it < 16; ++it) {
+        u32x2_t o;
+        o.x = f2h_bits(v[it].x) | ((uint32_t)f2h_bits(v[it].y) << 16);
+        o.y = f2h_bits(v[it].z) | ((uint32_t)f2h_bits(v[it].w) << 16);
+        __builtin_amdgcn_raw_buffer_store_b64(o, rc, OFF(it), 0, 0);
+      }
+    } else if (mode == 2) {
+#pragma unroll
+      for (int it = 0; it < 16; ++it)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v[it]), rc, OFF(it), 0, 0);
+    } else {
+      // fp32 C += (the main_grad accumulation): all loads first
+      u32x4_t old[16];
+#pragma unroll
+      for (int it = 0; it < 16; ++it) old[it] = __builtin_amdgcn_raw_buffer_load_b128(rc, OFF(it), 0, 0);
+#pragma unroll
+      for (int it = 0; it < 16; ++it) {
+        float4 o = __builtin_bit_cast(float4, old[it]);
+        o.x += v[it].x;
+        o.y += v[it].y;
+        o.z += v[it].z;
+        o.w += v[it].w;
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, o), rc, OFF(it), 0, 0);
+      }
+    }
+#undef OFF
+  };
+  dma_barrier();  // every wave is done with the k-loop stages, no load in flight
+  // slab S: row blocks 2S, 2S+1 -> staging rows (I % 2) * 16 + lane % 16
+#define STAGE_SLAB(S)                                                                     \
+  {                                                                                       \
+    _Pragma("unroll") for (int h = 0; h < 2; ++h)                                         \
+      _Pragma("unroll") for (int j = 0; j < 8; ++j) {                                     \
+        const f32x4_t a = acc[2 * (S) + h][j];                                            \
+        *reinterpret_cast<float4*>(stage + (h * 16 + l16) * ER + j * 16 + lg * 4) =      \
+            make_float4(a[0], a[1], a[2], a[3]);                                          \
+      }                                                                                   \
+    write_slab(S);                                                                        \
+  }
+  STAGE_SLAB(0) STAGE_SLAB(1) STAGE_SLAB(2) STAGE_SLAB(3)
+#undef STAGE_SLAB
+}
+
+// The same tiles with v_mfma_f32_32x32x16 (4 x 4 blocks of 32x32 per wave,
+// 16 accumulators per lane each), for a row-contiguous A: with transposing
+// reads on both operands the 16x16x32 kernel does not keep its accumulators
+// in place in AGPRs (the register allocator moves them around every MFMA).
+template <bool A_K, bool B_K, bool FP16>
+__global__ void __launch_bounds__(256, 1) gemm256_m32_kernel(GemmArgs g) {
   constexpr int BM = 256, BN = 256, BK = 64;
   typedef DTile<BM, BK, A_K> ATile;
   typedef DTile<BN, BK, B_K> BTile;
@@ -749,13 +1050,13 @@ template <bool FP16>
 static int launch_256(const GemmArgs& a, int a_k, int b_k, hipStream_t s, int splits = 1) {
   const int tiles = ((a.M + 255) / 256) * ((a.N + 255) / 256) * splits;
   if (a_k && b_k)
-    gemm256_kernel<true, true, FP16><<<tiles, 256, 0, s>>>(a);
+    gemm256_m16_kernel<true, true, FP16><<<tiles, 256, 0, s>>>(a);
   else if (a_k && !b_k)
-    gemm256_kernel<true, false, FP16><<<tiles, 256, 0, s>>>(a);
+    gemm256_m16_kernel<true, false, FP16><<<tiles, 256, 0, s>>>(a);
   else if (!a_k && !b_k)
-    gemm256_kernel<false, false, FP16><<<tiles, 256, 0, s>>>(a);
+    gemm256_m32_kernel<false, false, FP16><<<tiles, 256, 0, s>>>(a);
   else
-    gemm256_kernel<false, true, FP16><<<tiles, 256, 0, s>>>(a);
+    gemm256_m32_kernel<false, true, FP16><<<tiles, 256, 0, s>>>(a);
   ETH_CHECK_LAUNCH("eth_gemm");
   return ETH_OK;
 }
