@@ -339,7 +339,7 @@ def main():
         "step_mfma_frac": step_tflops / PEAK_BF16_TFLOPS,
         "grad_norm": norm,
         "roofline": {
-            "kernel": "eth_gemm (gemm256_kernel + gemm_kernel, all GEMM launches of the timed steps)",
+            "kernel": "eth_gemm (gemm256_m16_kernel, gemm256_m32_kernel and gemm_kernel: all GEMM launches of the timed steps)",
             "bound": "mfma",
             "achieved": gemm_tflops,
             "peak": PEAK_BF16_TFLOPS,
