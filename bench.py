@@ -38,10 +38,11 @@ H, HEADS, FFN, SEQ, MB, LAYERS = 2048, 16, 8192, 2048, 4, 6
 # HBM (L2-miss) bytes per GEMM launch of one stage step, from the FETCH_SIZE /
 # WRITE_SIZE counter runs (each scaled by what it reads for a 1 GiB copy:
 # 2.0 and 1.0) recorded in profiles/gemm_traffic_stage_step_gpt1p3b.md; the
-# algorithmic bytes (A + B + C, plus the fp32 main_grad read and write of a
-# weight gradient) of the same launches for comparison
-GEMM_TRAFFIC_BYTES_PER_LAUNCH = 420.1e6
-GEMM_ALGORITHMIC_BYTES_PER_LAUNCH = 184.5e6
+# algorithmic bytes (A + B + C, a weight gradient storing its fp32 main_grad:
+# the step's only contribution after the deferred zeroing) of the same
+# launches for comparison
+GEMM_TRAFFIC_BYTES_PER_LAUNCH = 422.3e6
+GEMM_ALGORITHMIC_BYTES_PER_LAUNCH = 167.8e6
 
 
 def quiet_gc():
