@@ -75,6 +75,14 @@ __device__ __forceinline__ void lds_barrier() {
 __device__ __forceinline__ void dma_barrier() {
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
+// The same with the newest N vector-memory loads of this wave still in
+// flight (loads complete in issue order): the prologues start on k-tile 0
+// while k-tile 1 is still arriving.
+template <int N>
+__device__ __forceinline__ void dma_barrier_but() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
 
 // Map a linear workgroup id to (tile_m, tile_n): XCD-contiguous, then
 // GROUP_M-row grouped.
@@ -599,7 +607,7 @@ __global__ void __launch_bounds__(256, 1) gemm256_m16_kernel(GemmArgs g) {
     PRO_Q(6) PRO_Q(7) PRO_Q(8) PRO_Q(9) PRO_Q(10) PRO_Q(11)
 #undef PRO_Q
   }
-  dma_barrier();
+  dma_barrier_but<12>();
 
   // Fragment of row block I (16 rows) for k-step KS (32 k): lane l holds row
   // l%16, k 8*(l/16) .. +7.
@@ -850,7 +858,7 @@ __global__ void __launch_bounds__(256, 1) gemm256_m32_kernel(GemmArgs g) {
   lb.template issue<0, NB>(smem + A_IMG, rb, g.ldb, kb);
   // A pieces 0-7 of k-tile 1; the loop's first k-step issues a piece 8
   la.template issue<0, 8>(smem1, nk > 1 ? ra : ra0, g.lda, kb + BK);
-  dma_barrier();
+  dma_barrier_but<8>();
 
   // fragment of (row block I, k-step KS): lanes 0-31 hold rows, lanes 32-63
   // the second 8 k of the 16
