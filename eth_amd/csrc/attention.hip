@@ -63,6 +63,9 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
     return f2bf_pair(a, b);
 }
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+// s_waitcnt vmcnt(0) (expcnt, lgkmcnt unconstrained) as the builtin, so the
+// compiler's own wait-count tracking knows that no vector load is pending
+__device__ __forceinline__ void vm_wait_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 // 8 fp32 -> one 16-byte MFMA operand
 template <bool FP16>
 __device__ __forceinline__ uint4 pack8(const float* v) {
@@ -222,6 +225,11 @@ __global__ void __launch_bounds__(kAttnThreads, 2) attn_fwd_kernel(AttnArgs a) {
   vt.store(Vs[0]);
   const int vtr = tr_lane(lane, VL);
   __syncthreads();
+  // the Q fragment loads may still be in flight here; waiting for them now
+  // (through the builtin, which the compiler's wait-count pass sees) keeps
+  // that pass from making every iteration's first MFMAs wait for the next
+  // block's prefetch loads
+  vm_wait_all();
 
   for (int j = 0; j < nkv; ++j) {
     const int st = j & 1;
@@ -360,9 +368,18 @@ __global__ void __launch_bounds__(kAttnThreads, PART == 3 ? 1 : 2) attn_bwd_dkdv
   dt.init(a.dout, b, h);
   const int qtr = tr_lane(lane, QN);
   const int first = (kb * kBKV2) / kBQ2, nq = a.S / kBQ2;
-  // the next step's Q / dO rows are loaded while this step computes
+  // the next step's Q / dO rows, and its queries' lse and delta, are loaded
+  // while this step computes
+  float lse_n = 0.f, del_n = 0.f;
+  auto load_stats = [&](int qs) __attribute__((always_inline)) {
+    if (threadIdx.x < kBQ2) {
+      lse_n = a.lse[(int64_t)bh * a.S + qs + threadIdx.x];
+      if constexpr (DK) del_n = a.delta[(int64_t)bh * a.S + qs + threadIdx.x];
+    }
+  };
   qt.load(first * kBQ2);
   dt.load(first * kBQ2);
+  load_stats(first * kBQ2);
   for (int qb = first; qb < nq; ++qb) {
     const int qs0 = qb * kBQ2;
     __syncthreads();  // previous step's LDS readers are done
@@ -373,13 +390,14 @@ __global__ void __launch_bounds__(kAttnThreads, PART == 3 ? 1 : 2) attn_bwd_dkdv
     }
     if constexpr (DV) dt.template store_natural<QN>(dOn);
     if (threadIdx.x < kBQ2) {
-      lse_s[threadIdx.x] = a.lse[(int64_t)bh * a.S + qs0 + threadIdx.x];
-      if constexpr (DK) del_s[threadIdx.x] = a.delta[(int64_t)bh * a.S + qs0 + threadIdx.x];
+      lse_s[threadIdx.x] = lse_n;
+      if constexpr (DK) del_s[threadIdx.x] = del_n;
     }
     __syncthreads();
     if (qb + 1 < nq) {
       qt.load(qs0 + kBQ2);
       dt.load(qs0 + kBQ2);
+      load_stats(qs0 + kBQ2);
     }
     if (qs0 + kBQ2 - 1 < k0) continue;  // every query of the step precedes this wave's keys
     const bool diag = qs0 < k0 + 31;
