@@ -159,7 +159,7 @@ def test_layer_norm_fwd_bwd(cuda, dtype, rows, cols):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("rows,cols", [(300, 256), (1000, 2048), (33, 4096), (5, 8), (40, 1536), (17, 8192)])
+@pytest.mark.parametrize("rows,cols", [(300, 256), (1000, 2048), (2100, 1032), (33, 4096), (5, 8), (40, 1536), (17, 8192)])
 def test_layer_norm_bwd_residual_colsum(cuda, dtype, rows, cols):
     """LayerNorm backward fused with the residual gradient: dx equals the
     plain backward's dx plus dresid, rounded as two 16-bit tensors and a
