@@ -29,15 +29,13 @@ def _rel(a, b):
     return (a - b).norm().item() / (b.norm().item() + 1e-30)
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-def test_middle_stage_matches_fp32_oracle(cuda, dtype):
-    announce(f"middle stage parity {dtype}")
-    cfg = GPTConfig(hidden_size=256, num_attention_heads=4, ffn_hidden_size=1024, num_layers=2,
-                    seq_length=128, micro_batch_size=2, params_dtype=dtype, device="cuda", seed=5)
+def _stage_parity(cuda, dtype, hidden, heads, ffn, layers, seq, mb, seed):
+    cfg = GPTConfig(hidden_size=hidden, num_attention_heads=heads, ffn_hidden_size=ffn, num_layers=layers,
+                    seq_length=seq, micro_batch_size=mb, params_dtype=dtype, device="cuda", seed=seed)
     tr = MiddleStageTrainer(cfg, lr=1e-4, weight_decay=0.1, clip_grad=1.0)
     gen = torch.Generator().manual_seed(77)
-    x = torch.randn(128, 2, 256, generator=gen).to(dtype)
-    dy = (torch.randn(128, 2, 256, generator=gen) * 1e-2).to(dtype)
+    x = torch.randn(seq, mb, hidden, generator=gen).to(dtype)
+    dy = (torch.randn(seq, mb, hidden, generator=gen) * 1e-2).to(dtype)
     params = tr.layer_parameters()
     # give biases / LN params non-trivial values so their paths are exercised
     with torch.no_grad():
@@ -52,7 +50,7 @@ def test_middle_stage_matches_fp32_oracle(cuda, dtype):
     tr.ddp.zero_grad_buffer()
     out, dx = tr.forward_backward(x.to(cuda), dy.to(cuda))
     torch.cuda.synchronize()
-    ref_out, ref_dx, ref_grads = ol.middle_stage_fwd_bwd(x.float(), host, 4, dy.float())
+    ref_out, ref_dx, ref_grads = ol.middle_stage_fwd_bwd(x.float(), host, heads, dy.float())
     assert _rel(out, ref_out) < 2e-2
     assert _rel(dx, ref_dx) < 2e-2
     for li, (layer, ref) in enumerate(zip(params, ref_grads)):
@@ -62,6 +60,21 @@ def test_middle_stage_matches_fp32_oracle(cuda, dtype):
             gn, rn = g.double().norm().item(), ref[k].double().norm().item()
             assert abs(gn - rn) <= 2e-2 * rn + 1e-12, f"layer {li} {k}: |g| {gn} vs {rn}"
             assert _rel(g, ref[k]) < 5e-2, f"layer {li} {k}: rel err {_rel(g, ref[k])}"
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_middle_stage_matches_fp32_oracle(cuda, dtype):
+    announce(f"middle stage parity {dtype}")
+    _stage_parity(cuda, dtype, hidden=256, heads=4, ffn=1024, layers=2, seq=128, mb=2, seed=5)
+
+
+def test_middle_stage_layer_at_bench_shape_matches_fp32_oracle(cuda):
+    """One layer at the benchmarked shape (hidden 2048, 16 heads of 128,
+    FFN 8192, seq 2048, micro-batch 4, bf16): the widths that select the
+    production GEMM tiles, the 128-wide attention kernels and the
+    1025-2048-column LayerNorm backward."""
+    announce("middle stage parity at the bench shape (1 layer, 8192 tokens)")
+    _stage_parity(cuda, torch.bfloat16, hidden=2048, heads=16, ffn=8192, layers=1, seq=2048, mb=4, seed=5)
 
 
 def test_deferred_zero_matches_eager_zero(cuda):
