@@ -27,9 +27,10 @@
 //    Row-contiguous operands land as they are in memory and their
 //    fragments come out of LDS through ds_read_b64_tr_b16.  The epilogue
 //    stages each 32-row slab through LDS and writes whole rows with buffer
-//    stores.  m16 (v_mfma_f32_16x16x32, single-buffered fragments) serves a
-//    K-contiguous A (forward and data-gradient products), m32
-//    (v_mfma_f32_32x32x16) a row-contiguous A (weight gradients).  Both
+//    stores.  m16 (v_mfma_f32_16x16x32, single-buffered fragments) serves
+//    the forward, data-gradient and weight-gradient products (for the last,
+//    both operands row-contiguous, through asm MFMAs); m32
+//    (v_mfma_f32_32x32x16) a row-contiguous A with a K-contiguous B.  Both
 //    need K % 128 == 0, 16-byte aligned C rows and enough tiles to fill
 //    the chip.
 //  * gemm_kernel, the general fallback: 256x256 (8 waves) or 128x128 (4
@@ -525,6 +526,25 @@ __device__ __forceinline__ f32x4_t mfma16(const uint4& a, const uint4& b, const 
   }
 }
 
+// The same MFMA as inline assembly with the accumulator tied to its AGPRs
+// ("+a"), for the kernel whose operands both come through transposing
+// reads: through the builtin the register allocator there keeps some 30
+// accumulator tuples in VGPRs and copies them around the MFMAs every k-tile.
+// The compiler still inserts the LDS waits for the operands (it sees the
+// asm's register uses); the only hazard it cannot see, an accumulator read
+// right after its MFMA, is covered after the k loop.
+template <bool FP16>
+__device__ __forceinline__ void mfma16_asm(f32x4_t& c, const uint4& a, const uint4& b) {
+  if constexpr (FP16)
+    asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0"
+                 : "+a"(c)
+                 : "v"(__builtin_bit_cast(u32x4_t, a)), "v"(__builtin_bit_cast(u32x4_t, b)));
+  else
+    asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0"
+                 : "+a"(c)
+                 : "v"(__builtin_bit_cast(u32x4_t, a)), "v"(__builtin_bit_cast(u32x4_t, b)));
+}
+
 template <bool A_K, bool B_K, bool FP16>
 __global__ void __launch_bounds__(256, 1) gemm256_m16_kernel(GemmArgs g) {
   constexpr int BM = 256, BN = 256, BK = 64;
@@ -645,7 +665,11 @@ __global__ void __launch_bounds__(256, 1) gemm256_m16_kernel(GemmArgs g) {
 #define RD_B(BASE, KS, J)                                                             \
   fb[J] = B_K ? *reinterpret_cast<const uint4*>((BASE) + b_frag[KS] + (J) * 16 * BK) \
               : tr_frag((BASE) + b_frag[KS] + (J) * 16, LM);
-#define MM(I, J) acc[I][J] = mfma16<FP16>(fb[J], fa[I], acc[I][J]);
+#define MM(I, J)                                  \
+  if constexpr (A_K)                              \
+    acc[I][J] = mfma16<FP16>(fb[J], fa[I], acc[I][J]); \
+  else                                            \
+    mfma16_asm<FP16>(acc[I][J], fb[J], fa[I]);
   // items 0-11 of k-tile t+2 in the barrier k-step of k-tile t, the rest
   // in the first k-step of k-tile t+1
 #define LOAD_CUR(Q) LOAD_Q(Q, cur, rsa2, rsb2, k2)
@@ -702,6 +726,8 @@ __global__ void __launch_bounds__(256, 1) gemm256_m16_kernel(GemmArgs g) {
     ITER(smem, smem1, kt)
     ITER(smem1, smem, kt + 1)
   }
+  // asm MFMAs: wait states before any instruction reads their accumulators
+  if constexpr (!A_K) asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
 #undef PIN_ACC
 #undef ITER
 #undef KSTEP_A
@@ -1062,7 +1088,7 @@ static int launch_256(const GemmArgs& a, int a_k, int b_k, hipStream_t s, int sp
   else if (a_k && !b_k)
     gemm256_m16_kernel<true, false, FP16><<<tiles, 256, 0, s>>>(a);
   else if (!a_k && !b_k)
-    gemm256_m32_kernel<false, false, FP16><<<tiles, 256, 0, s>>>(a);
+    gemm256_m16_kernel<false, false, FP16><<<tiles, 256, 0, s>>>(a);
   else
     gemm256_m32_kernel<false, true, FP16><<<tiles, 256, 0, s>>>(a);
   ETH_CHECK_LAUNCH("eth_gemm");
