@@ -41,7 +41,7 @@ H, HEADS, FFN, SEQ, MB, LAYERS = 2048, 16, 8192, 2048, 4, 6
 # algorithmic bytes (A + B + C, a weight gradient storing its fp32 main_grad:
 # the step's only contribution after the deferred zeroing) of the same
 # launches for comparison
-GEMM_TRAFFIC_BYTES_PER_LAUNCH = 422.3e6
+GEMM_TRAFFIC_BYTES_PER_LAUNCH = 409.0e6
 GEMM_ALGORITHMIC_BYTES_PER_LAUNCH = 167.8e6
 
 
