@@ -8,69 +8,77 @@ path, logical id, shared-weight id, root flag, required, TP semantics), and
 which fixes every topology field of the descriptor.
 """
 
+import functools
+
 from .metadata import LocalGradientBinding, SerializableGradientDescriptor
 
-PARAMETERLESS_OPS = {
-    "enc-attention-score",
-    "enc-attention-softmax",
-    "enc-attention-dropout",
-    "enc-attention-context",
-    "enc-flash-attention",
-    "enc-post-attention-dropout",
-    "enc-MLP-gelu",
-    "enc-post-MLP-dropout",
+# ops without trainable parameters (the flash path's attention pieces, the
+# dropouts and the GELU)
+PARAMETERLESS_OPS = frozenset(
+    {
+        "enc-attention-score",
+        "enc-attention-softmax",
+        "enc-attention-dropout",
+        "enc-attention-context",
+        "enc-flash-attention",
+        "enc-post-attention-dropout",
+        "enc-MLP-gelu",
+        "enc-post-MLP-dropout",
+    }
+)
+
+# gradient semantics of a linear's (weight, bias) by the op's `algo`:
+# column-parallel splits both along dim 0; row-parallel splits the weight
+# along dim 1 and replicates the bias
+LINEAR_SEMANTICS = {"column": ("sharded_dim0", "sharded_dim0"), "row": ("sharded_dim1", "replicated")}
+
+# op name -> logical component of its (weight, bias) pair
+_NORM_COMPONENTS = {
+    "enc-1st-layernorm": "gpt.layers.{layer}.attention.input_layernorm",
+    "enc-2nd-layernorm": "gpt.layers.{layer}.mlp.input_layernorm",
+    "final-layernorm": "gpt.final_layernorm",
+}
+_LINEAR_COMPONENTS = {
+    "enc-attention-qkv": ("query_key_value", "gpt.layers.{layer}.attention.query_key_value"),
+    "enc-attention-dense": ("dense", "gpt.layers.{layer}.attention.dense"),
+    "enc-MLP-GEMM-1": ("dense", "gpt.layers.{layer}.mlp.dense_h_to_4h"),
+    "enc-MLP-GEMM-2": ("dense", "gpt.layers.{layer}.mlp.dense_4h_to_h"),
+}
+# entries: (path on the op, logical id, shared-weight id, shared root,
+#           required, gradient semantics)
+_VOCAB_ENTRIES = {
+    "encoder-embedding": (
+        ("word_embeddings.weight", "gpt.word_embeddings.weight", "gpt.word_embeddings", True, True, "sharded_dim0"),
+        ("position_embeddings.weight", "gpt.position_embeddings.weight", None, False, True, "replicated"),
+        ("tokentype_embeddings.weight", "gpt.tokentype_embeddings.weight", None, False, False, "replicated"),
+    ),
+    "gpt-post-process": (
+        ("word_embeddings.weight", "gpt.output_head.word_embeddings.weight", "gpt.word_embeddings", False, True,
+         "sharded_dim0"),
+    ),
 }
 
 
-def _linear_semantics(op):
-    algo = getattr(op, "algo", None)
-    if algo == "column":
-        return "sharded_dim0", "sharded_dim0"
-    if algo == "row":
-        return "sharded_dim1", "replicated"
-    raise ValueError(f"runtime op {getattr(op, 'op_index', None)} has unsupported linear algo {algo!r}")
-
-
 def parameter_schema(op, layer_index):
+    """The (path, logical id, shared id, root, required, semantics) entries of
+    one manifest op, in parameter order."""
     name = op.name
-    pre = f"gpt.layers.{layer_index}"
-    if name == "encoder-embedding":
-        return (
-            ("word_embeddings.weight", "gpt.word_embeddings.weight", "gpt.word_embeddings", True, True, "sharded_dim0"),
-            ("position_embeddings.weight", "gpt.position_embeddings.weight", None, False, True, "replicated"),
-            ("tokentype_embeddings.weight", "gpt.tokentype_embeddings.weight", None, False, False, "replicated"),
+    if name in _VOCAB_ENTRIES:
+        return _VOCAB_ENTRIES[name]
+    if name in _NORM_COMPONENTS:
+        comp = _NORM_COMPONENTS[name].format(layer=layer_index)
+        return tuple(
+            (f"input_layernorm.{leaf}", f"{comp}.{leaf}", None, False, True, "replicated") for leaf in ("weight", "bias")
         )
-    if name in ("enc-1st-layernorm", "enc-2nd-layernorm", "final-layernorm"):
-        comp = {
-            "enc-1st-layernorm": f"{pre}.attention.input_layernorm",
-            "enc-2nd-layernorm": f"{pre}.mlp.input_layernorm",
-            "final-layernorm": "gpt.final_layernorm",
-        }[name]
-        return (
-            ("input_layernorm.weight", f"{comp}.weight", None, False, True, "replicated"),
-            ("input_layernorm.bias", f"{comp}.bias", None, False, True, "replicated"),
-        )
-    if name == "enc-attention-qkv":
-        w, b = "sharded_dim0", "sharded_dim0"
-        comp = f"{pre}.attention.query_key_value"
-        return (
-            ("query_key_value.weight", f"{comp}.weight", None, False, True, w),
-            ("query_key_value.bias", f"{comp}.bias", None, False, True, b),
-        )
-    if name in ("enc-attention-dense", "enc-MLP-GEMM-1", "enc-MLP-GEMM-2"):
-        w, b = _linear_semantics(op)
-        comp = {
-            "enc-attention-dense": f"{pre}.attention.dense",
-            "enc-MLP-GEMM-1": f"{pre}.mlp.dense_h_to_4h",
-            "enc-MLP-GEMM-2": f"{pre}.mlp.dense_4h_to_h",
-        }[name]
-        return (
-            ("dense.weight", f"{comp}.weight", None, False, True, w),
-            ("dense.bias", f"{comp}.bias", None, False, True, b),
-        )
-    if name == "gpt-post-process":
-        return (
-            ("word_embeddings.weight", "gpt.output_head.word_embeddings.weight", "gpt.word_embeddings", False, True, "sharded_dim0"),
+    if name in _LINEAR_COMPONENTS:
+        module, comp = _LINEAR_COMPONENTS[name]
+        comp = comp.format(layer=layer_index)
+        algo = "column" if name == "enc-attention-qkv" else getattr(op, "algo", None)
+        if algo not in LINEAR_SEMANTICS:
+            raise ValueError(f"runtime op {getattr(op, 'op_index', None)} has unsupported linear algo {algo!r}")
+        return tuple(
+            (f"{module}.{leaf}", f"{comp}.{leaf}", None, False, True, sem)
+            for leaf, sem in zip(("weight", "bias"), LINEAR_SEMANTICS[algo])
         )
     if name in PARAMETERLESS_OPS:
         return ()
@@ -78,12 +86,8 @@ def parameter_schema(op, layer_index):
 
 
 def _resolve(root, path):
-    value = root
-    for part in path.split("."):
-        if value is None or not hasattr(value, part):
-            return None
-        value = getattr(value, part)
-    return value
+    """root.a.b.c, or None when any link is missing."""
+    return functools.reduce(lambda obj, attr: getattr(obj, attr, None) if obj is not None else None, path.split("."), root)
 
 
 def collect_stage_metadata(ops, stage_op_begin, stage_op_end, model_impl="gpt", manifest_hash="manifest"):

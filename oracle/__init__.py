@@ -14,15 +14,28 @@ Modules:
 
 Pinning (what each function is checked against, in tests/):
   gradsync.pack_bucket / execute   -> reference known answers restated in
-      tests/golden/grad_sync_known_answers.json (executor strided pack
+      tests/golden/known_answers.json (executor strided pack
       [0,1,2,6,7,8,3,4,5,9,10,11], scratch tail, replicated x0.5) and the
-      invariant sum(exact_numel) == sum(numel)
-  gradsync.l2_norm / clip          -> [3,4,0,0] -> 5.0 -> [1.2,1.6,0,0],
-      zeros 2, inf-norm 1.6 (golden); fp64 brute force
+      invariant sum(exact_numel) == sum(numel)   [test_grad_sync_host.py]
+  gradsync.l2_norm / clip / inf_norm / count_zeros
+                                   -> [3,4,0,0] -> 5.0 -> [1.2,1.6,0,0],
+      zeros 2, inf-norm 1.6 (golden)
+  gradsync.unscale_and_check       -> non-finite flag and the exact
+      power-of-two scale (closed forms)
   adamw.adamw_step                 -> torch.optim.AdamW (third-party, the
       reference's FusedAdam fallback) and the step-1 closed form
       m = 0.1 g, v = 0.05 g^2 (golden)
-  layer.*                          -> torch.nn.functional (F.layer_norm,
-      F.gelu(tanh), F.scaled_dot_product_attention(is_causal),
-      F.cross_entropy) and fp64 brute force on tiny shapes
-"""
+  adamw.to_bf16                    -> torch's round-to-nearest-even cast
+  layer.layer_norm / bias_gelu     -> eps 1e-5 and tanh-GELU closed values
+  layer.causal_attention           -> the explicit masked softmax (fp64)
+  layer.vocab_cross_entropy        -> F.cross_entropy at the reference's own
+      bar (13x17 rows, V 11, logits x1000, error < 1e-6; the unshifted
+      form fails it) and ln V for uniform logits
+  layer.transformer_layer          -> closed forms: zero weights give
+      x + proj_b + fc2_b; per-head q|k|v split; causal running mean along
+      the sequence axis; MLP = fc2 gelu(fc1 bias); gradients by gradcheck
+  layer.middle_stage_fwd_bwd       -> central differences of <stage(x), dy>
+  layer.full_model_fwd_bwd         -> zero tied head: loss ln V and the
+      closed-form tied gradient; central differences along the word table
+      (tied sum), position table, final LN and a layer weight
+  [test_oracle_pins.py, test_grad_sync_host.py]

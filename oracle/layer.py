@@ -11,7 +11,8 @@ Follows eth/runtime/megatron/model/flex_ops.py:
   * proj / fc2: F.linear without bias (skip_bias_add), bias added in
     bias-dropout-add: residual + dropout(x + b) (flex_ops.py:104-134)
   * fc1 + GELU: F.gelu(x + b, approximate="tanh") (flex_ops.py:60-63,1897)
-  * LM head + cross entropy: logits = h @ E^T, loss = logsumexp - z[label]
+  * LM head + cross entropy: logits = h @ E^T, max-subtracted
+    loss = log sum exp(z - max) - (z[label] - max)
     (model/language_model.py:126-141, mpu/cross_entropy.py:36-92)
 """
 
@@ -88,10 +89,18 @@ def middle_stage_fwd_bwd(x, layers, heads, dy, dtype=torch.float32):
 
 
 def vocab_cross_entropy(logits, labels):
-    """Per-token loss = logsumexp(z) - z[label] in fp32 (the fp32 cast of
-    flex_ops.py:1976-1981)."""
-    z = logits.float()
-    return torch.logsumexp(z, dim=-1) - z.gather(-1, labels.unsqueeze(-1)).squeeze(-1)
+    """Per-token loss of _VocabParallelCrossEntropy at TP = 1
+    (mpu/cross_entropy.py:36-92): subtract the row maximum, then
+    loss = log(sum(exp(z - max))) - (z[label] - max).  The maximum is a
+    constant of the backward, as in the reference's autograd Function.
+
+    Computes in the dtype it is given (fp32 for the reference's
+    `output.float()`, flex_ops.py:1976-1981; fp64 in the fp64 oracle); 16-bit
+    logits are widened to fp32 first."""
+    z = logits if logits.dtype in (torch.float32, torch.float64) else logits.float()
+    shifted = z - z.detach().amax(dim=-1, keepdim=True)
+    target = shifted.gather(-1, labels.unsqueeze(-1)).squeeze(-1)
+    return torch.log(torch.exp(shifted).sum(dim=-1)) - target
 
 
 def full_model_fwd_bwd(tokens, positions, loss_mask, params, heads, labels=None, dtype=torch.float64):

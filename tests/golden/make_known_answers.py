@@ -83,6 +83,82 @@ RECORDS = {
         "expected_exp_avg_over_grad": 0.1,
         "expected_exp_avg_sq_over_grad_sq": 0.05,
     },
+    "loss_contract_global_mean": {
+        "source": "tests/test_global_loss_and_clock.py:127-152",
+        "microbatches": [
+            {"losses": [1.0, 2.0, 3.0], "mask": [1.0, 0.0, 1.0]},
+            {"losses": [4.0, 5.0], "mask": [1.0, 0.0]},
+        ],
+        "nominal_global_loss_scale": 8.0,
+        "expected_local_loss_sum": [4.0, 4.0],
+        "expected_local_loss_weight": [2.0, 1.0],
+        "expected_normalized_grads": [[1 / 3, 0.0, 1 / 3], [1 / 3, 0.0]],
+    },
+    "loss_aggregation": {
+        "source": "tests/test_global_loss_and_clock.py:241-253",
+        "outputs": [[2.0, 1.0], [6.0, 1.0], [12.0, 2.0]],
+        "expected_numerator": 20.0,
+        "expected_weight": 4.0,
+        "expected_mean": 5.0,
+    },
+    "training_clock": {
+        "source": "tests/test_global_loss_and_clock.py:207-219",
+        "total_gbs": 10,
+        "global_data_cursor": 20,
+        "successful_optimizer_steps": 3,
+        "attempts": [False, True],
+        "expected_returns": [0, 10],
+        "expected_cursor": 40,
+        "expected_steps": 4,
+    },
+    "training_clock_restore": {
+        "source": "tests/test_global_loss_and_clock.py:221-239",
+        "checkpoint": {"consumed_train_samples": 12, "global_data_cursor": 30, "successful_optimizer_steps": 4},
+        "legacy_checkpoint": {"consumed_train_samples": 12},
+        "iteration": 7,
+        "expected": [30, 4],
+        "expected_legacy": [12, 7],
+    },
+    "sample_slots": {
+        "source": "tests/test_global_loss_and_clock.py:160-200 (the slots listed here follow from its sequences)",
+        "mbs_sequences": [[[4, 8], [2, 8]], [[2, 8], [2, 8]]],
+        "pipeline_sample_offsets": [0, 6],
+        "total_gbs": 10,
+        "cases": [
+            [[0, 0, 1, 0, 0], [0, 1, 2, 3]],
+            [[0, 0, 2, 0, 0], [0, 1]],
+            [[0, 0, 2, 1, 0], [2, 3]],
+            [[0, 1, 2, 1, 0], [5]],
+            [[1, 0, 2, 1, 0], [7]],
+            [[1, 1, 1, 0, 0], [8, 9]],
+            [[0, 0, 1, 0, 10], [10, 11, 12, 13]],
+        ],
+    },
+    "synthetic_gpt_batch": {
+        "source": "grad_sync/loss.py:100-119 (values computed by hand from the LCG); "
+                  "tests/test_global_loss_and_clock.py:202-205 uses the (0,1)/(2,3), s 4, V 100 batches",
+        "cases": [
+            {"ids": [0, 1], "seq": 4, "vocab": 100, "tokens": [[0, 45, 90, 35], [45, 90, 35, 80]],
+             "mask": [[0, 1, 1, 1], [1, 1, 1, 0]]},
+            {"ids": [2, 3], "seq": 4, "vocab": 100, "tokens": [[90, 35, 80, 25], [35, 80, 25, 70]],
+             "mask": [[1, 1, 0, 1], [1, 0, 1, 1]]},
+            {"ids": [3, 8], "seq": 6, "vocab": 50257,
+             "tokens": [[16631, 28976, 41321, 3409, 15754, 28099], [27597, 39942, 2030, 14375, 26720, 39065]],
+             "mask": [[1, 0, 1, 1, 1, 0], [0, 1, 1, 1, 0, 1]]},
+        ],
+    },
+    "dynamic_loss_scale": {
+        "source": "optimizer/grad_scaler.py:99-119 (update rule), arguments.py:644 (hysteresis 2)",
+        "initial_scale": 65536.0,
+        "min_scale": 16384.0,
+        "growth_factor": 2.0,
+        "backoff_factor": 0.5,
+        "growth_interval": 3,
+        "hysteresis": 2,
+        "found_inf": [False, False, False, True, False, True, True, True, True, False, False, False],
+        "expected_scale": [65536.0, 65536.0, 131072.0, 131072.0, 131072.0, 65536.0, 32768.0, 16384.0, 16384.0,
+                           16384.0, 16384.0, 32768.0],
+    },
     "main_grad_accumulation": {
         "source": "tests/test_local_ddp_runtime.py:48-72",
         "param": [1.0, 2.0],

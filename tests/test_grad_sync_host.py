@@ -14,7 +14,6 @@ from eth_amd.grad_sync.planner import (
     ProcessGroupSpec,
     TensorSegmentSpec,
     plan_canonical_fragments,
-    shard_intervals,
 )
 from oracle import adamw as oadam
 from oracle import gradsync as og
@@ -99,13 +98,6 @@ def test_gpt_1p3b_grad_list_gives_121_block_and_288_tensor_buckets():
             assert p.destination_offset == off
             off += next(f.numel for f in block.canonical_fragments if f.fragment_id == p.fragment_id)
         assert off == b.exact_numel
-
-
-def test_shard_intervals_with_stride():
-    assert shard_intervals(8, 2, 0, 2, "w") == ((0, 2), (4, 6))
-    assert shard_intervals(8, 2, 1, 2, "w") == ((2, 4), (6, 8))
-    with pytest.raises(ValueError):
-        shard_intervals(6, 4, 0, 1, "w")
 
 
 def test_replicated_tp2_contributes_half_and_sharded_tp2_splits():
