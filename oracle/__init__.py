@@ -39,3 +39,4 @@ Pinning (what each function is checked against, in tests/):
       closed-form tied gradient; central differences along the word table
       (tied sum), position table, final LN and a layer weight
   [test_oracle_pins.py, test_grad_sync_host.py]
+"""
