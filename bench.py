@@ -7,17 +7,22 @@ gradient N(0, 1e-3), dropout 0.  A step is: zero main grads, forward,
 backward (input + weight gradients into fp32 main grads), Block-wise grad
 sync (32 MiB buckets; pack / unpack with the fused unscale-flag-L2
 statistics), clip at 1.0, fused AdamW (lr 1e-4, betas .9/.95, eps 1e-8,
-wd 0.1) with the bf16 model copy.
+wd 0.1) with the bf16 model copy.  Inputs are resident in HBM before the
+timed region.
 
-Prints one JSON line.  `value` is tokens/s of the whole step; `roofline`
-covers the dominant kernel (the MFMA GEMM): algorithmic FLOPs of its
-launches / their summed duration, from HIP events recorded on the launch
-stream around every GEMM of the timed steps.  `hbm_path` reports the
-grad-pack+unscale+L2 pass and AdamW at BASELINE configs[2]/[3] scale
-(1,208,598,528 fp32 elements).  `first_last_stage` times the GPT-6.7B
-first+last stage in fp16.  `cpu_baseline` times the oracle's torch-CPU
-fp32 restatement of one layer (forward + backward + grad sync + AdamW) on
-the host cores, on a bounded sample, scaled to the 6-layer stage.
+Prints one JSON line.  `value` is tokens/s of the K timed steps (wall clock
+between two device synchronizations); `step_ms_median` / `step_ms_p90` come
+from HIP events around each step on the compute stream.  `roofline` covers
+the dominant kernel, the MFMA GEMM: its algorithmic FLOPs per launch over
+its average launch duration, both from HIP events recorded on the launch
+stream around every GEMM of separate instrumented steps (the timed steps run
+without the events).  `attention` gives the same for the attention forward
+and backward.  `hbm_path` reports grad pack+unscale(2^-16)+inf flag+L2+
+unpack (also with 0.1 % of the gradients +inf) and AdamW at BASELINE
+configs[2]/[3] scale (1,208,598,528 fp32 elements).  `first_last_stage`
+times the GPT-6.7B first+last stage in fp16.
+`cpu_baseline` times this build's torch-CPU restatement of the same step on
+the host cores (the oracle; the reference's Python does not travel).
 """
 
 import argparse
@@ -25,6 +30,7 @@ import gc
 import json
 import math
 import os
+import re
 import sys
 import time
 
@@ -35,14 +41,10 @@ if ROOT not in sys.path:
 PEAK_BF16_TFLOPS = 2516.0  # MI355X dense bf16 MFMA (2.5 PFLOP/s)
 PEAK_HBM_GBPS = 8000.0     # MI355X HBM3E
 H, HEADS, FFN, SEQ, MB, LAYERS = 2048, 16, 8192, 2048, 4, 6
-# HBM (L2-miss) bytes per GEMM launch of one stage step, from the FETCH_SIZE /
-# WRITE_SIZE counter runs (each scaled by what it reads for a 1 GiB copy:
-# 2.0 and 1.0) recorded in profiles/gemm_traffic_stage_step_gpt1p3b.md; the
-# algorithmic bytes (A + B + C, a weight gradient storing its fp32 main_grad:
-# the step's only contribution after the deferred zeroing) of the same
-# launches for comparison
-GEMM_TRAFFIC_BYTES_PER_LAUNCH = 409.0e6
-GEMM_ALGORITHMIC_BYTES_PER_LAUNCH = 167.8e6
+# the committed FETCH_SIZE / WRITE_SIZE counter summary of the GEMM launches
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemm_traffic_stage_step_gpt1p3b.md")
+# host threads for the CPU baseline: the GPU box's CPU share per GPU
+CPU_THREADS_CAP = 16
 
 
 def quiet_gc():
@@ -63,108 +65,211 @@ def step_flops(layers=LAYERS, s=SEQ, b=MB, h=H, f=FFN):
     return 3 * per_layer * layers
 
 
-class GemmMeter:
-    """Records HIP events around every GEMM launch, on the stream the launch
-    goes to, and sums FLOPs.  The weight-gradient GEMMs of the timed steps
-    run on a side stream, overlapped with the data-gradient chain, so
-    launches can overlap in time: `busy_ms` is the length of the union of
-    the launch intervals (time during which at least one GEMM ran), and
-    `total_ms` the plain sum of launch durations."""
+def percentile(values, q):
+    v = sorted(values)
+    if not v:
+        return None
+    k = (len(v) - 1) * q
+    lo, hi = math.floor(k), math.ceil(k)
+    return v[lo] + (v[hi] - v[lo]) * (k - lo)
+
+
+class KernelMeter:
+    """HIP events around every GEMM / attention launch, recorded on the
+    stream the launch goes to, with the launch's algorithmic FLOPs.
+    Weight-gradient GEMMs run on a side stream, overlapped with the
+    data-gradient chain, so launches can overlap in time."""
 
     def __init__(self, torch):
         self.torch = torch
-        self.events = []
-        self.flops = 0.0
+        self.launches = {}  # kind -> [[begin, end, flops]]
         self.base = torch.cuda.Event(enable_timing=True)
         self.base.record()
 
-    def __call__(self, phase, M, N, K):
+    def __call__(self, kind, phase, flops):
+        e = self.torch.cuda.Event(enable_timing=True)
+        e.record()
         if phase == "begin":
-            e = self.torch.cuda.Event(enable_timing=True)
-            e.record()
-            self.events.append([e, None])
-            self.flops += 2.0 * M * N * K
+            self.launches.setdefault(kind, []).append([e, None, flops])
         else:
-            e = self.torch.cuda.Event(enable_timing=True)
-            e.record()
-            self.events[-1][1] = e
+            self.launches[kind][-1][1] = e
 
-    def total_ms(self):
-        return sum(a.elapsed_time(b) for a, b in self.events)
-
-    def busy_ms(self):
-        spans = sorted((self.base.elapsed_time(a), self.base.elapsed_time(b)) for a, b in self.events)
-        busy, cur0, cur1 = 0.0, None, None
+    def summary(self, kind, steps):
+        rec = self.launches.get(kind, [])
+        if not rec:
+            return None
+        durs = [a.elapsed_time(b) for a, b, _ in rec]
+        flops = sum(f for _, _, f in rec)
+        spans = sorted((self.base.elapsed_time(a), self.base.elapsed_time(b)) for a, b, _ in rec)
+        union, c0, c1 = 0.0, None, None
         for t0, t1 in spans:
-            if cur1 is None or t0 > cur1:
-                if cur1 is not None:
-                    busy += cur1 - cur0
-                cur0, cur1 = t0, t1
+            if c1 is None or t0 > c1:
+                if c1 is not None:
+                    union += c1 - c0
+                c0, c1 = t0, t1
             else:
-                cur1 = max(cur1, t1)
-        if cur1 is not None:
-            busy += cur1 - cur0
-        return busy
+                c1 = max(c1, t1)
+        union += (c1 - c0) if c1 is not None else 0.0
+        n = len(rec)
+        return {
+            "launches_per_step": n / steps,
+            "flops_per_launch": flops / n,
+            "avg_launch_us": 1e3 * sum(durs) / n,
+            "achieved_tflops": flops / (sum(durs) * 1e-3) / 1e12,
+            "launch_sum_ms_per_step": sum(durs) / steps,
+            "busy_union_ms_per_step": union / steps,
+            "achieved_over_busy_union_tflops": flops / (union * 1e-3) / 1e12,
+        }
 
 
-def cpu_baseline(budget_s=20.0):
-    """oracle torch-CPU fp32: one layer fwd+bwd at s=2048, b=1 (+ numpy grad
-    pack/unpack + torch.optim.AdamW over that layer), scaled to 6 layers."""
-    import numpy as np
-    import torch
+def traffic_from_profile():
+    """(HBM bytes per GEMM launch, algorithmic bytes per launch, source) from
+    the committed counter summary, or (None, None, reason)."""
+    try:
+        text = open(TRAFFIC_PROFILE).read()
+    except OSError:
+        return None, None, "no counter summary in profiles/"
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", text)
+    a = re.search(r"algorithmic_bytes_per_launch:\s*([0-9.eE+]+)", text)
+    if not m:
+        return None, None, "counter summary lacks traffic_bytes_per_launch"
+    return float(m.group(1)), float(a.group(1)) if a else None, os.path.relpath(TRAFFIC_PROFILE, ROOT)
 
+
+def cpu_info():
+    model, logical, cores_per_socket, sockets = "unknown", os.cpu_count(), None, None
+    try:
+        import subprocess
+
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            key, _, val = line.partition(":")
+            val = val.strip()
+            if key == "Model name":
+                model = val
+            elif key == "Core(s) per socket":
+                cores_per_socket = int(val)
+            elif key == "Socket(s)":
+                sockets = int(val)
+    except Exception:  # lscpu missing: report what Python knows
+        pass
+    physical = cores_per_socket * sockets if cores_per_socket and sockets else None
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except AttributeError:
+        affinity = logical
+    return {"model": model, "logical_cpus": logical, "physical_cores": physical, "affinity_cpus": affinity}
+
+
+def cpu_baseline(torch):
+    """This build's torch-CPU fp32 restatement (the oracle) of the reference
+    sequence on the host: the whole 6-layer stage forward+backward at the
+    full shape once, then the grad sync (per-segment copy_ pack/unpack,
+    torch._amp_foreach_non_finite_check_and_unscale_, per-tensor
+    pow(2).sum()) and torch.optim.AdamW over the stage's 302 M parameters;
+    plus the grad-sync and AdamW legs alone on a 2-layer slice of the
+    C3/C4 tensor list, reported in GB/s of the same algorithmic bytes as
+    the GPU legs."""
     from oracle import layer as ol
 
-    threads = min(16, os.cpu_count() or 1)
+    info = cpu_info()
+    threads = max(1, min(CPU_THREADS_CAP, info["affinity_cpus"] or 1))
     torch.set_num_threads(threads)
     gen = torch.Generator().manual_seed(0)
-    p = {
-        "ln1_w": torch.ones(H), "ln1_b": torch.zeros(H),
-        "qkv_w": torch.randn(3 * H, H, generator=gen) * 0.02, "qkv_b": torch.zeros(3 * H),
-        "proj_w": torch.randn(H, H, generator=gen) * 0.02, "proj_b": torch.zeros(H),
-        "ln2_w": torch.ones(H), "ln2_b": torch.zeros(H),
-        "fc1_w": torch.randn(FFN, H, generator=gen) * 0.02, "fc1_b": torch.zeros(FFN),
-        "fc2_w": torch.randn(H, FFN, generator=gen) * 0.02, "fc2_b": torch.zeros(H),
-    }
-    s, b = SEQ, 1
-    x = torch.randn(s, b, H, generator=gen)
-    dy = torch.randn(s, b, H, generator=gen) * 1e-3
-    params = [torch.nn.Parameter(v.clone()) for v in p.values()]
-    opt = torch.optim.AdamW(params, lr=1e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1)
-    reps, t0 = 0, time.perf_counter()
-    while reps < 1 or (time.perf_counter() - t0 < budget_s and reps < 3):
-        out, dx, grads = ol.middle_stage_fwd_bwd(x, [p], HEADS, dy)
-        flat = np.concatenate([g.numpy().ravel() for g in grads[0].values()])  # pack
-        payload = flat * np.float32(1.0)
-        off = 0
-        for prm, g in zip(params, grads[0].values()):  # unpack
-            n = g.numel()
-            prm.grad = torch.from_numpy(payload[off : off + n].reshape(g.shape))
-            off += n
-        opt.step()
-        reps += 1
-    per_layer = (time.perf_counter() - t0) / reps
-    tokens_per_s = (s * b) / (per_layer * LAYERS)
-    import platform
 
+    def layer_params():
+        return {
+            "ln1_w": torch.ones(H), "ln1_b": torch.zeros(H),
+            "qkv_w": torch.randn(3 * H, H, generator=gen) * 0.02, "qkv_b": torch.zeros(3 * H),
+            "proj_w": torch.randn(H, H, generator=gen) * 0.02, "proj_b": torch.zeros(H),
+            "ln2_w": torch.ones(H), "ln2_b": torch.zeros(H),
+            "fc1_w": torch.randn(FFN, H, generator=gen) * 0.02, "fc1_b": torch.zeros(FFN),
+            "fc2_w": torch.randn(H, FFN, generator=gen) * 0.02, "fc2_b": torch.zeros(H),
+        }
+
+    layers = [layer_params() for _ in range(LAYERS)]
+    x = torch.randn(SEQ, MB, H, generator=gen)
+    dy = torch.randn(SEQ, MB, H, generator=gen) * 1e-3
+    params = [torch.nn.Parameter(v.clone()) for lp in layers for v in lp.values()]
+    opt = torch.optim.AdamW(params, lr=1e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1)
+
+    def grad_sync(grads, scratch):
+        """executor.py:199-261 + optimizer.py:436-461 + the canonical norm."""
+        off = 0
+        for g in grads:  # pack: one copy_ per segment
+            n = g.numel()
+            scratch[off : off + n].copy_(g.reshape(-1))
+            off += n
+        off = 0
+        for g in grads:  # unpack
+            n = g.numel()
+            g.reshape(-1).copy_(scratch[off : off + n])
+            off += n
+        found = torch.zeros(1)
+        torch._amp_foreach_non_finite_check_and_unscale_(grads, found, torch.full((1,), 2.0**-16))
+        return math.sqrt(sum(float(g.pow(2).sum()) for g in grads))
+
+    t0 = time.perf_counter()
+    _, _, grads = ol.middle_stage_fwd_bwd(x, layers, HEADS, dy)
+    t_fwd_bwd = time.perf_counter() - t0
+    flat_grads = [g for gl in grads for g in gl.values()]
+    scratch = torch.empty(sum(g.numel() for g in flat_grads))
+    t1 = time.perf_counter()
+    grad_sync(flat_grads, scratch)
+    for p, g in zip(params, flat_grads):
+        p.grad = g
+    opt.step()
+    t_tail = time.perf_counter() - t1
+    step_s = t_fwd_bwd + t_tail
+    del grads, flat_grads, scratch, opt, params
+
+    # C3 / C4 legs alone on the first 2 of the 24 layers of the tensor list
+    from eth_amd.grad_sync.synthetic import gpt_layer_shapes
+
+    shapes = gpt_layer_shapes(H, FFN, 2)
+    n_elem = sum(math.prod(s[1]) for s in shapes)
+    gs = [torch.randn(s[1], generator=gen) * 1e-3 for s in shapes]
+    scratch = torch.empty(n_elem)
+    t2 = time.perf_counter()
+    grad_sync(gs, scratch)
+    t_sync = time.perf_counter() - t2
+    adam = {}
+    for label, kw in (("foreach_false", {"foreach": False}), ("default", {})):
+        ps = [torch.nn.Parameter(torch.randn(s[1], generator=gen) * 0.02) for s in shapes]
+        o = torch.optim.AdamW(ps, lr=1e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, **kw)
+        for p, g in zip(ps, gs):
+            p.grad = g
+        o.step()  # state allocation outside the timing
+        t3 = time.perf_counter()
+        o.step()
+        adam[label] = time.perf_counter() - t3
+        del o, ps
     return {
-        "value": tokens_per_s,
+        "value": (SEQ * MB) / step_s,
         "unit": "tokens/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"1 layer fwd+bwd fp32 torch-CPU at s={s} b={b} + grad pack/unpack + AdamW, {reps} reps, "
-                  f"{per_layer:.2f} s/layer, scaled to {LAYERS} layers ({platform.processor() or 'cpu'})",
+        "sample": (
+            f"one full step of the 6-layer stage in fp32 torch-CPU (oracle restatement): fwd+bwd at s {SEQ} b {MB} "
+            f"{t_fwd_bwd:.2f} s, grad sync + unscale + L2 + AdamW over 302M params {t_tail:.2f} s; "
+            f"{threads} threads (the box's CPU share per GPU) on {info['model']}"
+        ),
+        "cpu": info,
+        "grad_sync_gbps": 16.0 * n_elem / t_sync / 1e9,
+        "adamw_gbps": {k: 30.0 * n_elem / v / 1e9 for k, v in adam.items()},
+        "hbm_leg_sample": f"2 of the 24 layers of the C3/C4 tensor list ({n_elem} fp32 elements); GB/s of 16 B "
+                          "(grad sync) and 30 B (AdamW) per element",
     }
 
 
-def hbm_path(torch, iters=5):
+def hbm_path(torch, iters=10):
     """Grad pack+unscale+flag+L2+unpack and AdamW over the 24-layer
-    GPT-1.3B grad list ([3])."""
+    GPT-1.3B grad list ([3]), HIP-event timed."""
     from eth_amd.grad_sync import bucket_plan as bp
-    from eth_amd.grad_sync.executor import GradientBucketExecutor, GradientStatistics
-    from eth_amd.grad_sync.planner import plan_canonical_fragments
     from eth_amd.grad_sync.bucket_plan import ProcessGroupRegistry
+    from eth_amd.grad_sync.executor import GradientBucketExecutor, GradientStatistics
     from eth_amd.grad_sync.metadata import LocalGradientBinding
+    from eth_amd.grad_sync.planner import plan_canonical_fragments
     from eth_amd.grad_sync.synthetic import descriptors_for, gpt_layer_shapes
     from eth_amd.optimizer.fused_adam import FusedAdamW
 
@@ -174,7 +279,8 @@ def hbm_path(torch, iters=5):
     plan = bp.build_gradient_sync_plan(plan_canonical_fragments(descs, (0,)), "block", 32 << 20, "gpt", "m", "t")
     total = sum(math.prod(s[1]) for s in shapes)
     buf = torch.empty(total, dtype=torch.float32, device=dev)
-    buf.normal_(0, 1e-3)
+    g = torch.Generator(device=dev).manual_seed(1234)
+    buf.normal_(0, 1e-3, generator=g)
     grads, off = {}, total
     for lid, shape, *_ in shapes:
         n = math.prod(shape)
@@ -186,34 +292,59 @@ def hbm_path(torch, iters=5):
     ex = GradientBucketExecutor(plan, 0, descs, bindings, registry, lambda p, h: None)
     st = GradientStatistics(ex.n_partials, dev)
     ex.bind_statistics(st)
-    ex.set_inv_loss_scale(1.0)
+    ex.set_inv_loss_scale(2.0**-16)
 
-    def timed(fn):
+    def timed(fn, prepare=None):
+        """Mean of `iters` event-timed calls; `prepare` runs before each
+        call, outside the events."""
         fn()
-        torch.cuda.synchronize()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
+        total_ms = 0.0
         for _ in range(iters):
+            if prepare is not None:
+                prepare()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
             fn()
-        b.record()
-        torch.cuda.synchronize()
-        return a.elapsed_time(b) / iters
+            b.record()
+            b.synchronize()
+            total_ms += a.elapsed_time(b)
+        return total_ms / iters
 
-    t_sync = timed(lambda: (ex.execute(1.0), st.finalize(1.0)))
-    params = [torch.nn.Parameter(torch.empty(s[1], device=dev).normal_(0, 0.02)) for s in shapes]
+    sync = lambda: (ex.execute(1.0), st.finalize(1.0))  # noqa: E731
+    # the unpack writes the unscaled gradients back; scaling them up again
+    # by 2^16 (exact) outside the timing keeps every call on the same data
+    rescale = lambda: buf.mul_(2.0**16)  # noqa: E731
+    t_sync = timed(sync, rescale)
+    found_clean = float(st.found_inf.item())
+    # 0.1 % of the elements +inf (a seeded index set), the C3 overflow variant
+    idx = torch.randint(0, total, (total // 1000,), generator=g, device=dev)
+    buf[idx] = float("inf")
+    del idx
+    t_sync_inf = timed(sync, rescale)
+    found_inf = float(st.found_inf.item())
+    buf.normal_(0, 1e-3, generator=g)
+    params = [torch.nn.Parameter(torch.empty(s[1], device=dev).normal_(0, 0.02, generator=g)) for s in shapes]
     model = [torch.empty(s[1], device=dev, dtype=torch.bfloat16) for s in shapes]
     for p, (lid, *_) in zip(params, shapes):
         p.grad = grads[lid]
     opt = FusedAdamW([{"params": params}], lr=1e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1)
     opt.set_model_copies(dict(zip(params, model)), torch.bfloat16)
+    ex.set_inv_loss_scale(1.0)
+    sync()
     t_adam = timed(lambda: opt.step(stats=st.stats))
     out = {
         "elements": total,
+        "inv_loss_scale": 2.0**-16,
         "grad_sync_ms": t_sync,
         "grad_sync_gbps": 16.0 * total / t_sync / 1e6,
+        "grad_sync_found_inf": found_clean,
+        "grad_sync_inf_variant_ms": t_sync_inf,
+        "grad_sync_inf_variant_gbps": 16.0 * total / t_sync_inf / 1e6,
+        "grad_sync_inf_variant_found_inf": found_inf,
         "adam_ms": t_adam,
         "adam_gbps": 30.0 * total / t_adam / 1e6,
         "peak_gbps": PEAK_HBM_GBPS,
+        "bytes_per_element": {"grad_sync": 16, "adam": 30},
     }
     out["grad_sync_frac"] = out["grad_sync_gbps"] / PEAK_HBM_GBPS
     out["adam_frac"] = out["adam_gbps"] / PEAK_HBM_GBPS
@@ -271,9 +402,13 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--meter-steps", type=int, default=3,
+                    help="extra steps with HIP events around every GEMM / attention launch (roofline)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-hbm-path", action="store_true")
     ap.add_argument("--no-first-last", action="store_true")
+    ap.add_argument("--first-last-only", action="store_true",
+                    help="time only the configs[4] first+last stage (for its kernel profile)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="after the timed steps, copy 1 GiB once (the calibration kernel of the "
                          "FETCH_SIZE / WRITE_SIZE counter runs behind roofline.traffic)")
@@ -289,6 +424,11 @@ def main():
     from eth_amd.model.flex_ops import GPTConfig
     from eth_amd.stage import MiddleStageTrainer
 
+    if args.first_last_only:
+        fl = first_last_stage(torch, steps=args.steps, warmup=args.warmup)
+        print(json.dumps({"first_last_stage": fl}), flush=True)
+        return
+
     cfg = GPTConfig(hidden_size=H, num_attention_heads=HEADS, ffn_hidden_size=FFN, num_layers=LAYERS,
                     seq_length=SEQ, micro_batch_size=MB, params_dtype=torch.bfloat16, device="cuda", seed=1234)
     tr = MiddleStageTrainer(cfg, lr=1e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, clip_grad=1.0)
@@ -300,21 +440,32 @@ def main():
     torch.cuda.synchronize()
     quiet_gc()
 
-    meter = GemmMeter(torch)
-    K.set_gemm_observer(meter)
+    # timed steps: no instrumentation besides one event pair per step
+    marks = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    marks[0].record()
+    for i in range(args.steps):
         out, dx, ok, norm = tr.train_step(x, dy)
+        marks[i + 1].record()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    K.set_gemm_observer(None)
+    step_ms = [marks[i].elapsed_time(marks[i + 1]) for i in range(args.steps)]
     ms = 1e3 * elapsed / args.steps
     tokens = SEQ * MB
     value = tokens * args.steps / elapsed
-    gemm_ms = meter.busy_ms()
-    gemm_sum_ms = meter.total_ms()
-    gemm_tflops = meter.flops / (gemm_ms * 1e-3) / 1e12 if gemm_ms > 0 else 0.0
     step_tflops = step_flops() / (ms * 1e-3) / 1e12
+
+    # instrumented steps for the kernel rooflines
+    meter = KernelMeter(torch)
+    K.set_kernel_observer(meter)
+    for _ in range(args.meter_steps):
+        tr.train_step(x, dy)
+    torch.cuda.synchronize()
+    K.set_kernel_observer(None)
+    gemm = meter.summary("gemm", args.meter_steps)
+    attn_f = meter.summary("attn_fwd", args.meter_steps)
+    attn_b = meter.summary("attn_bwd", args.meter_steps)
+    traffic, algo_bytes, traffic_src = traffic_from_profile()
 
     result = {
         "metric": "stage train tokens/s (GPT-1.3B, 6 layers) on 1 GPU; grad-pack+Adam HBM GB/s",
@@ -324,6 +475,8 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": ms,
+        "step_ms_median": percentile(step_ms, 0.5),
+        "step_ms_p90": percentile(step_ms, 0.9),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -340,21 +493,29 @@ def main():
         "step_mfma_frac": step_tflops / PEAK_BF16_TFLOPS,
         "grad_norm": norm,
         "roofline": {
-            "kernel": "eth_gemm (gemm256_m16_kernel, gemm256_m32_kernel and gemm_kernel: all GEMM launches of the timed steps)",
+            "kernel": "eth_gemm (gemm256_m16/m32 and gemm_kernel instantiations: every GEMM launch of a step)",
             "bound": "mfma",
-            "achieved": gemm_tflops,
+            "achieved": gemm["achieved_tflops"],
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
-            "frac": gemm_tflops / PEAK_BF16_TFLOPS,
-            "traffic": GEMM_TRAFFIC_BYTES_PER_LAUNCH,
-            "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)",
-            "algorithmic_bytes_per_launch": GEMM_ALGORITHMIC_BYTES_PER_LAUNCH,
-            "launches": len(meter.events),
-            "gemm_ms_per_step": gemm_ms / args.steps,
-            "time_basis": "union of the GEMM launch intervals (weight-gradient GEMMs run on a side stream, "
-                          "overlapped with the data-gradient chain)",
-            "launch_sum_ms_per_step": gemm_sum_ms / args.steps,
-            "achieved_over_launch_sum": meter.flops / (gemm_sum_ms * 1e-3) / 1e12 if gemm_sum_ms > 0 else 0.0,
+            "frac": gemm["achieved_tflops"] / PEAK_BF16_TFLOPS,
+            "traffic": traffic,
+            "traffic_unit": "HBM bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)",
+            "traffic_source": traffic_src,
+            "algorithmic_bytes_per_launch": algo_bytes,
+            "basis": "algorithmic FLOPs per launch / average launch duration (HIP events on the launch stream, "
+                     f"{args.meter_steps} instrumented steps)",
+            **{k: gemm[k] for k in ("launches_per_step", "flops_per_launch", "avg_launch_us",
+                                    "launch_sum_ms_per_step", "busy_union_ms_per_step",
+                                    "achieved_over_busy_union_tflops")},
+        },
+        "attention": {
+            "bound": "mfma",
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "flops_basis": "fwd 2*b*s^2*h (causal half of QK^T and PV); bwd 2.5x fwd (recomputed S, dP, dV, dQ, dK)",
+            "fwd": {**attn_f, "frac": attn_f["achieved_tflops"] / PEAK_BF16_TFLOPS} if attn_f else None,
+            "bwd": {**attn_b, "frac": attn_b["achieved_tflops"] / PEAK_BF16_TFLOPS} if attn_b else None,
         },
     }
     del tr, out, dx
@@ -371,7 +532,7 @@ def main():
     if not args.no_first_last:
         result["first_last_stage"] = first_last_stage(torch)
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline()
+        result["cpu_baseline"] = cpu_baseline(torch)
     print(json.dumps(result), flush=True)
 
 

@@ -71,7 +71,7 @@ SIGNATURES = {
     "eth_reduce_partials": [_P, _I64, _I64, _I64, _P, _I32, _P],
 }
 SIGNATURES["eth_embedding_fwd"] = [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _I32, _P]
-SIGNATURES["eth_embedding_bwd"] = [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I32, _P]
+SIGNATURES["eth_embedding_bwd"] = [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I32, _P]
 SIGNATURES["eth_xent_fwd"] = [_P, _I64, _P, _P, _P, _I64, _I64, _P, _I32, _P]
 SIGNATURES["eth_xent_bwd"] = [_P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _I32, _P]
 SIGNATURES["eth_tied_grad_sum"] = [_P, _P, _I64, _P]
@@ -106,6 +106,7 @@ VALUE_SIGNATURES = {
     "eth_bias_gelu_bwd_workspace": ([_I64, _I64], _I64),
     "eth_col_sum_workspace": ([_I64, _I64], _I64),
     "eth_gemm_splitk_workspace": ([_I64, _I64, _I32], _I64),
+    "eth_embedding_bwd_workspace": ([_I64, _I64], _I64),
 }
 GEMM_ACCUMULATE, GEMM_BIAS = 1, 2
 

@@ -4,9 +4,10 @@
 //                   one rounding, written directly in the [s, b, h] layout the
 //                   reference gets from .transpose(0, 1).contiguous())
 //                   (Embedding_v1.forward, eth/runtime/megatron/model/flex_ops.py:450-485)
-//   embedding bwd   dword[tok] += dout, dpos[pid] += dout in fp32 main grads
-//                   (atomic adds; F.embedding's backward)
-//   cross entropy   loss = logsumexp(z) - z[label] per row in fp32 from the
+//   embedding bwd   dword[tok] += dout, dpos[pid] += dout in fp32 main grads,
+//                   deterministic (sort + one owner per row; F.embedding's
+//                   backward, which is a sort + segmented reduction too)
+//   cross entropy   loss = log sum exp(z - max) - (z[label] - max) per row in fp32 from the
 //                   16-bit logits (the `.float()` of flex_ops.py:1976-1981 is
 //                   folded into the read); backward
 //                   dz = (exp(z - lse) - onehot(label)) * dloss, written 16-bit
@@ -62,30 +63,95 @@ __global__ void __launch_bounds__(256) embedding_fwd_kernel(const int64_t* __res
   }
 }
 
-template <bool FP16>
-__global__ void __launch_bounds__(256) embedding_bwd_kernel(const int64_t* __restrict__ tok,
-                                                            const int64_t* __restrict__ pid,
-                                                            const uint16_t* __restrict__ dout,
-                                                            float* __restrict__ dword, float* __restrict__ dpos,
-                                                            int B, int S, int H, int64_t V, int64_t P) {
-  const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= (int64_t)S * B) return;
-  const int si = (int)(row / B), bi = (int)(row % B);
-  int64_t t = tok[(int64_t)bi * S + si], p = pid[(int64_t)bi * S + si];
-  t = t < 0 ? 0 : (t >= V ? V - 1 : t);
-  p = p < 0 ? 0 : (p >= P ? P - 1 : p);
-  const uint16_t* g = dout + row * H;
-  for (int c = lane * 8; c < H; c += 512) {
-    uint4 a = *reinterpret_cast<const uint4*>(g + c);
-    const uint16_t* ae = reinterpret_cast<const uint16_t*>(&a);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float v = vin<FP16>(ae[j]);
-      if (dword) atomicAdd(dword + t * H + c + j, v);
-      if (dpos) atomicAdd(dpos + p * H + c + j, v);
+// ---------------------------------------------------------------------------
+// Deterministic embedding backward: sort, then one owner per table row.
+//
+// For each table (word ids, position ids) a single workgroup sorts the keys
+//   key = (clamped id << row_bits) | dout row        (row = s * B + b)
+// in LDS with a bitonic network, so equal ids become one contiguous run
+// ordered by dout row.  The accumulate kernel then gives every run to the
+// workgroup of its first sorted slot, which sums the run's dout rows in fp32
+// in that order and adds the sum into the fp32 main grad once: no atomics,
+// and the same bits on every run.  The keys fit 32 bits when
+// bits(V - 1) + bits(T - 1) <= 32; T <= kEmbSortMax keeps the LDS image at
+// 128 KB (static; gfx950 gives a workgroup up to 160 KB).
+constexpr int kEmbSortThreads = 1024;
+constexpr int kEmbSortMax = 32768;
+
+__device__ __forceinline__ int64_t clamp_id(int64_t v, int64_t n) { return v < 0 ? 0 : (v >= n ? n - 1 : v); }
+
+// blockIdx.x = 0 sorts the token ids into keys[0, T), 1 the position ids
+// into keys[T, 2T)
+__global__ void __launch_bounds__(kEmbSortThreads) embedding_sort_kernel(const int64_t* __restrict__ tok,
+                                                                        const int64_t* __restrict__ pid,
+                                                                        uint32_t* __restrict__ keys, int B, int S,
+                                                                        int64_t V, int64_t P, int row_bits, int n2) {
+  __shared__ uint32_t sk[kEmbSortMax];
+  const int T = B * S;
+  const int64_t* ids = blockIdx.x == 0 ? tok : pid;
+  const int64_t lim = blockIdx.x == 0 ? V : P;
+  for (int i = threadIdx.x; i < n2; i += kEmbSortThreads) {
+    uint32_t k = 0xFFFFFFFFu;
+    if (i < T) {
+      const int si = i / B, bi = i - si * B;  // dout row i holds (s, b)
+      k = ((uint32_t)clamp_id(ids[(int64_t)bi * S + si], lim) << row_bits) | (uint32_t)i;
+    }
+    sk[i] = k;
+  }
+  __syncthreads();
+  for (int k = 2; k <= n2; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int i = threadIdx.x; i < (n2 >> 1); i += kEmbSortThreads) {
+        const int lo = 2 * j * (i / j) + (i % j), hi = lo + j;
+        const uint32_t a = sk[lo], b = sk[hi];
+        if ((a > b) == ((lo & k) == 0)) {
+          sk[lo] = b;
+          sk[hi] = a;
+        }
+      }
+      __syncthreads();
     }
   }
+  uint32_t* out = keys + (int64_t)blockIdx.x * T;
+  for (int i = threadIdx.x; i < T; i += kEmbSortThreads) out[i] = sk[i];
+}
+
+// grid (T, column chunks of 2048, tables): the workgroup at the first
+// sorted slot of a run owns that table row
+template <bool FP16>
+__global__ void __launch_bounds__(256) embedding_accum_kernel(const uint32_t* __restrict__ keys,
+                                                              const uint16_t* __restrict__ dout,
+                                                              float* __restrict__ dword, float* __restrict__ dpos,
+                                                              int T, int H, int row_bits) {
+  const uint32_t* ks = keys + (int64_t)blockIdx.z * T;
+  float* dst = blockIdx.z == 0 ? dword : dpos;
+  const int j = blockIdx.x;
+  const uint32_t id = ks[j] >> row_bits;
+  if (dst == nullptr || (j > 0 && (ks[j - 1] >> row_bits) == id)) return;
+  const int c = blockIdx.y * 2048 + threadIdx.x * 8;
+  if (c >= H) return;
+  const uint32_t mask = (1u << row_bits) - 1u;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  int end = j + 1;
+  while (end < T && (ks[end] >> row_bits) == id) ++end;
+  for (int r = j; r < end; ++r) {
+    const uint4 a = *reinterpret_cast<const uint4*>(dout + (int64_t)(ks[r] & mask) * H + c);
+    const uint16_t* e = reinterpret_cast<const uint16_t*>(&a);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) acc[q] += vin<FP16>(e[q]);
+  }
+  float4* d = reinterpret_cast<float4*>(dst + (int64_t)id * H + c);
+  float4 x0 = d[0], x1 = d[1];
+  x0.x += acc[0]; x0.y += acc[1]; x0.z += acc[2]; x0.w += acc[3];
+  x1.x += acc[4]; x1.y += acc[5]; x1.z += acc[6]; x1.w += acc[7];
+  d[0] = x0;
+  d[1] = x1;
+}
+
+static int bits_for(int64_t n) {  // bits to hold values 0 .. n-1
+  int b = 0;
+  while (b < 63 && (1LL << b) < n) ++b;
+  return b;
 }
 
 constexpr int kXentThreads = 256;
@@ -142,14 +208,16 @@ __global__ void __launch_bounds__(kXentThreads) xent_fwd_kernel(const uint16_t* 
       Ssum = Ssum * __expf(M - mx) + ss[k] * __expf(sm[k] - mx);
       M = mx;
     }
-    const float l = M + __logf(Ssum);
+    const float log_s = __logf(Ssum);
     int64_t t = labels[row];
     if (t < 0 || t >= V) {
       *bad = 1;
       t = t < 0 ? 0 : V - 1;
     }
-    lse[row] = l;
-    loss[row] = l - vin<FP16>(z[t]);
+    lse[row] = M + log_s;
+    // the reference's order: log(sum exp(z - max)) - (z[t] - max), so the
+    // row maximum never enters the sum with the target logit
+    loss[row] = log_s - (vin<FP16>(z[t]) - M);
   }
 }
 
@@ -241,21 +309,40 @@ extern "C" int eth_embedding_fwd(const int64_t* tokens, const int64_t* positions
   return ETH_OK;
 }
 
+extern "C" int64_t eth_embedding_bwd_workspace(int64_t batch, int64_t seq) {
+  return batch > 0 && seq > 0 ? 2 * batch * seq * (int64_t)sizeof(uint32_t) : 0;
+}
+
 extern "C" int eth_embedding_bwd(const int64_t* tokens, const int64_t* positions, const void* dout,
-                                 float* dword, float* dpos, int64_t batch, int64_t seq, int64_t hidden,
-                                 int64_t vocab, int64_t max_pos, int dtype, void* stream) {
+                                 float* dword, float* dpos, void* workspace, int64_t batch, int64_t seq,
+                                 int64_t hidden, int64_t vocab, int64_t max_pos, int dtype, void* stream) {
   ETH_CHECK_ARG(dtype == ETH_BF16 || dtype == ETH_F16, "eth_embedding_bwd: dtype must be bf16/fp16");
-  ETH_CHECK_ARG(batch > 0 && seq > 0 && hidden > 0 && hidden % 8 == 0, "eth_embedding_bwd: bad shape");
-  ETH_CHECK_ARG(tokens && positions && dout && (dword || dpos), "eth_embedding_bwd: null pointer");
-  const int64_t rows = batch * seq;
-  const int grid = (int)((rows + 3) / 4);
+  ETH_CHECK_ARG(batch > 0 && seq > 0 && hidden > 0 && hidden % 8 == 0 && vocab > 0 && max_pos > 0,
+                "eth_embedding_bwd: bad shape");
+  ETH_CHECK_ARG(tokens && positions && dout && workspace && (dword || dpos), "eth_embedding_bwd: null pointer");
+  const int64_t T = batch * seq;
+  ETH_CHECK_ARG(T <= kEmbSortMax, "eth_embedding_bwd: at most %d tokens per call (got %lld)", kEmbSortMax,
+                (long long)T);
+  const int row_bits = bits_for(T);
+  ETH_CHECK_ARG(row_bits + bits_for(vocab) <= 32 && row_bits + bits_for(max_pos) <= 32,
+                "eth_embedding_bwd: ids and rows do not fit a 32-bit sort key");
+  ETH_CHECK_ARG(((uintptr_t)dword & 15) == 0 && ((uintptr_t)dpos & 15) == 0 && ((uintptr_t)workspace & 3) == 0,
+                "eth_embedding_bwd: gradient tables must be 16-byte aligned");
+  int n2 = 1;
+  while (n2 < T) n2 <<= 1;
+  if (n2 < 2) n2 = 2;
   hipStream_t s = (hipStream_t)stream;
+  uint32_t* keys = (uint32_t*)workspace;
+  embedding_sort_kernel<<<2, kEmbSortThreads, 0, s>>>(tokens, positions, keys, (int)batch, (int)seq, vocab,
+                                                        max_pos, row_bits, n2);
+  ETH_CHECK_LAUNCH("eth_embedding_bwd (sort)");
+  dim3 grid((unsigned)T, (unsigned)((hidden + 2047) / 2048), 2);
   if (dtype == ETH_BF16)
-    embedding_bwd_kernel<false><<<grid, 256, 0, s>>>(tokens, positions, (const uint16_t*)dout, dword, dpos,
-                                                     (int)batch, (int)seq, (int)hidden, vocab, max_pos);
+    embedding_accum_kernel<false><<<grid, 256, 0, s>>>(keys, (const uint16_t*)dout, dword, dpos, (int)T,
+                                                       (int)hidden, row_bits);
   else
-    embedding_bwd_kernel<true><<<grid, 256, 0, s>>>(tokens, positions, (const uint16_t*)dout, dword, dpos,
-                                                    (int)batch, (int)seq, (int)hidden, vocab, max_pos);
+    embedding_accum_kernel<true><<<grid, 256, 0, s>>>(keys, (const uint16_t*)dout, dword, dpos, (int)T,
+                                                      (int)hidden, row_bits);
   ETH_CHECK_LAUNCH("eth_embedding_bwd");
   return ETH_OK;
 }

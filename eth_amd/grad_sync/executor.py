@@ -1,9 +1,11 @@
 """Execution of an immutable gradient synchronization plan on the GPU.
 
 Drop-in for eth/runtime/megatron/grad_sync/executor.py:24-261
-(GradientBucketExecutor): same constructor, `execute(normalization_scale)`,
-`scratch(dtype)`, `scratch_dtypes`, same validation errors carrying
-`bucket {id} rank {r} logical_param_id {id} fragment {id}` context.
+(GradientBucketExecutor): same constructor (including the opt-in
+`runtime_evidence_dir`, grad_sync/runtime_evidence.py), `execute(
+normalization_scale)`, `scratch(dtype)`, `scratch_dtypes`, same validation
+errors carrying `bucket {id} rank {r} logical_param_id {id} fragment {id}`
+context.
 
 What differs is how a bucket is moved.  Instead of one `copy_` per segment
 plus a `mul_` per bucket, every segment of every bucket is resolved once, at
@@ -22,6 +24,7 @@ import numpy as np
 import torch
 
 from .. import _native as nat
+from .runtime_evidence import GradientRuntimeEvidenceRecorder
 
 
 def _dtype_name(dtype):
@@ -124,14 +127,19 @@ class GradientBucketExecutor:
             if rank == global_rank
             for b in bindings
         }
-        if runtime_evidence_dir:
-            raise ValueError("runtime evidence recording is not supported by the eth_amd executor")
         self._validate_local_contract()
         self._scratch = self._allocate_scratch()
         self._tables = self._build_tables()
         self._statistics = None
         self._inv_scale = 1.0
         self._pass = None
+        # opt-in record of every packed payload (executor.py:59-67,248-260)
+        self._evidence = (
+            GradientRuntimeEvidenceRecorder(plan, global_rank, process_group_registry, self._scratch,
+                                            runtime_evidence_dir)
+            if runtime_evidence_dir
+            else None
+        )
 
     # ------------------------------------------------------------ contract --
     @staticmethod
@@ -321,6 +329,9 @@ class GradientBucketExecutor:
         if normalization_scale != 1.0:
             flags |= nat.UNPACK_WRITEBACK
         self._pass = (float(normalization_scale), flags)
+        self._next_bucket = 0
+        if self._evidence is not None:
+            self._evidence.begin_execution(normalization_scale)
 
     def run_bucket(self, i):
         """pack -> all_reduce_sum seam -> fused unpack of bucket i
@@ -331,8 +342,15 @@ class GradientBucketExecutor:
         bucket, table, n_chunks, base = self._tables[i]
         payload = self._scratch[bucket.grad_dtype][: bucket.exact_numel]
         dcode = nat.dtype_code(payload.dtype)
+        if self._evidence is not None:
+            # the evidence hashes the plan's buckets in plan order, each once
+            if i != self._next_bucket:
+                raise ValueError("runtime evidence records buckets in plan order; the streamed sync reorders them")
+            self._next_bucket += 1
         if n_chunks:
             nat.call("eth_bucket_pack", nat.ptr(table), n_chunks, nat.ptr(payload), dcode, stream)
+        if self._evidence is not None:
+            self._evidence.observe_packed_bucket(bucket, payload)
         self._all_reduce_sum(payload, self._registry.handle(bucket.process_group_id))
         if n_chunks:
             f = flags if (dcode == nat.ETH_F32 or not (flags & nat.UNPACK_UNSCALE)) else flags & ~nat.UNPACK_UNSCALE
@@ -357,6 +375,8 @@ class GradientBucketExecutor:
             stats.fresh = True
             stats.inv_scale_used = self._inv_scale
         self._pass = None
+        if self._evidence is not None:
+            self._evidence.finish_execution()
 
     def execute(self, normalization_scale=1.0):
         self.begin(normalization_scale)

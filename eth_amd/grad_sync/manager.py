@@ -42,6 +42,7 @@ def initialize_gradient_sync(
     all_gather_object=_single_rank_all_gather,
     create_group=lambda ranks: ranks,
     all_reduce_sum=lambda payload, handle: None,
+    runtime_evidence_dir=None,
 ):
     """Plan, verify and bind gradient synchronization for this rank."""
     gathered = all_gather_object(tuple(descriptors))
@@ -54,6 +55,7 @@ def initialize_gradient_sync(
     registry = ProcessGroupRegistry(plan.process_groups, create_group)
     registry.initialize()
     executor = GradientBucketExecutor(
-        plan, global_rank, tuple(d for d in descriptors), tuple(bindings), registry, all_reduce_sum
+        plan, global_rank, tuple(descriptors), tuple(bindings), registry, all_reduce_sum,
+        runtime_evidence_dir=runtime_evidence_dir,
     )
     return GradientSyncManager(plan, executor, registry)

@@ -48,15 +48,23 @@ def _matrix_layout(t):
     raise ValueError(f"operand with strides {t.stride()} is neither row- nor column-major")
 
 
-_gemm_observer = None
+_observer = None
 
 
-def set_gemm_observer(fn):
-    """fn(phase, M, N, K) is called right before ("begin") and after ("end")
-    every GEMM launch (used by the benchmark to time the GEMMs with events on
-    the launch stream); None disables it."""
-    global _gemm_observer
-    _gemm_observer = fn
+def set_kernel_observer(fn):
+    """fn(kind, phase, flops) is called right before ("begin") and after
+    ("end") every GEMM ("gemm") and attention ("attn_fwd", "attn_bwd")
+    launch, on the thread that launches it, with the launch's algorithmic
+    FLOPs (the benchmark records HIP events on the launch stream with it);
+    None disables it."""
+    global _observer
+    _observer = fn
+
+
+def _observe(kind, phase, flops):
+    obs = _observer
+    if obs is not None:
+        obs(kind, phase, flops)
 
 
 def _splitk_splits(M, N, K, out):
@@ -133,9 +141,7 @@ def gemm(a, b, out=None, bias=None, accumulate=False, out_dtype=None, alpha=1.0)
         if bias.dtype != a.dtype or bias.numel() != N or not bias.is_contiguous():
             raise ValueError("bias must be a contiguous [N] tensor of the input dtype")
         flags |= nat.GEMM_BIAS
-    obs = _gemm_observer
-    if obs is not None:
-        obs("begin", M, N, K)
+    _observe("gemm", "begin", 2.0 * M * N * K)
     fp32_product = out.dtype == torch.float32 and alpha == 1.0 and bias is None
     splits = _splitk_splits(M, N, K, out) if fp32_product else 1
     if splits > 1:
@@ -147,8 +153,7 @@ def gemm(a, b, out=None, bias=None, accumulate=False, out_dtype=None, alpha=1.0)
             nat.ptr(out), out.stride(0), M, N, K, code, splits, 1 if accumulate else 0, nat.ptr(ws),
             nat.stream_ptr(a.device),
         )
-        if obs is not None:
-            obs("end", M, N, K)
+        _observe("gemm", "end", 2.0 * M * N * K)
         return out
     nat.call(
         "eth_gemm",
@@ -158,8 +163,7 @@ def gemm(a, b, out=None, bias=None, accumulate=False, out_dtype=None, alpha=1.0)
         nat.ptr(bias), M, N, K, code, flags, float(alpha),
         nat.stream_ptr(a.device),
     )
-    if obs is not None:
-        obs("end", M, N, K)
+    _observe("gemm", "end", 2.0 * M * N * K)
     return out
 
 
@@ -322,8 +326,11 @@ def attention_fwd(q, k, v, out=None):
     desc.k_strides[:] = _sbhd_strides(k)
     desc.v_strides[:] = _sbhd_strides(v)
     desc.o_strides[:] = _sbhd_strides(o4)
+    flops = 2.0 * b * n * s * s * d  # QK^T and PV over the causal half
+    _observe("attn_fwd", "begin", flops)
     nat.call("eth_attn_fwd", ctypes.byref(desc), nat.ptr(q), nat.ptr(k), nat.ptr(v), nat.ptr(o4), nat.ptr(lse),
              nat.stream_ptr(q.device))
+    _observe("attn_fwd", "end", flops)
     return out, lse
 
 
@@ -344,8 +351,11 @@ def attention_bwd(q, k, v, out, dout, lse, dq, dk, dv):
         if t.shape != q.shape:
             raise ValueError(f"{name} shape mismatch")
         getattr(desc, f"{name}_strides")[:] = _sbhd_strides(t)
+    flops = 2.5 * 2.0 * b * n * s * s * d  # dS = dP, dQ, dK, dV: 2.5x the forward's products
+    _observe("attn_bwd", "begin", flops)
     nat.call("eth_attn_bwd", ctypes.byref(desc), nat.ptr(q), nat.ptr(k), nat.ptr(v), nat.ptr(o4), nat.ptr(do4),
              nat.ptr(lse), nat.ptr(delta), nat.ptr(dq), nat.ptr(dk), nat.ptr(dv), nat.stream_ptr(q.device))
+    _observe("attn_bwd", "end", flops)
 
 
 # --------------------------------------------------------------- vocabulary --
@@ -373,7 +383,8 @@ def embedding_fwd(tokens, positions, word, pos, bad_flag):
 
 
 def embedding_bwd(tokens, positions, dout, dword, dpos):
-    """fp32 dword[tokens] += dout and dpos[positions] += dout (dout [s, b, h])."""
+    """fp32 dword[tokens] += dout and dpos[positions] += dout (dout [s, b, h]),
+    bitwise deterministic (sorted ids, one owner per table row)."""
     code = _check_half(dout)
     b, s = tokens.shape
     _check_ids(tokens)
@@ -386,8 +397,9 @@ def embedding_bwd(tokens, positions, dout, dword, dpos):
             raise ValueError("embedding gradients must be contiguous fp32 [rows, hidden]")
     V = dword.shape[0] if dword is not None else 1
     P = dpos.shape[0] if dpos is not None else 1
+    ws = _scratch_f32(-(-nat.value("eth_embedding_bwd_workspace", b, s) // 4), dout.device)
     nat.call("eth_embedding_bwd", nat.ptr(tokens), nat.ptr(positions), nat.ptr(dout), nat.ptr(dword), nat.ptr(dpos),
-             b, s, h, V, P, code, nat.stream_ptr(dout.device))
+             nat.ptr(ws), b, s, h, V, P, code, nat.stream_ptr(dout.device))
 
 
 def xent_fwd(logits2d, labels, bad_flag):

@@ -49,6 +49,10 @@ class Embedding_v1(RopalaModule):
         self.embedding_dropout = cfg.hidden_dropout
         self.shared_weights_info = {"word_embeddings": {"root": True, "sharing_with_ops": [10 * cfg.num_layers + 2]}}
         self._bad = torch.zeros(1, dtype=torch.int32, device=cfg.device)
+        # dropout stream: a fresh mask per call, replayed by that call's
+        # backward (the seed travels with the autograd node)
+        self._seed = (cfg.seed * 1000003 + 0x5EED + op_index) & (2**63 - 1)
+        self._calls = 0
 
     def forward(self, input_tensors, input_extra_tensors, output_extra_tensors, profiling=False):
         ids = input_tensors["enc_input_ids"]
@@ -56,7 +60,9 @@ class Embedding_v1(RopalaModule):
         out = EmbeddingFn.apply(self.word_embeddings.weight, self.position_embeddings.weight, ids, pos, self._bad)
         if self.training and self.embedding_dropout > 0:
             zero = torch.zeros(out.shape[-1], dtype=out.dtype, device=out.device)
-            out = BiasDropoutAddFn.apply(out, zero, torch.zeros_like(out), self.embedding_dropout, 0x5EED + self.op_index)
+            seed = self._seed + 7919 * self._calls
+            self._calls += 1
+            out = BiasDropoutAddFn.apply(out, zero, torch.zeros_like(out), self.embedding_dropout, seed)
         return {"hidden_states": out}
 
     def check_ids(self):

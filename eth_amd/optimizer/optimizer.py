@@ -86,6 +86,17 @@ class MegatronOptimizer:
             raise ValueError("model parameter is not owned by this optimizer")
         return p
 
+    def hyperparameters_for_model_parameter(self, model_parameter):
+        """{beta1, beta2, epsilon, weight_decay} of the parameter's group (what
+        the evidence snapshots record, optimizer/optimizer.py:113-131)."""
+        p = self.optimizer_parameter_for_model_parameter(model_parameter)
+        for group in self.optimizer.param_groups:
+            if any(q is p for q in group["params"]):
+                beta1, beta2 = group.get("betas", (None, None))
+                return {"beta1": beta1, "beta2": beta2, "epsilon": group.get("eps"),
+                        "weight_decay": group.get("weight_decay", 0.0)}
+        raise ValueError("optimizer parameter has no parameter group")
+
     def bind_gradient_sync(self, executor):
         """Fuse unscale / inf-nan flag / L2 partials into `executor`'s unpack.
 

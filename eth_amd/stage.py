@@ -18,17 +18,50 @@ import torch
 
 from . import kernels as K
 from .grad_sync.gpt_adapter import collect_stage_metadata
-from .loss import global_normalization_scale, gpt_loss_output, synthetic_gpt_batch
+from .loss import global_normalization_scale, gpt_loss_output, sum_loss_outputs, synthetic_gpt_batch
 from .grad_sync.manager import initialize_gradient_sync
 from .grad_sync.streamed import StreamedGradSync
 from .model.distributed import DistributedDataParallel
-from .model.flex_model import FlexGPTModel, middle_stage
+from .grad_sync.evidence import save_rank_snapshot
+from .model.flex_model import FlexGPTModel, middle_stage, op_range_stage
 from .model.functional import overlapped_wgrad
 from .model.flex_ops import GPTConfig
 from .optimizer.optimizer import get_megatron_optimizer
 
 
+def save_stage_snapshot(trainer, output_dir, phase, iteration, metrics=None, clock=None, run_metadata=None):
+    """Snapshot of a trainer's parameters, main grads and optimizer state
+    with the reference's record layout (training.py:720-808 gathers the same
+    three optimizer maps through the optimizer's model-parameter accessors)."""
+    opt = trainer.optimizer
+    state, master, hyper = {}, {}, {}
+    for b in trainer.bindings:
+        st = opt.state_for_model_parameter(b.parameter)
+        state[b.logical_param_id] = {k: st[k] for k in ("step", "exp_avg", "exp_avg_sq") if k in st}
+        master[b.logical_param_id] = opt.optimizer_parameter_for_model_parameter(b.parameter)
+        hyper[b.logical_param_id] = opt.hyperparameters_for_model_parameter(b.parameter)
+    base_clock = {"learning_rate": opt.param_groups[0]["lr"], "loss_scale": float(opt.get_loss_scale().item())}
+    return save_rank_snapshot(
+        output_dir,
+        phase=phase,
+        iteration=iteration,
+        global_rank=0,
+        descriptors=trainer.descriptors,
+        runtime_bindings=trainer.bindings,
+        optimizer_state_by_logical=state,
+        optimizer_parameter_by_logical=master,
+        optimizer_hyperparameters_by_logical=hyper,
+        clock={**base_clock, **(clock or {})},
+        metrics=metrics,
+        run_metadata=run_metadata,
+    )
+
+
 class MiddleStageTrainer:
+    """A middle pipeline stage (no embedding, no head): whole layers
+    `[first_layer, first_layer + num_layers)`, or any manifest op range
+    `op_range = (op_start, op_end)` that may cut a layer."""
+
     def __init__(
         self,
         cfg: GPTConfig,
@@ -42,25 +75,32 @@ class MiddleStageTrainer:
         sync_mode="block",
         bucket_cap_bytes=32 * 1024 * 1024,
         all_reduce_sum=None,
+        op_range=None,
+        recompute_ops=None,
+        runtime_evidence_dir=None,
     ):
         if cfg.params_dtype not in (torch.bfloat16, torch.float16):
             raise ValueError("the stage trains in bf16 or fp16")
         self.cfg = cfg
-        self.model = middle_stage(cfg, first_layer, num_layers)
+        if op_range is not None:
+            self.model = op_range_stage(cfg, *op_range, recompute_ops=recompute_ops)
+        else:
+            self.model = middle_stage(cfg, first_layer, num_layers, recompute_ops=recompute_ops)
         # main grads accumulate in fp32 for bf16 (as the reference forces) and
         # for fp16 too: the wgrad GEMM adds into fp32, which is strictly more
         # accurate than the reference's fp16 main_grad + later fp32 copy
         self.ddp = DistributedDataParallel(self.model, accumulate_allreduce_grads_in_fp32=True)
         lm = self.model.language_model
-        descriptors, bindings = collect_stage_metadata(lm.ops, self.model.op_start, self.model.op_end)
+        self.descriptors, self.bindings = collect_stage_metadata(lm.ops, self.model.op_start, self.model.op_end)
         self.grad_sync = initialize_gradient_sync(
-            descriptors,
-            bindings,
+            self.descriptors,
+            self.bindings,
             global_rank=0,
             expected_pipeline_ids=(0,),
             sync_mode=sync_mode,
             bucket_cap_bytes=bucket_cap_bytes,
             all_reduce_sum=all_reduce_sum or (lambda payload, handle: None),
+            runtime_evidence_dir=runtime_evidence_dir,
         )
         self.optimizer = get_megatron_optimizer(
             [self.model],
@@ -80,6 +120,76 @@ class MiddleStageTrainer:
         if dev.type == "cuda":
             self._streamed = StreamedGradSync(self.grad_sync.executor, dev)
 
+    # ------------------------------------------------ stage dict contract --
+    def forward_step(self, input_tensors, input_extra_tensors=None):
+        """Forward of one microbatch with the stage's dict I/O
+        (schedules.py:62-111, flex_model.py:554-600): `input_tensors` as the
+        previous stage sends them ({"hidden_states": [s, b, h]}) and the
+        side-channel tensors of ops in earlier stages this stage consumes.
+        Returns (outputs, output_extra_tensors, leaves); `leaves` are this
+        stage's own copies of the inputs, which collect the input gradients."""
+        ins = {k: v.detach().requires_grad_(True) for k, v in input_tensors.items()}
+        extras = {
+            k: v.detach().requires_grad_(v.is_floating_point()) for k, v in (input_extra_tensors or {}).items()
+        }
+        self.model.set_input_tensor(ins)
+        out, out_extra = self.model(None, dict(extras))
+        return out, out_extra, (ins, extras)
+
+    def backward_step(self, outputs, output_grads, output_extra_tensors=None, output_extra_grads=None, leaves=None):
+        """Backward of one microbatch (schedules.py:196-227): the upstream
+        gradients of the outputs and of the cross-stage side-channel outputs
+        enter one autograd pass (weight gradients into the fp32 main grads);
+        returns the gradients of the inputs and of the input side-channel
+        tensors, zeros where nothing flowed (schedules.py:151-172).
+
+        The reference assigns the side-channel gradients to `.grad` of its
+        outputs (schedules.py:113-117), which autograd does not read for a
+        tensor that is not a leaf; here they are backpropagated, so a stage
+        cut inside a layer gives the gradients of the uncut model."""
+        tensors, grads = [], []
+        for key in sorted(outputs):
+            tensors.append(outputs[key])
+            grads.append(output_grads[key])
+        for key in sorted(output_extra_tensors or {}):
+            g = (output_extra_grads or {}).get(key)
+            t = output_extra_tensors[key]
+            if g is not None and t.requires_grad:
+                tensors.append(t)
+                grads.append(g)
+        with overlapped_wgrad():
+            torch.autograd.backward(tensors, grads)
+        ins, extras = leaves if leaves is not None else ({}, {})
+        zero = lambda t: t.grad if t.grad is not None else torch.zeros_like(t)  # noqa: E731
+        return {k: zero(t) for k, t in ins.items()}, {k: zero(t) for k, t in extras.items() if t.is_floating_point()}
+
+    def train_step_microbatches(self, microbatches, normalization_scale=1.0):
+        """forward_backward_no_pipelining (schedules.py:236-281) and the rest
+        of train_step for this stage: every microbatch's forward and
+        backward, main grads accumulating across them (the first
+        contribution after the deferred zeroing stores, the rest add), then
+        one gradient sync and one optimizer step.
+
+        Each microbatch is a dict with `input_tensors`, `output_grads` and
+        optionally `input_extra_tensors` / `output_extra_grads`.  Returns
+        ([(outputs, output_extra_tensors, input_grads, input_extra_grads)],
+        update_successful, grad_norm)."""
+        if hasattr(normalization_scale, "item"):
+            normalization_scale = float(normalization_scale.item())
+        self.ddp.zero_grad_buffer(defer=True)
+        results = []
+        for mb in microbatches:
+            out, out_extra, leaves = self.forward_step(mb["input_tensors"], mb.get("input_extra_tensors"))
+            in_g, extra_g = self.backward_step(out, mb["output_grads"], out_extra, mb.get("output_extra_grads"),
+                                               leaves)
+            results.append(({k: v.detach() for k, v in out.items()}, {k: v.detach() for k, v in out_extra.items()},
+                            in_g, extra_g))
+        self.ddp.settle_grad_buffer()
+        self.grad_sync.execute(normalization_scale)
+        ok, norm, _zeros = self.optimizer.step()
+        return results, ok, norm
+
+    # --------------------------------------------- single-microbatch path --
     def forward_backward(self, x, dy):
         """Forward the stage on activations x [s, b, h] and backpropagate the
         upstream gradient dy; returns (output, input gradient)."""
@@ -92,14 +202,14 @@ class MiddleStageTrainer:
         return hidden.detach(), x.grad
 
     def train_step(self, x, dy, normalization_scale=1.0, streamed_sync=False):
-        """One step.  With streamed_sync each gradient bucket is packed /
-        all-reduced / unpacked as soon as the backward has written it,
-        overlapped with the rest of the backward; otherwise (the default) the
-        whole sync runs after it, as in the reference.  Both give identical
-        results.  On one GPU the all-reduce seam moves no data, and the
-        overlapped pack/unpack slows the backward's GEMMs by about as much as
-        it hides (measured 413 K vs 417-420 K tokens/s), so the overlap is
-        for deployments whose seam does real communication."""
+        """One step over one microbatch.  With streamed_sync each gradient
+        bucket is packed / all-reduced / unpacked as soon as the backward has
+        written it, overlapped with the rest of the backward; otherwise (the
+        default) the whole sync runs after it, as in the reference.  Both
+        give identical results.  On one GPU the all-reduce seam moves no
+        data, and the overlapped pack/unpack slows the backward's GEMMs by
+        about as much as it hides (measured 413 K vs 417-420 K tokens/s), so
+        the overlap is for deployments whose seam does real communication."""
         if hasattr(normalization_scale, "item"):
             normalization_scale = float(normalization_scale.item())
         # deferred: the first gradient written into each main_grad stores
@@ -118,6 +228,13 @@ class MiddleStageTrainer:
             self.grad_sync.execute(normalization_scale)
         ok, norm, zeros = self.optimizer.step()
         return out, dx, ok, norm
+
+    # ---------------------------------------------------------- evidence --
+    def record_evidence(self, output_dir, phase, iteration, metrics=None, clock=None, run_metadata=None):
+        """Write this rank's numerical snapshot (grad_sync/evidence.py layout,
+        training.py:720-808) for `phase` in init / pre_sync / post_sync /
+        post_step."""
+        return save_stage_snapshot(self, output_dir, phase, iteration, metrics, clock, run_metadata)
 
     def layer_parameters(self):
         """[{oracle name: parameter}] per layer, in layer order."""
@@ -148,19 +265,22 @@ class FirstLastStageTrainer:
     shape) and configs[4] (GPT-6.7B first+last, fp16)."""
 
     def __init__(self, cfg: GPTConfig, lr=1e-4, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01, clip_grad=1.0,
-                 sync_mode="block", bucket_cap_bytes=1024 * 1024, initial_loss_scale=2.0**16, unpadded_vocab=50257):
+                 sync_mode="block", bucket_cap_bytes=1024 * 1024, initial_loss_scale=2.0**16, unpadded_vocab=50257,
+                 recompute_ops=None, runtime_evidence_dir=None):
         self.cfg = cfg
         self.unpadded_vocab = unpadded_vocab
         n_ops = 10 * cfg.num_layers + 3
-        self.model = FlexGPTModel(cfg, 0, n_ops)
+        self.model = FlexGPTModel(cfg, 0, n_ops, recompute_ops=recompute_ops)
         ops = self.model.language_model.ops
         self.embedding, self.post = ops[0], ops[-1]
         with torch.no_grad():  # the head copy starts from the root (training.py:349-470)
             self.post.word_embeddings.weight.copy_(self.embedding.word_embeddings.weight)
         self.ddp = DistributedDataParallel(self.model, accumulate_allreduce_grads_in_fp32=True)
-        descriptors, bindings = collect_stage_metadata(ops, 0, n_ops)
-        self.grad_sync = initialize_gradient_sync(descriptors, bindings, global_rank=0, expected_pipeline_ids=(0,),
-                                                  sync_mode=sync_mode, bucket_cap_bytes=bucket_cap_bytes)
+        self.descriptors, self.bindings = collect_stage_metadata(ops, 0, n_ops)
+        self.grad_sync = initialize_gradient_sync(self.descriptors, self.bindings, global_rank=0,
+                                                  expected_pipeline_ids=(0,), sync_mode=sync_mode,
+                                                  bucket_cap_bytes=bucket_cap_bytes,
+                                                  runtime_evidence_dir=runtime_evidence_dir)
         self.optimizer = get_megatron_optimizer(
             [self.model], lr=lr, weight_decay=weight_decay, betas=betas, eps=eps, clip_grad=clip_grad,
             bf16=cfg.params_dtype == torch.bfloat16, fp16=cfg.params_dtype == torch.float16,
@@ -170,14 +290,16 @@ class FirstLastStageTrainer:
         # so the optimizer computes its statistics itself (no fused binding)
         self.nominal = float(cfg.micro_batch_size * cfg.seq_length)
 
-    def forward_backward(self, sample_ids, labels=None):
-        """Returns (per-token loss [b, s], LossOutput)."""
+    def forward_backward(self, sample_ids, labels=None, nominal=None):
+        """One microbatch: forward, loss contract, backward of
+        numerator / nominal times the loss scale (schedules.py:97-104,214-217).
+        Returns (per-token loss [b, s], LossOutput)."""
         tokens, mask, positions, _ = synthetic_gpt_batch(sample_ids, self.cfg.seq_length, self.unpadded_vocab,
                                                          self.embedding.word_embeddings.weight.device)
         extra = {} if labels is None else {"labels": labels}
         out = self.model({"enc_input_ids": tokens, "enc_position_ids": positions}, extra)
         losses = out["output"]
-        lo = gpt_loss_output(losses, mask, self.nominal)
+        lo = gpt_loss_output(losses, mask, self.nominal if nominal is None else nominal)
         output_tensor = lo.local_loss_sum / lo.nominal_global_loss_scale
         with overlapped_wgrad():
             torch.autograd.backward(self.optimizer.scale_loss(output_tensor))
@@ -194,3 +316,29 @@ class FirstLastStageTrainer:
         self.tie_gradients()
         ok, norm, zeros = self.optimizer.step()
         return losses, lo, ok, norm
+
+    def train_step_microbatches(self, sample_id_batches, labels=None):
+        """train_step over several microbatches (schedules.py:236-281): the
+        nominal loss scale is the global token count of the step
+        (config_normalization.py:535-541), every microbatch backpropagates
+        its numerator / nominal, main grads accumulate, and the sync
+        normalizes by nominal / (sum of the masks) -- the gradient of the
+        masked mean over all microbatches.  Returns (per-microbatch losses,
+        summed LossOutput pair, update_successful, grad_norm)."""
+        nominal = float(len(sample_id_batches) * self.cfg.micro_batch_size * self.cfg.seq_length)
+        self.ddp.zero_grad_buffer(defer=True)
+        losses, outs = [], []
+        for i, ids in enumerate(sample_id_batches):
+            lab = None if labels is None else labels[i]
+            l, lo = self.forward_backward(ids, lab, nominal=nominal)
+            losses.append(l)
+            outs.append(lo)
+        self.ddp.settle_grad_buffer()
+        numerator, weight = sum_loss_outputs(outs)
+        self.grad_sync.execute(global_normalization_scale(nominal, weight))
+        self.tie_gradients()
+        ok, norm, _zeros = self.optimizer.step()
+        return losses, (numerator, weight), ok, norm
+
+    def record_evidence(self, output_dir, phase, iteration, metrics=None, clock=None, run_metadata=None):
+        return save_stage_snapshot(self, output_dir, phase, iteration, metrics, clock, run_metadata)

@@ -276,7 +276,14 @@ int eth_attn_bwd(const eth_attn_desc_t* desc, const void* q, const void* k, cons
  *   (tokens/positions int64 [batch, seq]; out [seq, batch, hidden]); replaces
  *   Embedding_v1.forward (eth/runtime/megatron/model/flex_ops.py:450-485,
  *   VocabParallelEmbedding mpu/layers.py:136-205 at TP = 1).
- * eth_embedding_bwd: fp32 dword[tok] += dout, dpos[pos] += dout (atomic).
+ * eth_embedding_bwd: fp32 dword[tok] += dout, dpos[pos] += dout, bitwise
+ *   deterministic: the ids are sorted with their dout rows (in `workspace`
+ *   of eth_embedding_bwd_workspace(batch, seq) bytes) and each table row is
+ *   summed by one workgroup in dout-row order; batch * seq <= 32768, and
+ *   bits(vocab - 1) + bits(batch * seq - 1) <= 32.  Either table may be NULL.
+ *   Replaces the embedding's autograd backward (embedding_dense_backward, a
+ *   sort + segmented reduction) and the main_grad.add_ hook of
+ *   model/distributed.py:116-123.
  * eth_xent_fwd / eth_xent_bwd: per-row loss = logsumexp(z) - z[label] from
  *   16-bit logits [rows, ld], saving lse; dz = (softmax - onehot) * dloss.
  *   Replace vocab_parallel_cross_entropy(logits.float(), labels)
@@ -286,9 +293,10 @@ int eth_attn_bwd(const eth_attn_desc_t* desc, const void* q, const void* k, cons
 int eth_embedding_fwd(const int64_t* tokens, const int64_t* positions, const void* word,
                       const void* pos, void* out, int64_t batch, int64_t seq, int64_t hidden,
                       int64_t vocab, int64_t max_pos, int* bad_index, int dtype, void* stream);
+int64_t eth_embedding_bwd_workspace(int64_t batch, int64_t seq);
 int eth_embedding_bwd(const int64_t* tokens, const int64_t* positions, const void* dout,
-                      float* dword, float* dpos, int64_t batch, int64_t seq, int64_t hidden,
-                      int64_t vocab, int64_t max_pos, int dtype, void* stream);
+                      float* dword, float* dpos, void* workspace, int64_t batch, int64_t seq,
+                      int64_t hidden, int64_t vocab, int64_t max_pos, int dtype, void* stream);
 int eth_xent_fwd(const void* logits, int64_t ld, const int64_t* labels, float* loss, float* lse,
                  int64_t rows, int64_t vocab, int* bad_index, int dtype, void* stream);
 int eth_xent_bwd(const void* logits, int64_t ld, const int64_t* labels, const float* lse,

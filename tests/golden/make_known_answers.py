@@ -159,6 +159,17 @@ RECORDS = {
         "expected_scale": [65536.0, 65536.0, 131072.0, 131072.0, 131072.0, 65536.0, 32768.0, 16384.0, 16384.0,
                            16384.0, 16384.0, 32768.0],
     },
+    "runtime_evidence_four_to_two": {
+        "source": "tests/test_gradient_executor.py:70-148",
+        "groups": [["pg-a", [0]], ["pg-b", [0]]],
+        "fragments": [["f0", "p0", "pg-a", 2, 0], ["f1", "p1", "pg-b", 2, 1], ["f2", "p2", "pg-a", 2, 2],
+                      ["f3", "p3", "pg-b", 2, 3]],
+        "tensors": {"p0": [1.0, 2.0], "p1": [2.0, 3.0], "p2": [3.0, 4.0], "p3": [4.0, 5.0]},
+        "cap_bytes": 1024,
+        "iterations": 2,
+        "expected_collectives": {"tensor": 4, "block": 2},
+        "expected_payload_bytes": 32,
+    },
     "main_grad_accumulation": {
         "source": "tests/test_local_ddp_runtime.py:48-72",
         "param": [1.0, 2.0],

@@ -1,0 +1,273 @@
+"""GPU tests of the stage's dict contract around the kernels: stage cuts
+inside a layer with side-channel tensors crossing the cut
+(schedules.py:113-227, flex_model.py:63-240), several microbatches per step
+(schedules.py:236-281), activation recompute (flex_model.py:395-588), and the
+evidence the executor and the trainers write (grad_sync/runtime_evidence.py,
+grad_sync/evidence.py)."""
+
+import hashlib
+import json
+
+import numpy as np
+import pytest
+import torch
+
+from eth_amd.grad_sync.evidence import load_rank_snapshot
+from eth_amd.grad_sync.executor import GradientBucketExecutor
+from eth_amd.model.flex_ops import GPTConfig
+from eth_amd.stage import FirstLastStageTrainer, MiddleStageTrainer
+from oracle import gradsync as og
+from oracle import layer as ol
+from tests.conftest import announce
+from tests.helpers import known_answers, runtime_binding
+from tests.test_evidence_host import evidence_plan
+
+pytestmark = pytest.mark.gpu
+KA = known_answers()
+H, HEADS, FFN, SEQ, MB = 256, 4, 1024, 128, 2
+
+
+def _cfg(dtype=torch.bfloat16, layers=2, dropout=0.0, mb=MB, seed=5):
+    return GPTConfig(hidden_size=H, num_attention_heads=HEADS, ffn_hidden_size=FFN, num_layers=layers,
+                     seq_length=SEQ, micro_batch_size=mb, hidden_dropout=dropout, params_dtype=dtype, device="cuda",
+                     seed=seed)
+
+
+def _rel(a, b):
+    a, b = a.double().cpu(), b.double().cpu()
+    return (a - b).norm().item() / (b.norm().item() + 1e-30)
+
+
+def _named_grads(tr):
+    return {name: p.main_grad.clone() for name, p in tr.model.named_parameters()}
+
+
+def _copy_weights(src, dst):
+    """Give dst's parameters (a sub-range of src's ops) src's values."""
+    by_index = {op.op_index: op for op in src.model.language_model.ops}
+    with torch.no_grad():
+        for op in dst.model.language_model.ops:
+            for (n1, p1), (n2, p2) in zip(op.named_parameters(), by_index[op.op_index].named_parameters()):
+                assert n1 == n2
+                p1.copy_(p2)
+    dst.optimizer.reload_model_params()
+
+
+def _randomize(tr, gen):
+    with torch.no_grad():
+        for name, p in tr.model.named_parameters():
+            if name.endswith("bias"):
+                p.copy_((torch.randn(p.shape, generator=gen) * 0.02).to(p.dtype))
+    tr.optimizer.reload_model_params()
+
+
+def _inputs(gen, dtype=torch.bfloat16, mb=MB):
+    x = torch.randn(SEQ, mb, H, generator=gen).to(dtype).cuda()
+    dy = (torch.randn(SEQ, mb, H, generator=gen) * 1e-2).to(dtype).cuda()
+    return x, dy
+
+
+def test_stage_cut_inside_a_layer_gives_the_uncut_gradients(cuda):
+    """Ops [1, 5) and [5, 21) of a 2-layer model: the first stage ends at the
+    attention projection, so the LayerNorm residual (hidden_states_1) and the
+    projection bias (output_bias) cross the cut as side-channel tensors.
+    Outputs, the input gradient and every main grad equal the uncut stage's
+    bit for bit, except the projection bias, whose gradient crosses the cut
+    as a bf16 tensor (as in the reference) instead of straight into fp32."""
+    announce("stage cut inside a layer")
+    gen = torch.Generator().manual_seed(3)
+    whole = MiddleStageTrainer(_cfg())
+    _randomize(whole, gen)
+    first = MiddleStageTrainer(_cfg(), op_range=(1, 5))
+    second = MiddleStageTrainer(_cfg(), op_range=(5, 21))
+    _copy_weights(whole, first)
+    _copy_weights(whole, second)
+    x, dy = _inputs(gen)
+    for tr in (whole, first, second):
+        tr.ddp.zero_grad_buffer()
+    out_w, dx_w = whole.forward_backward(x, dy)
+    a_out, a_extra, a_leaves = first.forward_step({"hidden_states": x})
+    assert sorted(a_out) == ["output_tensor"] and sorted(a_extra) == ["hidden_states_1", "output_bias"]
+    b_out, b_extra, b_leaves = second.forward_step(a_out, a_extra)
+    assert b_extra == {}
+    b_in_grads, b_extra_grads = second.backward_step(b_out, {"hidden_states": dy}, b_extra, {}, b_leaves)
+    assert sorted(b_extra_grads) == ["hidden_states_1", "output_bias"]
+    a_in_grads, _ = first.backward_step(a_out, b_in_grads, a_extra, b_extra_grads, a_leaves)
+    torch.cuda.synchronize()
+    assert torch.equal(b_out["hidden_states"], out_w)
+    assert torch.equal(a_in_grads["hidden_states"], dx_w)
+    gw = _named_grads(whole)
+    cut = {**{f"0.{k}": v for k, v in _named_grads(first).items()}, **{f"1.{k}": v for k, v in _named_grads(second).items()}}
+    by_index = {}
+    for tr, tag in ((first, "0"), (second, "1")):
+        for op in tr.model.language_model.ops:
+            for n, p in op.named_parameters():
+                by_index[(op.op_index, n)] = p.main_grad
+    for op in whole.model.language_model.ops:
+        for n, p in op.named_parameters():
+            g = by_index[(op.op_index, n)]
+            if op.name == "enc-attention-dense" and n == "dense.bias" and op.op_index == 4:
+                assert _rel(g, p.main_grad) < 1e-2, (op.op_index, n)
+            else:
+                assert torch.equal(g, p.main_grad), (op.op_index, n)
+    assert len(cut) == len(gw)
+
+
+def test_microbatches_accumulate_main_grads(cuda):
+    """Two microbatches in one step: every main grad is the fp32 sum of the
+    two microbatches' gradients (bit for bit against running them one at a
+    time), the outputs and input gradients are each microbatch's own, and
+    the step applies once."""
+    announce("two microbatches per step")
+    gen = torch.Generator().manual_seed(4)
+    tr = MiddleStageTrainer(_cfg())
+    _randomize(tr, gen)
+    mbs = [_inputs(gen) for _ in range(2)]
+    singles = []
+    for x, dy in mbs:
+        tr.ddp.zero_grad_buffer()
+        out, dx = tr.forward_backward(x, dy)
+        singles.append((out.clone(), dx.clone(), _named_grads(tr)))
+    results, ok, norm = tr.train_step_microbatches(
+        [{"input_tensors": {"hidden_states": x}, "output_grads": {"hidden_states": dy}} for x, dy in mbs]
+    )
+    torch.cuda.synchronize()
+    assert ok and np.isfinite(norm)
+    for (out, _extra, in_g, _eg), (s_out, s_dx, _) in zip(results, singles):
+        assert torch.equal(out["hidden_states"], s_out)
+        assert torch.equal(in_g["hidden_states"], s_dx)
+    # the main grads after the step hold the synced (unscaled, unclipped)
+    # sum; recompute it from the single runs
+    for name, p in tr.model.named_parameters():
+        expect = singles[0][2][name] + singles[1][2][name]
+        assert torch.equal(p.main_grad, expect), name
+
+
+@pytest.mark.parametrize("pattern", ["all", "attention-only"])
+@pytest.mark.parametrize("dropout", [0.0, 0.1])
+def test_recompute_is_bit_identical(cuda, pattern, dropout):
+    """Activation recompute over whole layers, or over the middle of each
+    layer (ops 1-6: QKV to the 2nd LayerNorm, so side-channel tensors cross
+    the segment edges), gives the outputs, input gradient and main grads of
+    the plain stage bit for bit, with dropout masks replayed."""
+    announce(f"recompute {pattern} dropout {dropout}")
+    gen = torch.Generator().manual_seed(6)
+    flags = {"all": [1] * 20, "attention-only": ([0] + [1] * 6 + [0] * 3) * 2}[pattern]
+    plain = MiddleStageTrainer(_cfg(dropout=dropout))
+    ckpt = MiddleStageTrainer(_cfg(dropout=dropout), recompute_ops=flags)
+    _randomize(plain, gen)
+    _copy_weights(plain, ckpt)
+    x, dy = _inputs(gen)
+    for tr in (plain, ckpt):
+        tr.model.train()
+        tr.ddp.zero_grad_buffer()
+    out_p, dx_p = plain.forward_backward(x, dy)
+    out_c, dx_c = ckpt.forward_backward(x, dy)
+    torch.cuda.synchronize()
+    assert torch.equal(out_p, out_c)
+    assert torch.equal(dx_p, dx_c)
+    gp, gc = _named_grads(plain), _named_grads(ckpt)
+    for name in gp:
+        assert torch.equal(gp[name], gc[name]), name
+    if dropout:
+        assert any(getattr(op, "_calls", 0) for op in ckpt.model.language_model.ops)
+
+
+def test_first_last_microbatches_match_the_fp64_oracle(cuda):
+    """Two microbatches of one sample each on the first+last stage: the
+    synced main grads are the gradients of the masked mean over both
+    samples (fp64 oracle on the 2-sample batch)."""
+    announce("first+last, two microbatches")
+    from tests.test_gpu_full_stage import _oracle_params, tr_layer_params
+
+    cfg = GPTConfig(hidden_size=H, num_attention_heads=HEADS, ffn_hidden_size=FFN, num_layers=2, seq_length=SEQ,
+                    micro_batch_size=1, padded_vocab_size=50304, params_dtype=torch.bfloat16, device="cuda", seed=11)
+    tr = FirstLastStageTrainer(cfg, initial_loss_scale=1.0)
+    params = _oracle_params(tr)
+    from eth_amd.loss import synthetic_gpt_batch
+
+    tokens, mask, positions, _ = synthetic_gpt_batch([3, 8], SEQ, 50257, "cpu")
+    ref_losses, ref_mean, grads = ol.full_model_fwd_bwd(tokens, positions, mask, params, HEADS)
+    # stop before the optimizer: run the pieces of train_step_microbatches
+    tr.ddp.zero_grad_buffer(defer=True)
+    outs = [tr.forward_backward([i], nominal=2.0 * SEQ) for i in (3, 8)]
+    tr.ddp.settle_grad_buffer()
+    from eth_amd.loss import global_normalization_scale, sum_loss_outputs
+
+    num, weight = sum_loss_outputs([lo for _, lo in outs])
+    tr.grad_sync.execute(global_normalization_scale(2.0 * SEQ, weight))
+    tr.tie_gradients()
+    torch.cuda.synchronize()
+    assert _rel(torch.cat([l for l, _ in outs]), ref_losses) < 2e-2
+    assert abs((num / weight).item() - ref_mean.item()) < 2e-2 * abs(ref_mean.item())
+    checks = [(tr.embedding.word_embeddings.weight, grads["word"]), (tr.embedding.position_embeddings.weight, grads["pos"])]
+    for lp, gl in zip(tr_layer_params(tr), grads["layers"]):
+        checks += [(p, gl[k]) for k, p in lp.items()]
+    for p, ref in checks:
+        assert _rel(p.main_grad, ref) < 5e-2
+    # and the packaged step applies
+    losses, (num, weight), ok, norm = tr.train_step_microbatches([[3], [8]])
+    assert ok and np.isfinite(norm)
+
+
+def test_executor_runtime_evidence_hashes_the_packed_bytes(cuda, tmp_path):
+    """The reference's known answer (4 tensor-mode vs 2 block-mode
+    collectives, equal payload hash) through the HIP pack: every bucket's
+    hash is the SHA-256 of the oracle's packed payload."""
+    announce("runtime evidence through the executor")
+    rec = KA["runtime_evidence_four_to_two"]
+
+    class Registry:
+        group_count = 2
+        creation_count = 2
+
+        def handle(self, gid):
+            return gid
+
+    reports = {}
+    for mode in ("tensor", "block"):
+        plan = evidence_plan(rec, mode)
+        grads = {lid: torch.tensor(v, device=cuda) for lid, v in rec["tensors"].items()}
+        descs = [type("D", (), {"logical_param_id": lid, "partition_dim": 0})() for lid in grads]
+        ex = GradientBucketExecutor(plan, 0, descs, [runtime_binding(l, t) for l, t in grads.items()], Registry(),
+                                    lambda payload, handle: None, runtime_evidence_dir=tmp_path / mode)
+        for _ in range(rec["iterations"]):
+            for lid, v in rec["tensors"].items():
+                grads[lid].copy_(torch.tensor(v))
+            ex.execute()
+        host = {lid: np.asarray(v, dtype=np.float32) for lid, v in rec["tensors"].items()}
+        packed = og.execute(plan, 0, {l: type("D", (), {"partition_dim": 0})() for l in host}, host)
+        report = json.loads((tmp_path / mode / "rank-00000.json").read_text())
+        reports[mode] = report
+        it = report["iterations"][-1]
+        assert it["collective_count"] == rec["expected_collectives"][mode]
+        assert [b["packed_payload_sha256"] for b in it["buckets"]] == [hashlib.sha256(p.tobytes()).hexdigest()
+                                                                        for p in packed]
+        assert report["scratch_stable"]
+    assert reports["tensor"]["iterations"][0]["packed_payload_sha256"] == \
+        reports["block"]["iterations"][0]["packed_payload_sha256"]
+
+
+def test_trainer_evidence_snapshot_and_runtime_record(cuda, tmp_path):
+    """A training step with runtime evidence on, then a post_step snapshot:
+    the JSON lists every bucket of the plan, and the snapshot holds the
+    step's main grads, fp32 masters and AdamW state for every parameter."""
+    announce("trainer evidence")
+    tr = MiddleStageTrainer(_cfg(), runtime_evidence_dir=tmp_path / "runtime")
+    gen = torch.Generator().manual_seed(9)
+    x, dy = _inputs(gen)
+    _, _, ok, _ = tr.train_step(x, dy)
+    path = tr.record_evidence(tmp_path / "numerical", "post_step", 1, metrics={"grad_norm": 1.0})
+    torch.cuda.synchronize()
+    report = json.loads((tmp_path / "runtime" / "rank-00000.json").read_text())
+    assert report["iterations"][0]["collective_count"] == len(tr.grad_sync.plan.global_bucket_order)
+    snap = load_rank_snapshot(path)
+    assert snap["phase"] == "post_step" and len(snap["records"]) == len(tr.bindings)
+    by_id = {b.logical_param_id: b for b in tr.bindings}
+    for r in snap["records"]:
+        b = by_id[r["descriptor"]["logical_param_id"]]
+        assert torch.equal(r["main_grad"], b.main_grad.cpu())
+        assert torch.equal(r["parameter"], b.parameter.detach().cpu())
+        assert r["optimizer_parameter"].dtype == torch.float32
+        assert r["optimizer_state"]["step"].item() == 1.0
+        assert set(r["optimizer_hyperparameters"]) == {"beta1", "beta2", "epsilon", "weight_decay"}

@@ -294,3 +294,34 @@ def test_whole_model_gradients_are_the_directional_derivatives():
     minus = {**params, "layers": [{**lp, "fc1_w": lp["fc1_w"] - eps * D}]}
     fd = (mean_at(plus) - mean_at(minus)) / (2 * eps)
     assert fd == pytest.approx((grads["layers"][0]["fc1_w"] * D).sum().item(), rel=1e-6, abs=1e-12)
+
+
+# --------------------------------------------------------- embedding backward --
+def test_ordered_embedding_grad_equals_index_add():
+    """Against torch's index_add in fp64 (the scatter-add the embedding
+    backward is): exactly for small-integer gradients, to fp32 rounding
+    otherwise; ids past the table are clamped; accumulates into the table."""
+    import numpy as np
+
+    gen = torch.Generator().manual_seed(12)
+    s, b, h, V = 9, 3, 16, 7
+    tok = torch.randint(0, V, (b, s), generator=gen)
+    tok[0, 0] = V + 3  # clamped to V - 1
+    pos = torch.arange(s).expand(b, s).contiguous()
+    for dout in (torch.randint(-8, 9, (s, b, h), generator=gen).float(), torch.randn(s, b, h, generator=gen)):
+        start = torch.randn(V, h, generator=gen)
+        word = start.numpy().copy()
+        posg = np.zeros((s, h), dtype=np.float32)
+        ol.embedding_grad_ordered(tok.numpy(), pos.numpy(), dout.numpy(), word, posg)
+        flat = dout.transpose(0, 1).reshape(-1, h).double()
+        ref_w = start.double().index_add(0, tok.clamp(0, V - 1).reshape(-1), flat)
+        ref_p = torch.zeros(s, h, dtype=torch.float64).index_add(0, pos.reshape(-1), flat)
+        exact = dout.abs().max() <= 8 and float(dout.round().sub(dout).abs().max()) == 0.0
+        tol = 0 if exact else 1e-5
+        assert torch.allclose(torch.from_numpy(posg).double(), ref_p, rtol=0, atol=tol)
+        if exact:
+            # integers: the ordered fp32 sum is exact, so only the add into
+            # the random start rounds
+            assert torch.allclose(torch.from_numpy(word).double(), ref_w, rtol=2**-23, atol=0)
+        else:
+            assert torch.allclose(torch.from_numpy(word).double(), ref_w, rtol=0, atol=1e-5)
