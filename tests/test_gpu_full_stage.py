@@ -255,16 +255,26 @@ def test_c5_full_shape_trains(cuda):
 
     cfg = GPTConfig(num_layers=2, seq_length=2048, micro_batch_size=2, seed=1234, **C5_WIDTHS)
     tr = _c5_trainer(cfg)
+    # uniform labels: with the reference's labels = 0 every gradient of the
+    # step pushes the same logit up, and AdamW's first (sign-like) update
+    # across 4096-wide layers already saturates the fp16 softmax, leaving
+    # the second step with a zero loss and zero gradients
+    gen = torch.Generator(device="cuda").manual_seed(7)
     for step in range(2):
-        losses, lo, ok, norm = tr.train_step([2 * step, 2 * step + 1])
+        labels = torch.randint(0, 50257, (2, 2048), generator=gen, device="cuda")
+        losses, lo, ok, norm = tr.train_step([2 * step, 2 * step + 1], labels)
         torch.cuda.synchronize()
         assert ok, f"step {step} overflowed at loss scale {tr.optimizer.get_loss_scale().item()}"
         assert norm is not None and np.isfinite(norm) and norm > 0
         assert bool(torch.isfinite(losses).all())
         mean = (lo.local_loss_sum / lo.local_loss_weight).item()
-        # unit-variance LN output against N(0, 0.02) head rows: logits of
-        # variance 0.02^2 * 4096, so the expected loss is ln V + var / 2
-        assert abs(mean - (math.log(50304) + 0.5 * 0.02**2 * 4096)) < 1.0, mean
+        if step == 0:
+            # unit-variance LN output against N(0, 0.02) head rows: logits of
+            # variance 0.02^2 * 4096, so the expected loss is ln V + var / 2
+            assert abs(mean - (math.log(50304) + 0.5 * 0.02**2 * 4096)) < 1.0, mean
+            first = mean
+        else:
+            assert np.isfinite(mean) and mean < first + 1.0, (first, mean)
         for name, p in tr.model.named_parameters():
             assert bool(torch.isfinite(p.main_grad).all()), name
         assert torch.equal(tr.embedding.word_embeddings.weight, tr.post.word_embeddings.weight)
