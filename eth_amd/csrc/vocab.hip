@@ -16,6 +16,8 @@
 // Token ids outside [0, V) are clamped for the memory access and reported in
 // `bad_index` (set to 1), which the host checks; the reference's embedding
 // would raise for them.
+#include <mutex>
+
 #include "common.h"
 
 namespace eth {
@@ -345,6 +347,52 @@ extern "C" int eth_embedding_bwd(const int64_t* tokens, const int64_t* positions
                                                       (int)hidden, row_bits);
   ETH_CHECK_LAUNCH("eth_embedding_bwd");
   return ETH_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free form of eth_embedding_bwd: the sort keys live in a
+// file-scope device array instead of a caller workspace.  Each GPU holds its
+// own copy of the array (2 * kEmbSortMax keys = 256 KiB) until the process
+// ends; its device address is looked up once per device and kept.  Calls on
+// one GPU share the array, so calls that overlap on one GPU race.
+static __device__ __align__(256) uint32_t scratch[2 * kEmbSortMax];
+constexpr int kMaxDevices = 64;
+static void* g_scratch_ptr[kMaxDevices];
+static std::mutex g_scratch_mutex;
+
+static int scratch_for_current_device(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    ::eth::set_error("eth_embedding_bwd_noalloc: no usable current device (%s)", hipGetErrorString(e));
+    return ETH_ERR_HIP;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr) {
+      ::eth::set_error("eth_embedding_bwd_noalloc: hipGetSymbolAddress failed: %s", hipGetErrorString(e));
+      return ETH_ERR_HIP;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return ETH_OK;
+}
+
+extern "C" int eth_embedding_bwd_noalloc(const int64_t* tokens, const int64_t* positions, const void* dout,
+                                         float* dword, float* dpos, int64_t batch, int64_t seq, int64_t hidden,
+                                         int64_t vocab, int64_t max_pos, int dtype, void* stream) {
+  ETH_CHECK_ARG(batch > 0 && seq > 0 && batch * seq <= kEmbSortMax,
+                "eth_embedding_bwd_noalloc: batch * seq must be in [1, %d] (the static scratch holds %d keys "
+                "per table), got %lld",
+                kEmbSortMax, kEmbSortMax, (long long)(batch * seq));
+  void* ws = nullptr;
+  const int rc = scratch_for_current_device(&ws);
+  if (rc != ETH_OK) return rc;
+  return eth_embedding_bwd(tokens, positions, dout, dword, dpos, ws, batch, seq, hidden, vocab, max_pos, dtype,
+                           stream);
 }
 
 extern "C" int eth_xent_fwd(const void* logits, int64_t ld, const int64_t* labels, float* loss, float* lse,

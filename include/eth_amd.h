@@ -297,6 +297,18 @@ int64_t eth_embedding_bwd_workspace(int64_t batch, int64_t seq);
 int eth_embedding_bwd(const int64_t* tokens, const int64_t* positions, const void* dout,
                       float* dword, float* dpos, void* workspace, int64_t batch, int64_t seq,
                       int64_t hidden, int64_t vocab, int64_t max_pos, int dtype, void* stream);
+/* Allocation-free form of eth_embedding_bwd, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  It has no counterpart in the
+ * reference.  The sort keys live in a static device array of 2 * 32768 keys
+ * (256 KiB per GPU, held until the process ends) instead of a caller
+ * workspace; batch * seq beyond 32768 is rejected.  Every call on one GPU
+ * uses that GPU's array, so calls that overlap on one GPU race.  Same
+ * arguments and results as eth_embedding_bwd otherwise; calls no
+ * allocating routine. */
+int eth_embedding_bwd_noalloc(const int64_t* tokens, const int64_t* positions, const void* dout,
+                              float* dword, float* dpos, int64_t batch, int64_t seq, int64_t hidden,
+                              int64_t vocab, int64_t max_pos, int dtype, void* stream);
 int eth_xent_fwd(const void* logits, int64_t ld, const int64_t* labels, float* loss, float* lse,
                  int64_t rows, int64_t vocab, int* bad_index, int dtype, void* stream);
 int eth_xent_bwd(const void* logits, int64_t ld, const int64_t* labels, const float* lse,
