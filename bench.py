@@ -407,6 +407,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-hbm-path", action="store_true")
     ap.add_argument("--no-first-last", action="store_true")
+    ap.add_argument("--inline-update", action="store_true",
+                    help="run the AdamW update in line instead of overlapped with the next step's forward")
     ap.add_argument("--first-last-only", action="store_true",
                     help="time only the configs[4] first+last stage (for its kernel profile)")
     ap.add_argument("--copy-probe", action="store_true",
@@ -431,7 +433,8 @@ def main():
 
     cfg = GPTConfig(hidden_size=H, num_attention_heads=HEADS, ffn_hidden_size=FFN, num_layers=LAYERS,
                     seq_length=SEQ, micro_batch_size=MB, params_dtype=torch.bfloat16, device="cuda", seed=1234)
-    tr = MiddleStageTrainer(cfg, lr=1e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, clip_grad=1.0)
+    tr = MiddleStageTrainer(cfg, lr=1e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, clip_grad=1.0,
+                            overlap_optimizer=not args.inline_update)
     g = torch.Generator(device="cuda").manual_seed(1234)
     x = torch.randn(SEQ, MB, H, device="cuda", generator=g).to(torch.bfloat16)
     dy = (torch.randn(SEQ, MB, H, device="cuda", generator=g) * 1e-3).to(torch.bfloat16)

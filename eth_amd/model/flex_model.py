@@ -30,6 +30,20 @@ from .flex_ops import GPTConfig, build_gpt_op_list, gen_op
 _SEGMENT_BREAK = "enc-1st-layernorm"
 
 
+def await_parameters(op):
+    """Make the current stream wait for the pending update of op's
+    parameters (an optimizer step overlapped with this forward leaves its
+    events on them), once per event."""
+    seen = set()
+    for p in op.parameters():
+        ev = getattr(p, "_eth_ready_event", None)
+        if ev is not None:
+            if id(ev) not in seen:
+                torch.cuda.current_stream(p.device).wait_event(ev)
+                seen.add(id(ev))
+            p._eth_ready_event = None
+
+
 def _rng_state(ops):
     return {id(op): op._calls for op in ops if hasattr(op, "_calls")}
 
@@ -59,6 +73,7 @@ class _Segment:
         extras = dict(zip(self.extra_keys, tensors[nh:]))
         cross = {}
         for op in self.ops:
+            await_parameters(op)
             hidden = op(hidden, extras, cross)
         layout = (tuple(sorted(hidden)), tuple(sorted(extras)), tuple(sorted(cross)))
         if self.out_layout is None:
@@ -169,12 +184,14 @@ class FlexPipeModel(nn.Module):
         hidden = inputs if self.pre_process else self.input_tensor
         if not any(self.recompute_ops):
             for op in self.ops:
+                await_parameters(op)
                 hidden = op(hidden, input_extra_tensors, output_extra_tensors)
         else:
             for start, end, ckpt in self.segments():
                 if ckpt:
                     hidden = self._checkpointed(start, end, hidden, input_extra_tensors, output_extra_tensors)
                 else:
+                    await_parameters(self.ops[start])
                     hidden = self.ops[start](hidden, input_extra_tensors, output_extra_tensors)
         if self.post_process:
             return hidden

@@ -30,6 +30,8 @@ class FusedAdamW(torch.optim.Optimizer):
         self._tables = None
         self._model_copies = {}
         self._model_dtype = nat.ETH_F32
+        self._partition = None
+        self.part_events = []
         self._allocate_state()
 
     # ---------------------------------------------------------------- state --
@@ -59,6 +61,14 @@ class FusedAdamW(torch.optim.Optimizer):
             st["exp_avg_sq"] = self._exp_avg_sq_flat[off : off + p.numel()].view_as(p)
             off += n
 
+    def set_partition(self, parts):
+        """Split every step into one launch per part (a list of parameter
+        lists, in launch order; parameters in no part form a last part),
+        with a HIP event recorded after each launch in `part_events`, so
+        later work can wait for the parameters it reads only."""
+        self._partition = [list(part) for part in parts] if parts else None
+        self._table_key = None
+
     def set_model_copies(self, mapping, model_dtype):
         """Master parameter -> 16-bit model parameter written by every step."""
         self._model_copies = dict(mapping)
@@ -73,16 +83,26 @@ class FusedAdamW(torch.optim.Optimizer):
             for p in g["params"]
         )
 
+    def _parts(self):
+        if not self._partition:
+            return [[p for g in self.param_groups for p in g["params"]]]
+        placed = {id(p) for part in self._partition for p in part}
+        rest = [p for g in self.param_groups for p in g["params"] if id(p) not in placed]
+        return [*self._partition, rest] if rest else list(self._partition)
+
     def _build_tables(self):
-        tensors = []
-        chunks = []
+        group_of = {id(p): g for g in self.param_groups for p in g["params"]}
         cap = nat.CHUNK_ELEMS
-        for g in self.param_groups:
-            for p in g["params"]:
+        device = self._all_params()[0].device
+        self._tables = []
+        for part in self._parts():
+            tensors, chunks = [], []
+            for p in part:
                 if p.grad is None:
                     continue
                 if p.grad.dtype != torch.float32 or not p.grad.is_contiguous() or p.grad.shape != p.shape:
                     raise ValueError("FusedAdamW needs contiguous fp32 gradients shaped like the parameter")
+                g = group_of[id(p)]
                 st = self.state[p]
                 model = self._model_copies.get(p)
                 idx = len(tensors)
@@ -100,21 +120,22 @@ class FusedAdamW(torch.optim.Optimizer):
                 )
                 for start in range(0, p.numel(), cap):
                     chunks.append((idx, min(cap, p.numel() - start), start))
-        ttab = np.zeros(len(tensors), dtype=nat.ADAM_TENSOR_DTYPE)
-        for i, name in enumerate(nat.ADAM_TENSOR_DTYPE.names):
-            ttab[name] = [t[i] for t in tensors]
-        ctab = np.zeros(len(chunks), dtype=nat.ADAM_CHUNK_DTYPE)
-        if chunks:
-            arr = np.asarray(chunks, dtype=np.int64)
-            ctab["tensor"] = arr[:, 0]
-            ctab["n"] = arr[:, 1]
-            ctab["start"] = arr[:, 2]
-        device = self._all_params()[0].device
-        self._tables = (
-            nat.table_to_device(ttab, device) if len(ttab) else None,
-            nat.table_to_device(ctab, device) if len(ctab) else None,
-            len(ctab),
-        )
+            ttab = np.zeros(len(tensors), dtype=nat.ADAM_TENSOR_DTYPE)
+            for i, name in enumerate(nat.ADAM_TENSOR_DTYPE.names):
+                ttab[name] = [t[i] for t in tensors]
+            ctab = np.zeros(len(chunks), dtype=nat.ADAM_CHUNK_DTYPE)
+            if chunks:
+                arr = np.asarray(chunks, dtype=np.int64)
+                ctab["tensor"] = arr[:, 0]
+                ctab["n"] = arr[:, 1]
+                ctab["start"] = arr[:, 2]
+            self._tables.append(
+                (
+                    nat.table_to_device(ttab, device) if len(ttab) else None,
+                    nat.table_to_device(ctab, device) if len(ctab) else None,
+                    len(ctab),
+                )
+            )
 
     # ----------------------------------------------------------------- step --
     @torch.no_grad()
@@ -130,29 +151,34 @@ class FusedAdamW(torch.optim.Optimizer):
         if key != self._table_key:
             self._build_tables()
             self._table_key = key
-        ttab, ctab, n_chunks = self._tables
-        if n_chunks == 0:
-            return loss
         groups = {(g["betas"], g["eps"]) for g in self.param_groups}
         if len(groups) != 1:
             raise ValueError("FusedAdamW needs identical betas/eps across parameter groups")
         (beta1, beta2), eps = next(iter(groups))
         # all parameters step together; the state mirrors torch's per-param step
         step = int(self.state[params[0]]["step"].item()) + 1
-        nat.call(
-            "eth_adam_step",
-            nat.ptr(ttab),
-            nat.ptr(ctab),
-            n_chunks,
-            float(beta1),
-            float(beta2),
-            float(eps),
-            step,
-            self._model_dtype,
-            nat.ptr(stats),
-            nat.ptr(found_inf),
-            nat.stream_ptr(params[0].device),
-        )
+        device = params[0].device
+        self.part_events = []
+        for ttab, ctab, n_chunks in self._tables:
+            if n_chunks:
+                nat.call(
+                    "eth_adam_step",
+                    nat.ptr(ttab),
+                    nat.ptr(ctab),
+                    n_chunks,
+                    float(beta1),
+                    float(beta2),
+                    float(eps),
+                    step,
+                    self._model_dtype,
+                    nat.ptr(stats),
+                    nat.ptr(found_inf),
+                    nat.stream_ptr(device),
+                )
+            if self._partition:
+                ev = torch.cuda.Event()
+                ev.record(torch.cuda.current_stream(device))
+                self.part_events.append(ev)
         self._pending_step = step
         if found_inf is None:
             self.commit_step(True)

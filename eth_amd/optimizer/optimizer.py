@@ -54,6 +54,7 @@ class MegatronOptimizer:
         self._stats_key = None
         self._model_to_optimizer_param = {}
         self._host_flags = None
+        self._overlap = None  # (side stream, [[model params] per part]) when the update overlaps the next forward
 
     # ----------------------------------------------------------- plumbing --
     @property
@@ -96,6 +97,32 @@ class MegatronOptimizer:
                 return {"beta1": beta1, "beta2": beta2, "epsilon": group.get("eps"),
                         "weight_decay": group.get("weight_decay", 0.0)}
         raise ValueError("optimizer parameter has no parameter group")
+
+    def overlap_with_next_forward(self, model_param_parts):
+        """Run the AdamW update on a side stream (default priority), one
+        launch per part of `model_param_parts` (lists of model parameters, in
+        the order the next forward reads them), and leave on each model
+        parameter the event after which its new value is written
+        (`_eth_ready_event`).  The stage's forward waits for those events op
+        by op, so the update of later layers overlaps the forward of earlier
+        ones; every result is the same as with the update in line."""
+        dev = self._device()
+        parts = [[self.optimizer_parameter_for_model_parameter(p) for p in part] for part in model_param_parts]
+        self.optimizer.set_partition(parts)
+        self._overlap = (torch.cuda.Stream(device=dev), [list(part) for part in model_param_parts])
+
+    def join_overlapped_update(self):
+        """Make the current stream wait for every part of an overlapped update
+        that no forward op has waited for yet."""
+        if self._overlap is None:
+            return
+        stream = torch.cuda.current_stream(self._device())
+        for part in self._overlap[1]:
+            for p in part:
+                ev = getattr(p, "_eth_ready_event", None)
+                if ev is not None:
+                    stream.wait_event(ev)
+                    p._eth_ready_event = None
 
     def bind_gradient_sync(self, executor):
         """Fuse unscale / inf-nan flag / L2 partials into `executor`'s unpack.
@@ -172,6 +199,7 @@ class MegatronOptimizer:
 
     @torch.no_grad()
     def step(self):
+        self.join_overlapped_update()
         self._copy_model_grads_to_main_grads()
         scaler = self.grad_scaler
         need_norm = self.clip_grad > 0.0
@@ -200,10 +228,22 @@ class MegatronOptimizer:
         host = None
         if st is not None and (need_norm or scaler is not None):
             host = self._read_back(st)
-        self.optimizer.step(
-            stats=st.stats if need_norm else None,
-            found_inf=st.found_inf if scaler is not None else None,
-        )
+        if self._overlap is None:
+            self.optimizer.step(
+                stats=st.stats if need_norm else None,
+                found_inf=st.found_inf if scaler is not None else None,
+            )
+        else:
+            side, model_parts = self._overlap
+            side.wait_stream(torch.cuda.current_stream(self._device()))
+            with torch.cuda.stream(side):
+                self.optimizer.step(
+                    stats=st.stats if need_norm else None,
+                    found_inf=st.found_inf if scaler is not None else None,
+                )
+            for part, ev in zip(model_parts, self.optimizer.part_events):
+                for p in part:
+                    p._eth_ready_event = ev
         if host is not None:
             host[1].synchronize()
         if scaler is not None:

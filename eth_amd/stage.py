@@ -78,6 +78,7 @@ class MiddleStageTrainer:
         op_range=None,
         recompute_ops=None,
         runtime_evidence_dir=None,
+        overlap_optimizer=False,
     ):
         if cfg.params_dtype not in (torch.bfloat16, torch.float16):
             raise ValueError("the stage trains in bf16 or fp16")
@@ -113,6 +114,13 @@ class MiddleStageTrainer:
             fp16=cfg.params_dtype == torch.float16,
         )
         self.optimizer.bind_gradient_sync(self.grad_sync.executor)
+        if overlap_optimizer:
+            # the update of layer l overlaps the next step's forward of the
+            # layers before it (one AdamW launch per layer, in forward order)
+            by_layer = {}
+            for op in self.model.language_model.ops:
+                by_layer.setdefault((op.op_index - 1) // 10, []).extend(op.parameters())
+            self.optimizer.overlap_with_next_forward([by_layer[k] for k in sorted(by_layer)])
         # buckets synced during the backward, as soon as their gradients
         # exist (train_step(streamed_sync=True))
         self._streamed = None
@@ -178,12 +186,14 @@ class MiddleStageTrainer:
             normalization_scale = float(normalization_scale.item())
         self.ddp.zero_grad_buffer(defer=True)
         results = []
+        # (the forwards below wait for an overlapped update layer by layer)
         for mb in microbatches:
             out, out_extra, leaves = self.forward_step(mb["input_tensors"], mb.get("input_extra_tensors"))
             in_g, extra_g = self.backward_step(out, mb["output_grads"], out_extra, mb.get("output_extra_grads"),
                                                leaves)
             results.append(({k: v.detach() for k, v in out.items()}, {k: v.detach() for k, v in out_extra.items()},
                             in_g, extra_g))
+        self.optimizer.join_overlapped_update()
         self.ddp.settle_grad_buffer()
         self.grad_sync.execute(normalization_scale)
         ok, norm, _zeros = self.optimizer.step()
@@ -216,6 +226,8 @@ class MiddleStageTrainer:
         self.ddp.zero_grad_buffer(defer=True)
         streamed = streamed_sync and self._streamed is not None
         if streamed:
+            # the sync resets the statistics the previous update reads
+            self.optimizer.join_overlapped_update()
             self._streamed.start(normalization_scale)
             try:
                 out, dx = self.forward_backward(x, dy)
@@ -224,6 +236,7 @@ class MiddleStageTrainer:
             self.ddp.settle_grad_buffer()
         else:
             out, dx = self.forward_backward(x, dy)
+            self.optimizer.join_overlapped_update()
             self.ddp.settle_grad_buffer()
             self.grad_sync.execute(normalization_scale)
         ok, norm, zeros = self.optimizer.step()

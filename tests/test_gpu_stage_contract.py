@@ -271,3 +271,25 @@ def test_trainer_evidence_snapshot_and_runtime_record(cuda, tmp_path):
         assert r["optimizer_parameter"].dtype == torch.float32
         assert r["optimizer_state"]["step"].item() == 1.0
         assert set(r["optimizer_hyperparameters"]) == {"beta1", "beta2", "epsilon", "weight_decay"}
+
+
+def test_update_overlapped_with_the_next_forward_is_bit_identical(cuda):
+    """AdamW on a side stream, one launch per layer, each layer's next
+    forward waiting only for its own weights: three steps give the outputs,
+    input gradients, norms and parameters of the in-line update bit for
+    bit."""
+    announce("optimizer update overlapped with the next forward")
+    gen = torch.Generator().manual_seed(12)
+    plain = MiddleStageTrainer(_cfg(layers=3))
+    over = MiddleStageTrainer(_cfg(layers=3), overlap_optimizer=True)
+    _randomize(plain, gen)
+    _copy_weights(plain, over)
+    steps = [_inputs(gen) for _ in range(3)]
+    for x, dy in steps:
+        out_p, dx_p, ok_p, n_p = plain.train_step(x, dy)
+        out_o, dx_o, ok_o, n_o = over.train_step(x, dy)
+        assert ok_p and ok_o and n_p == n_o
+        assert torch.equal(out_p, out_o) and torch.equal(dx_p, dx_o)
+    torch.cuda.synchronize()
+    for (n1, p1), (n2, p2) in zip(plain.model.named_parameters(), over.model.named_parameters()):
+        assert torch.equal(p1, p2), n1
