@@ -350,6 +350,18 @@ def hbm_path(torch, iters=10):
     out["adam_frac"] = out["adam_gbps"] / PEAK_HBM_GBPS
     del ex, st, opt, params, model, buf, grads
     torch.cuda.empty_cache()
+    # the practical ceiling of mixed read/write traffic on this box: a 1 GiB
+    # device-to-device copy (1 GiB read + 1 GiB written), same timing method
+    src = torch.empty(1 << 28, dtype=torch.float32, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    t_copy = timed(lambda: dst.copy_(src))
+    out["copy_ms"] = t_copy
+    out["copy_gbps"] = 2.0 * src.numel() * 4 / t_copy / 1e6
+    out["copy_frac"] = out["copy_gbps"] / PEAK_HBM_GBPS
+    out["adam_over_copy"] = out["adam_gbps"] / out["copy_gbps"]
+    out["grad_sync_over_copy"] = out["grad_sync_gbps"] / out["copy_gbps"]
+    del src, dst
+    torch.cuda.empty_cache()
     return out
 
 

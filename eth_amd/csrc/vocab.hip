@@ -272,6 +272,16 @@ __global__ void tied_sum_kernel(float* __restrict__ a, float* __restrict__ b, in
   }
 }
 
+// the same over 16-bit gradients: the sum is formed in fp32 and rounded
+// once to the gradient dtype (a two-rank sum all-reduce in that dtype)
+__global__ void tied_sum_half_kernel(uint16_t* __restrict__ a, uint16_t* __restrict__ b, int64_t n, int dtype) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const float v = load_elem(a, i, dtype) + load_elem(b, i, dtype);
+    store_elem(a, i, dtype, v);
+    store_elem(b, i, dtype, v);
+  }
+}
+
 }  // namespace eth
 
 using namespace eth;
@@ -286,6 +296,17 @@ extern "C" int eth_tied_grad_sum(float* root, float* copy, int64_t n, void* stre
   if (blocks < 1) blocks = 1;
   tied_sum_kernel<<<(int)blocks, 256, 0, (hipStream_t)stream>>>(root, copy, n);
   ETH_CHECK_LAUNCH("eth_tied_grad_sum");
+  return ETH_OK;
+}
+
+extern "C" int eth_tied_grad_sum_half(void* root, void* copy, int64_t n, int dtype, void* stream) {
+  ETH_CHECK_ARG(dtype == ETH_BF16 || dtype == ETH_F16, "eth_tied_grad_sum_half: dtype must be bf16/fp16");
+  ETH_CHECK_ARG(n >= 0 && (n == 0 || (root && copy)), "eth_tied_grad_sum_half: bad arguments");
+  if (n == 0) return ETH_OK;
+  int64_t blocks = (n + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  tied_sum_half_kernel<<<(int)blocks, 256, 0, (hipStream_t)stream>>>((uint16_t*)root, (uint16_t*)copy, n, dtype);
+  ETH_CHECK_LAUNCH("eth_tied_grad_sum_half");
   return ETH_OK;
 }
 

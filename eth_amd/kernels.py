@@ -428,9 +428,15 @@ def xent_bwd(logits2d, labels, lse, dloss):
 
 
 def tied_grad_sum(root, copy):
-    """root = copy = root + copy (fp32 main grads of a tied weight)."""
-    if root.dtype != torch.float32 or copy.dtype != torch.float32 or root.shape != copy.shape:
-        raise ValueError("tied gradients must be fp32 tensors of one shape")
+    """root = copy = root + copy (main grads of a tied weight: fp32, or 16-bit
+    with the sum rounded once to their dtype)."""
+    if root.dtype != copy.dtype or root.shape != copy.shape:
+        raise ValueError("tied gradients must be tensors of one dtype and shape")
     if not (root.is_contiguous() and copy.is_contiguous()):
         raise ValueError("tied gradients must be contiguous")
-    nat.call("eth_tied_grad_sum", nat.ptr(root), nat.ptr(copy), root.numel(), nat.stream_ptr(root.device))
+    if root.dtype == torch.float32:
+        nat.call("eth_tied_grad_sum", nat.ptr(root), nat.ptr(copy), root.numel(), nat.stream_ptr(root.device))
+    else:
+        code = _check_half(root, copy)
+        nat.call("eth_tied_grad_sum_half", nat.ptr(root), nat.ptr(copy), root.numel(), code,
+                 nat.stream_ptr(root.device))

@@ -1,12 +1,15 @@
 """autograd Functions over the HIP kernels.
 
 Weight and bias gradients follow the Megatron local-DDP contract
-(eth/runtime/megatron/model/distributed.py:116-123): when a parameter has a
-`main_grad` (fp32) buffer, its gradient is accumulated straight into it by
+(eth/runtime/megatron/model/distributed.py:116-123): when a parameter has an
+fp32 `main_grad` buffer, its gradient is accumulated straight into it by
 the kernel (the wgrad GEMM adds into main_grad; bias / LayerNorm gradients
 are reduced in fp32 and added), and the autograd gradient returned for the
-parameter is None, so `param.grad` stays None.  Without `main_grad` the
-gradient is returned in the parameter's dtype.
+parameter is None, so `param.grad` stays None.  Without `main_grad`, or with
+a 16-bit one (fp16 training without fp32 accumulation, the reference's
+default), the gradient is returned in the parameter's dtype -- rounded once
+from its fp32 reduction -- and the DDP hook adds it into main_grad, a second
+rounding, as the reference's `main_grad.add_(param.grad)` does.
 """
 
 import torch
@@ -39,10 +42,11 @@ class overlapped_wgrad:
 def _fp32_accum_target(param):
     """(main_grad, accumulate): the fp32 buffer the kernel writes param's
     gradient into, and whether it adds (False for the first contribution
-    after a deferred zero_grad_buffer(), when it stores)."""
+    after a deferred zero_grad_buffer(), when it stores).  (None, False) when
+    param has no fp32 main_grad: the gradient is then returned."""
     mg = getattr(param, "main_grad", None)
-    if mg is not None and mg.dtype != torch.float32:
-        raise ValueError("main_grad must be fp32 for the fused accumulation")
+    if mg is None or mg.dtype != torch.float32:
+        return None, False
     return main_grad_target(param)
 
 
@@ -54,10 +58,8 @@ def _pair_target(p1, p2):
     left as they were)."""
     for p in (p1, p2):
         mg = getattr(p, "main_grad", None)
-        if mg is None:
+        if mg is None or mg.dtype != torch.float32:
             return None, None, False
-        if mg.dtype != torch.float32:
-            raise ValueError("main_grad must be fp32 for the fused accumulation")
     s1 = getattr(p1, "_eth_main_grad_stale", False)
     s2 = getattr(p2, "_eth_main_grad_stale", False)
     if s1 and s2:
@@ -105,9 +107,8 @@ class LinearFn(torch.autograd.Function):
                 K.gemm(dy2.t(), x2, out=mg, accumulate=accumulate)
                 grad_written(weight)
             else:
-                acc = torch.empty(weight.shape, dtype=torch.float32, device=weight.device)
-                K.gemm(dy2.t(), x2, out=acc)
-                dw = acc.to(weight.dtype)
+                # one rounding of the fp32 product to the parameter dtype
+                dw = K.gemm(dy2.t(), x2, out_dtype=weight.dtype)
         if bias is not None and ctx.needs_input_grad[2]:
             mg, accumulate = _fp32_accum_target(bias)
             if mg is not None:
@@ -314,11 +315,13 @@ class EmbeddingFn(torch.autograd.Function):
     def backward(ctx, dout):
         tokens, positions, word, pos = ctx.saved_tensors
         # the scatter-add needs real values underneath: stale buffers are
-        # zeroed first
-        for p in (word, pos):
-            if getattr(p, "main_grad", None) is not None and p.main_grad.dtype != torch.float32:
-                raise ValueError("main_grad must be fp32 for the fused accumulation")
-        mw, mp = materialize_main_grad(word), materialize_main_grad(pos)
+        # zeroed first; 16-bit main grads receive the returned gradient
+        # through the DDP hook
+        def fp32_target(p):
+            mg = getattr(p, "main_grad", None)
+            return materialize_main_grad(p) if mg is not None and mg.dtype == torch.float32 else None
+
+        mw, mp = fp32_target(word), fp32_target(pos)
         gw = mw if mw is not None else torch.zeros(word.shape, dtype=torch.float32, device=word.device)
         gp = mp if mp is not None else torch.zeros(pos.shape, dtype=torch.float32, device=pos.device)
         K.embedding_bwd(tokens, positions, dout.contiguous(), gw, gp)

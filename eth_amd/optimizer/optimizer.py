@@ -330,6 +330,7 @@ class Float16OptimizerWithFloat16Params(MegatronOptimizer):
         super().__init__(optimizer, clip_grad, log_num_zeros_in_grad, params_have_main_grad)
         self.bf16 = bf16
         self.grad_scaler = grad_scaler
+        self._f32_grads = {}
         self.use_contiguous_buffers_in_ddp = use_contiguous_buffers_in_ddp
         model_dtypes = {p.dtype for p in half}
         if len(model_dtypes) > 1:
@@ -347,11 +348,34 @@ class Float16OptimizerWithFloat16Params(MegatronOptimizer):
             out.extend(getattr(p, "main_grad", None) for p in group)
         return out
 
+    def _fp32_grad_view(self, main_param):
+        """The persistent fp32 gradient of a master whose main_grad is 16-bit
+        (one flat buffer, carved in master order on first use), so the
+        statistics and AdamW tables keyed by gradient addresses stay valid
+        across steps."""
+        view = self._f32_grads.get(id(main_param))
+        if view is None:
+            masters = [m for g in self.fp32_from_float16_groups for m in g]
+            sizes = [(m.numel() + 3) // 4 * 4 for m in masters]  # 16-byte aligned views
+            flat = torch.empty(sum(sizes), dtype=torch.float32, device=masters[0].device)
+            off = 0
+            for m, n in zip(masters, sizes):
+                self._f32_grads[id(m)] = flat[off : off + m.numel()].view(m.shape)
+                off += n
+            view = self._f32_grads[id(main_param)]
+        return view
+
     def _copy_model_grads_to_main_grads(self):
         for mg, fg in zip(self.float16_groups, self.fp32_from_float16_groups):
             for model_param, main_param in zip(mg, fg):
                 if self.params_have_main_grad:
-                    main_param.grad = model_param.main_grad.float()
+                    g = model_param.main_grad
+                    if g.dtype == torch.float32:
+                        main_param.grad = g
+                    else:
+                        # main_grad.float() (optimizer.py:392-397) into a
+                        # persistent buffer: an exact widening copy
+                        main_param.grad = self._fp32_grad_view(main_param).copy_(g)
                 elif model_param.grad is not None:
                     main_param.grad = model_param.grad.float()
                 model_param.grad = None

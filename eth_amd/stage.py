@@ -57,6 +57,17 @@ def save_stage_snapshot(trainer, output_dir, phase, iteration, metrics=None, clo
     )
 
 
+def _fp32_main_grads(cfg, requested):
+    """Whether main grads accumulate (and buckets travel) in fp32: always
+    for bf16, as the reference forces (arguments.py:267-276); for fp16 as
+    requested.  The trainers default to True for fp16 too -- the weight-
+    gradient GEMM then adds straight into fp32, more accurate than the
+    reference's default fp16 main grads -- and False gives the reference's
+    default fp16 contract: fp16 main grads and bucket payloads, widened to
+    fp32 by the optimizer before unscaling (optimizer.py:388-404)."""
+    return True if cfg.params_dtype == torch.bfloat16 else bool(requested)
+
+
 class MiddleStageTrainer:
     """A middle pipeline stage (no embedding, no head): whole layers
     `[first_layer, first_layer + num_layers)`, or any manifest op range
@@ -79,18 +90,17 @@ class MiddleStageTrainer:
         recompute_ops=None,
         runtime_evidence_dir=None,
         overlap_optimizer=False,
+        accumulate_allreduce_grads_in_fp32=True,
     ):
         if cfg.params_dtype not in (torch.bfloat16, torch.float16):
             raise ValueError("the stage trains in bf16 or fp16")
+        fp32_grads = _fp32_main_grads(cfg, accumulate_allreduce_grads_in_fp32)
         self.cfg = cfg
         if op_range is not None:
             self.model = op_range_stage(cfg, *op_range, recompute_ops=recompute_ops)
         else:
             self.model = middle_stage(cfg, first_layer, num_layers, recompute_ops=recompute_ops)
-        # main grads accumulate in fp32 for bf16 (as the reference forces) and
-        # for fp16 too: the wgrad GEMM adds into fp32, which is strictly more
-        # accurate than the reference's fp16 main_grad + later fp32 copy
-        self.ddp = DistributedDataParallel(self.model, accumulate_allreduce_grads_in_fp32=True)
+        self.ddp = DistributedDataParallel(self.model, accumulate_allreduce_grads_in_fp32=fp32_grads)
         lm = self.model.language_model
         self.descriptors, self.bindings = collect_stage_metadata(lm.ops, self.model.op_start, self.model.op_end)
         self.grad_sync = initialize_gradient_sync(
@@ -113,7 +123,9 @@ class MiddleStageTrainer:
             bf16=cfg.params_dtype == torch.bfloat16,
             fp16=cfg.params_dtype == torch.float16,
         )
-        self.optimizer.bind_gradient_sync(self.grad_sync.executor)
+        if fp32_grads:
+            # 16-bit main grads are widened and unscaled by the optimizer
+            self.optimizer.bind_gradient_sync(self.grad_sync.executor)
         if overlap_optimizer:
             # the update of layer l overlaps the next step's forward of the
             # layers before it (one AdamW launch per layer, in forward order)
@@ -279,7 +291,7 @@ class FirstLastStageTrainer:
 
     def __init__(self, cfg: GPTConfig, lr=1e-4, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01, clip_grad=1.0,
                  sync_mode="block", bucket_cap_bytes=1024 * 1024, initial_loss_scale=2.0**16, unpadded_vocab=50257,
-                 recompute_ops=None, runtime_evidence_dir=None):
+                 recompute_ops=None, runtime_evidence_dir=None, accumulate_allreduce_grads_in_fp32=True):
         self.cfg = cfg
         self.unpadded_vocab = unpadded_vocab
         n_ops = 10 * cfg.num_layers + 3
@@ -288,7 +300,8 @@ class FirstLastStageTrainer:
         self.embedding, self.post = ops[0], ops[-1]
         with torch.no_grad():  # the head copy starts from the root (training.py:349-470)
             self.post.word_embeddings.weight.copy_(self.embedding.word_embeddings.weight)
-        self.ddp = DistributedDataParallel(self.model, accumulate_allreduce_grads_in_fp32=True)
+        self.ddp = DistributedDataParallel(
+            self.model, accumulate_allreduce_grads_in_fp32=_fp32_main_grads(cfg, accumulate_allreduce_grads_in_fp32))
         self.descriptors, self.bindings = collect_stage_metadata(ops, 0, n_ops)
         self.grad_sync = initialize_gradient_sync(self.descriptors, self.bindings, global_rank=0,
                                                   expected_pipeline_ids=(0,), sync_mode=sync_mode,

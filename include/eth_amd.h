@@ -319,6 +319,11 @@ int eth_xent_bwd(const void* logits, int64_t ld, const int64_t* labels, const fl
  * 16-byte aligned).  Replaces the same-rank branch of
  * synchronize_shared_weights_grads (eth/runtime/megatron/training.py:489-531). */
 int eth_tied_grad_sum(float* root, float* copy, int64_t n, void* stream);
+/* The same for 16-bit (bf16 / fp16, `dtype`) main grads, as fp16 training
+ * without fp32 gradient accumulation keeps them (the reference's default,
+ * eth/runtime/megatron/model/distributed.py:69-103): each sum is formed in
+ * fp32 and rounded once, as an all-reduce sum in that dtype rounds it. */
+int eth_tied_grad_sum_half(void* root, void* copy, int64_t n, int dtype, void* stream);
 
 #ifdef __cplusplus
 }

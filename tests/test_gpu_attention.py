@@ -32,7 +32,7 @@ def test_sdpa_oracle_matches_explicit_softmax():
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("s,b,n,d", [(128, 2, 2, 64), (256, 1, 3, 128), (384, 2, 1, 128)])
+@pytest.mark.parametrize("s,b,n,d", [(128, 2, 2, 64), (256, 1, 3, 128), (384, 2, 1, 128), (512, 2, 2, 64), (768, 1, 2, 128)])
 def test_attention_fwd_bwd_interleaved_qkv(cuda, dtype, s, b, n, d):
     announce(f"attention {dtype} s={s} b={b} n={n} d={d}")
     gen = torch.Generator().manual_seed(s + n + d)
