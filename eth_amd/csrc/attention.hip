@@ -1,5 +1,10 @@
 // Causal flash attention for the GPT block, forward and backward, on CDNA4
-// matrix cores (v_mfma_f32_32x32x16_{bf16,f16}), head_dim 64 or 128.
+// matrix cores (v_mfma_f32_32x32x16_{bf16,f16}).  Any head_dim that is a
+// multiple of 8 up to 128 runs on the 64-, 96- or 128-wide kernels with the
+// extra head-dim columns loaded as zeros and never stored; any sequence
+// length runs on whole 128-row blocks whose rows past the end load as zeros
+// (the causal mask already hides keys past every real query) and are never
+// stored.
 //
 // Semantics: O = softmax(Q K^T / sqrt(hn) + causal -inf) V per (batch, head),
 // i.e. F.scaled_dot_product_attention(q, k, v, is_causal=True) as called by
@@ -98,6 +103,7 @@ struct AttnArgs {
   float* lse;    // [B*H, S] log2-domain: m2 + log2(l)
   float* delta;  // [B*H, S] rowsum(dO * O)
   int B, H, S;
+  int hd;  // head dim (<= the kernel's D; columns hd..D-1 are zero padding)
   float scale_log2;  // log2(e) / sqrt(hn)
   float scale;       // 1 / sqrt(hn)
 };
@@ -108,6 +114,19 @@ constexpr int kBQ = 128;   // forward / dQ: queries per workgroup (4 waves x 32)
 constexpr int kBKV = 64;   // forward / dQ: keys per step
 constexpr int kBKV2 = 128; // dK/dV: keys per workgroup (4 waves x 32)
 constexpr int kBQ2 = 64;   // dK/dV: queries per step
+constexpr int32_t kAttnOob = (int32_t)0x80000000u;  // buffer offset past any tensor: loads read zeros
+// row length (elements) of an LDS tile read with ds_read_b64_tr_b16: four
+// consecutive rows then start 64 bytes apart in the bank space
+constexpr int tr_row(int d) { return d % 64 == 0 ? d + 32 : d + 64; }
+// 16 bytes of a row at column `col` of a strided tensor; with PAD, zeros
+// past the sequence or the head dim (without, every row and column is real)
+template <bool PAD>
+__device__ __forceinline__ uint4 load_row16(const uint16_t* row, bool in_seq, int col, int hd) {
+  if constexpr (PAD)
+    return in_seq && col < hd ? *reinterpret_cast<const uint4*>(row + col) : make_uint4(0u, 0u, 0u, 0u);
+  else
+    return *reinterpret_cast<const uint4*>(row + col);
+}
 
 __device__ __forceinline__ const uint16_t* row_ptr(const AttnTensor& t, int s, int b, int h) {
   return t.p + (int64_t)s * t.ss + (int64_t)b * t.sb + (int64_t)h * t.sh;
@@ -121,7 +140,7 @@ __device__ __forceinline__ uint16_t* row_ptr(const AttnOut& t, int s, int b, int
 // scalar offset, so a load costs no address arithmetic.  Stored into LDS
 // rows of LROW elements, row index optionally swizzled (SWZ).
 typedef __amdgpu_buffer_rsrc_t a_rsrc_t;
-template <int ROWS, int D, int LROW, bool SWZ>
+template <int ROWS, int D, int LROW, bool SWZ, bool PAD>
 struct BufTile {
   static constexpr int CPR = D / 8;
   static constexpr int CPT = ROWS * CPR / kAttnThreads;
@@ -130,18 +149,27 @@ struct BufTile {
   int32_t voff[CPT];
   a_rsrc_t rs;
   int32_t row_bytes;
-  __device__ __forceinline__ void init(const AttnTensor& t, int b, int h) {
+  int rows_left;  // tensor rows (sequence length); rows past it load zeros
+  // columns at or past hd load zeros (an out-of-range offset)
+  __device__ __forceinline__ void init(const AttnTensor& t, int b, int h, int seq, int hd) {
     rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(t.p), (short)0, (int)t.bytes, 0x00020000);
     row_bytes = (int32_t)(t.ss * 2);
+    rows_left = seq;
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
       const int c = threadIdx.x + i * kAttnThreads;
-      voff[i] = (int32_t)(((int64_t)b * t.sb + (int64_t)h * t.sh + (int64_t)(c / CPR) * t.ss + (c % CPR) * 8) * 2);
+      voff[i] = !PAD || (c % CPR) * 8 < hd
+                    ? (int32_t)(((int64_t)b * t.sb + (int64_t)h * t.sh + (int64_t)(c / CPR) * t.ss + (c % CPR) * 8) * 2)
+                    : kAttnOob;
     }
   }
   __device__ __forceinline__ void load(int r0) {
 #pragma unroll
-    for (int i = 0; i < CPT; ++i) v[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff[i], r0 * row_bytes, 0);
+    for (int i = 0; i < CPT; ++i) {
+      const int c = threadIdx.x + i * kAttnThreads;
+      const int32_t off = !PAD || r0 + c / CPR < rows_left ? voff[i] : kAttnOob;
+      v[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, off, r0 * row_bytes, 0);
+    }
   }
   __device__ __forceinline__ void store(uint16_t* lds) const {
 #pragma unroll
@@ -182,17 +210,17 @@ __device__ __forceinline__ uint4 tr_frag(const uint16_t* p, int lrow) {
 // 4 waves x 32 queries; K/V blocks of 64 keys double-buffered in LDS (the
 // next block's global loads are in flight while this one is computed); two
 // workgroups per CU, so one wave's softmax overlaps the other's MFMAs.
-template <int D, bool FP16>
+template <int D, bool FP16, bool PAD>
 __global__ void __launch_bounds__(kAttnThreads, 2) attn_fwd_kernel(AttnArgs a) {
   constexpr int KS = D / 16;  // k-steps over the head dim
   constexpr int DT = D / 32;  // 32-row tiles over the head dim
   // K rows swizzled (see the file comment); V rows as they are, padded to
   // D + 32 so the transposing reads of O^T = V^T P^T hit distinct banks
-  constexpr int VL = D + 32;
+  constexpr int VL = tr_row(D);
   __shared__ __attribute__((aligned(16))) uint16_t Ks[2][kBKV * (D + 8)];
   __shared__ __attribute__((aligned(16))) uint16_t Vs[2][kBKV * VL];
 
-  const int BH = a.B * a.H, nqb = a.S / kBQ;
+  const int BH = a.B * a.H, nqb = (a.S + kBQ - 1) / kBQ;
   const int bh = blockIdx.x % BH, qb = nqb - 1 - blockIdx.x / BH;
   const int b = bh / a.H, h = bh % a.H;
   const int lane = threadIdx.x & 63, hl = lane >> 5;
@@ -203,9 +231,9 @@ __global__ void __launch_bounds__(kAttnThreads, 2) attn_fwd_kernel(AttnArgs a) {
 
   uint4 qf[KS];
   {
-    const uint16_t* qp = row_ptr(a.q, q, b, h) + hl * 8;
+    const uint16_t* qp = row_ptr(a.q, q, b, h);
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) qf[ks] = *reinterpret_cast<const uint4*>(qp + ks * 16);
+    for (int ks = 0; ks < KS; ++ks) qf[ks] = load_row16<PAD>(qp, q < a.S, ks * 16 + hl * 8, a.hd);
   }
   a_f32x16 o[DT];
 #pragma unroll
@@ -215,10 +243,10 @@ __global__ void __launch_bounds__(kAttnThreads, 2) attn_fwd_kernel(AttnArgs a) {
   float m = -1e30f, l = 0.f;  // running max (log2 units) and sum for query q
 
   const int nkv = (qb * kBQ + kBQ) / kBKV;  // blocks up to the diagonal
-  BufTile<kBKV, D, D + 8, true> kt;
-  BufTile<kBKV, D, VL, false> vt;
-  kt.init(a.k, b, h);
-  vt.init(a.v, b, h);
+  BufTile<kBKV, D, D + 8, true, PAD> kt;
+  BufTile<kBKV, D, VL, false, PAD> vt;
+  kt.init(a.k, b, h, a.S, a.hd);
+  vt.init(a.v, b, h, a.S, a.hd);
   kt.load(0);
   vt.load(0);
   kt.store(Ks[0]);
@@ -307,12 +335,14 @@ __global__ void __launch_bounds__(kAttnThreads, 2) attn_fwd_kernel(AttnArgs a) {
     __syncthreads();
   }
   l += __shfl_xor(l, 32, 64);
+  if (PAD && q >= a.S) return;  // a padding row of the last query block
   const float inv = 1.0f / l;
   uint16_t* op = row_ptr(a.out, q, b, h);
 #pragma unroll
   for (int t = 0; t < DT; ++t)
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
+      if (PAD && t * 32 + g * 8 >= a.hd) continue;  // hd % 8 == 0: whole 8-column groups
       uint2 v;
       v.x = pack2<FP16>(o[t][g * 4 + 0] * inv, o[t][g * 4 + 1] * inv);
       v.y = pack2<FP16>(o[t][g * 4 + 2] * inv, o[t][g * 4 + 3] * inv);
@@ -325,14 +355,14 @@ __global__ void __launch_bounds__(kAttnThreads, 2) attn_fwd_kernel(AttnArgs a) {
 // PART 1: dV only, 2: dK only, 3: both.  Split, each part fits two
 // workgroups per CU (the fused kernel needs K, V fragments and both
 // accumulators live and runs one); splitting recomputes S once more.
-template <int D, bool FP16, int PART>
+template <int D, bool FP16, int PART, bool PAD>
 __global__ void __launch_bounds__(kAttnThreads, PART == 3 ? 1 : 2) attn_bwd_dkdv_kernel(AttnArgs a) {
   constexpr int KS = D / 16, DT = D / 32;
   constexpr bool DV = PART & 1, DK = PART & 2;
   // Q (and dO) rows swizzled for S (and dP); the B operands of dV += P^T dO
   // and dK += dS^T Q come from natural-order copies padded to D + 32
   // through transposing reads
-  constexpr int QN = D + 32;
+  constexpr int QN = tr_row(D);
   __shared__ __attribute__((aligned(16))) uint16_t Qs[kBQ2 * (D + 8)];
   __shared__ __attribute__((aligned(16))) uint16_t dOs[DK ? kBQ2 * (D + 8) : 8];
   __shared__ __attribute__((aligned(16))) uint16_t Qn[DK ? kBQ2 * QN : 8];
@@ -349,12 +379,12 @@ __global__ void __launch_bounds__(kAttnThreads, PART == 3 ? 1 : 2) attn_bwd_dkdv
 
   uint4 kf[KS], vf[KS];
   {
-    const uint16_t* kp = row_ptr(a.k, key, b, h) + hl * 8;
-    const uint16_t* vp = row_ptr(a.v, key, b, h) + hl * 8;
+    const uint16_t* kp = row_ptr(a.k, key, b, h);
+    const uint16_t* vp = row_ptr(a.v, key, b, h);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      kf[ks] = *reinterpret_cast<const uint4*>(kp + ks * 16);
-      if constexpr (DK) vf[ks] = *reinterpret_cast<const uint4*>(vp + ks * 16);
+      kf[ks] = load_row16<PAD>(kp, key < a.S, ks * 16 + hl * 8, a.hd);
+      if constexpr (DK) vf[ks] = load_row16<PAD>(vp, key < a.S, ks * 16 + hl * 8, a.hd);
     }
   }
   a_f32x16 dk[DT], dv[DT];
@@ -363,18 +393,19 @@ __global__ void __launch_bounds__(kAttnThreads, PART == 3 ? 1 : 2) attn_bwd_dkdv
 #pragma unroll
     for (int r = 0; r < 16; ++r) dk[t][r] = dv[t][r] = 0.f;
 
-  BufTile<kBQ2, D, D + 8, true> qt, dt;
-  qt.init(a.q, b, h);
-  dt.init(a.dout, b, h);
+  BufTile<kBQ2, D, D + 8, true, PAD> qt, dt;
+  qt.init(a.q, b, h, a.S, a.hd);
+  dt.init(a.dout, b, h, a.S, a.hd);
   const int qtr = tr_lane(lane, QN);
-  const int first = (kb * kBKV2) / kBQ2, nq = a.S / kBQ2;
+  const int first = (kb * kBKV2) / kBQ2, nq = (a.S + kBQ2 - 1) / kBQ2;
   // the next step's Q / dO rows, and its queries' lse and delta, are loaded
-  // while this step computes
+  // while this step computes; a padding query gets lse = 1e30, so P = 0
   float lse_n = 0.f, del_n = 0.f;
   auto load_stats = [&](int qs) __attribute__((always_inline)) {
     if (threadIdx.x < kBQ2) {
-      lse_n = a.lse[(int64_t)bh * a.S + qs + threadIdx.x];
-      if constexpr (DK) del_n = a.delta[(int64_t)bh * a.S + qs + threadIdx.x];
+      const bool real = !PAD || qs + (int)threadIdx.x < a.S;
+      lse_n = real ? a.lse[(int64_t)bh * a.S + qs + threadIdx.x] : 1e30f;
+      if constexpr (DK) del_n = real ? a.delta[(int64_t)bh * a.S + qs + threadIdx.x] : 0.f;
     }
   };
   qt.load(first * kBQ2);
@@ -460,23 +491,24 @@ __global__ void __launch_bounds__(kAttnThreads, PART == 3 ? 1 : 2) attn_bwd_dkdv
     for (int r = 0; r < 16; ++r) {
       const int kr = k0 + acc_row(r, hl);
       const int d = t * 32 + (lane & 31);
+      if (PAD && (kr >= a.S || d >= a.hd)) continue;
       if constexpr (DK) row_ptr(a.dk, kr, b, h)[d] = from_f<FP16>(dk[t][r] * a.scale);
       if constexpr (DV) row_ptr(a.dv, kr, b, h)[d] = from_f<FP16>(dv[t][r]);
     }
 }
 
 // ------------------------------------------------------------ backward: dQ --
-template <int D, bool FP16>
+template <int D, bool FP16, bool PAD>
 __global__ void __launch_bounds__(kAttnThreads, 2) attn_bwd_dq_kernel(AttnArgs a) {
   constexpr int KS = D / 16, DT = D / 32;
   // K and V rows swizzled for S^T and dP^T; K also in natural order, padded
   // to D + 32, for the transposing reads of dQ^T = K^T dS^T
-  constexpr int KN = D + 32;
+  constexpr int KN = tr_row(D);
   __shared__ __attribute__((aligned(16))) uint16_t Ks[kBKV * (D + 8)];
   __shared__ __attribute__((aligned(16))) uint16_t Vs[kBKV * (D + 8)];
   __shared__ __attribute__((aligned(16))) uint16_t Kn[kBKV * KN];
 
-  const int BH = a.B * a.H, nqb = a.S / kBQ;
+  const int BH = a.B * a.H, nqb = (a.S + kBQ - 1) / kBQ;
   const int bh = blockIdx.x % BH, qb = nqb - 1 - blockIdx.x / BH;
   const int b = bh / a.H, h = bh % a.H;
   const int lane = threadIdx.x & 63, hl = lane >> 5;
@@ -484,26 +516,27 @@ __global__ void __launch_bounds__(kAttnThreads, 2) attn_bwd_dq_kernel(AttnArgs a
   const int q0 = qb * kBQ + w * 32;
   const int q = q0 + (lane & 31);
 
+  const bool real = !PAD || q < a.S;  // false on padding rows of the last block
   uint4 qf[KS], of[KS];
   {
-    const uint16_t* qp = row_ptr(a.q, q, b, h) + hl * 8;
-    const uint16_t* op = row_ptr(a.dout, q, b, h) + hl * 8;
+    const uint16_t* qp = row_ptr(a.q, q, b, h);
+    const uint16_t* op = row_ptr(a.dout, q, b, h);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      qf[ks] = *reinterpret_cast<const uint4*>(qp + ks * 16);
-      of[ks] = *reinterpret_cast<const uint4*>(op + ks * 16);
+      qf[ks] = load_row16<PAD>(qp, real, ks * 16 + hl * 8, a.hd);
+      of[ks] = load_row16<PAD>(op, real, ks * 16 + hl * 8, a.hd);
     }
   }
-  const float lse = a.lse[(int64_t)bh * a.S + q];
+  const float lse = real ? a.lse[(int64_t)bh * a.S + q] : 1e30f;
   // delta = rowsum(dO * O) for this query, from the dO fragments already in
   // registers (the two half-waves hold alternate 8-element chunks of the row);
   // written out for the dK/dV kernel, which runs next
   float del = 0.f;
   {
-    const uint16_t* opp = row_ptr(a.o, q, b, h) + hl * 8;
+    const uint16_t* opp = row_ptr(a.o, q, b, h);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      const uint4 ov = *reinterpret_cast<const uint4*>(opp + ks * 16);
+      const uint4 ov = load_row16<PAD>(opp, real, ks * 16 + hl * 8, a.hd);
       const uint32_t ow[4] = {ov.x, ov.y, ov.z, ov.w};
       const uint32_t dw[4] = {of[ks].x, of[ks].y, of[ks].z, of[ks].w};
 #pragma unroll
@@ -513,7 +546,7 @@ __global__ void __launch_bounds__(kAttnThreads, 2) attn_bwd_dq_kernel(AttnArgs a
       }
     }
     del += __shfl_xor(del, 32, 64);
-    if (hl == 0) a.delta[(int64_t)bh * a.S + q] = del;
+    if (hl == 0 && real) a.delta[(int64_t)bh * a.S + q] = del;
   }
   a_f32x16 dq[DT];
 #pragma unroll
@@ -521,9 +554,9 @@ __global__ void __launch_bounds__(kAttnThreads, 2) attn_bwd_dq_kernel(AttnArgs a
 #pragma unroll
     for (int r = 0; r < 16; ++r) dq[t][r] = 0.f;
 
-  BufTile<kBKV, D, D + 8, true> kt, vt;
-  kt.init(a.k, b, h);
-  vt.init(a.v, b, h);
+  BufTile<kBKV, D, D + 8, true, PAD> kt, vt;
+  kt.init(a.k, b, h, a.S, a.hd);
+  vt.init(a.v, b, h, a.S, a.hd);
   const int ktr = tr_lane(lane, KN);
   const int nkv = (qb * kBQ + kBQ) / kBKV;
   // the next block's K / V rows are loaded while this block computes
@@ -580,11 +613,13 @@ __global__ void __launch_bounds__(kAttnThreads, 2) attn_bwd_dq_kernel(AttnArgs a
       }
     }
   }
+  if (PAD && !real) return;
   uint16_t* dqp = row_ptr(a.dq, q, b, h);
 #pragma unroll
   for (int t = 0; t < DT; ++t)
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
+      if (PAD && t * 32 + g * 8 >= a.hd) continue;
       uint2 v;
       v.x = pack2<FP16>(dq[t][g * 4 + 0] * a.scale, dq[t][g * 4 + 1] * a.scale);
       v.y = pack2<FP16>(dq[t][g * 4 + 2] * a.scale, dq[t][g * 4 + 3] * a.scale);
@@ -599,10 +634,9 @@ using namespace eth;
 static int attn_check(const eth_attn_desc_t* d) {
   ETH_CHECK_ARG(d, "attention: null descriptor");
   ETH_CHECK_ARG(d->dtype == ETH_BF16 || d->dtype == ETH_F16, "attention: dtype must be bf16/fp16");
-  ETH_CHECK_ARG(d->head_dim == 64 || d->head_dim == 128, "attention: head_dim must be 64 or 128 (got %d)",
-                d->head_dim);
-  ETH_CHECK_ARG(d->seq > 0 && d->seq % 128 == 0, "attention: seq must be a positive multiple of 128 (got %d)",
-                d->seq);
+  ETH_CHECK_ARG(d->head_dim >= 8 && d->head_dim <= 128 && d->head_dim % 8 == 0,
+                "attention: head_dim must be a multiple of 8 in [8, 128] (got %d)", d->head_dim);
+  ETH_CHECK_ARG(d->seq > 0, "attention: seq must be positive (got %d)", d->seq);
   ETH_CHECK_ARG(d->batch > 0 && d->heads > 0, "attention: bad batch/heads");
   return ETH_OK;
 }
@@ -648,18 +682,31 @@ extern "C" int eth_attn_fwd(const eth_attn_desc_t* d, const void* q, const void*
   a.B = d->batch;
   a.H = d->heads;
   a.S = d->seq;
+  a.hd = d->head_dim;
   a.scale = 1.0f / sqrtf((float)d->head_dim);
   a.scale_log2 = a.scale * 1.4426950408889634f;
-  const int grid = a.B * a.H * (a.S / kBQ);
+  const int grid = a.B * a.H * ((a.S + kBQ - 1) / kBQ);
   hipStream_t s = (hipStream_t)stream;
   const bool fp16 = d->dtype == ETH_F16;
-  if (d->head_dim == 128) {
-    if (fp16) attn_fwd_kernel<128, true><<<grid, kAttnThreads, 0, s>>>(a);
-    else attn_fwd_kernel<128, false><<<grid, kAttnThreads, 0, s>>>(a);
-  } else {
-    if (fp16) attn_fwd_kernel<64, true><<<grid, kAttnThreads, 0, s>>>(a);
-    else attn_fwd_kernel<64, false><<<grid, kAttnThreads, 0, s>>>(a);
+  const int width = a.hd > 96 ? 128 : a.hd > 64 ? 96 : 64;
+  // full blocks (every row and head-dim column real) take the unguarded kernels
+  const bool pad = a.S % kBQ != 0 || a.hd != width;
+#define ETH_ATTN_FWD(D)                                                                \
+  if (pad) {                                                                           \
+    if (fp16) attn_fwd_kernel<D, true, true><<<grid, kAttnThreads, 0, s>>>(a);         \
+    else attn_fwd_kernel<D, false, true><<<grid, kAttnThreads, 0, s>>>(a);             \
+  } else {                                                                             \
+    if (fp16) attn_fwd_kernel<D, true, false><<<grid, kAttnThreads, 0, s>>>(a);        \
+    else attn_fwd_kernel<D, false, false><<<grid, kAttnThreads, 0, s>>>(a);            \
   }
+  if (a.hd > 96) {
+    ETH_ATTN_FWD(128)
+  } else if (a.hd > 64) {
+    ETH_ATTN_FWD(96)
+  } else {
+    ETH_ATTN_FWD(64)
+  }
+#undef ETH_ATTN_FWD
   ETH_CHECK_LAUNCH("eth_attn_fwd");
   return ETH_OK;
 }
@@ -690,23 +737,36 @@ extern "C" int eth_attn_bwd(const eth_attn_desc_t* d, const void* q, const void*
   a.B = d->batch;
   a.H = d->heads;
   a.S = d->seq;
+  a.hd = d->head_dim;
   a.scale = 1.0f / sqrtf((float)d->head_dim);
   a.scale_log2 = a.scale * 1.4426950408889634f;
   hipStream_t s = (hipStream_t)stream;
   const bool fp16 = d->dtype == ETH_F16;
-  const int g_kv = a.B * a.H * (a.S / kBKV2);
-  const int g_q = a.B * a.H * (a.S / kBQ);
+  const int g_kv = a.B * a.H * ((a.S + kBKV2 - 1) / kBKV2);
+  const int g_q = a.B * a.H * ((a.S + kBQ - 1) / kBQ);
   // dQ first: it also writes delta = rowsum(dO * O), which dK/dV reads
-#define ETH_ATTN_BWD(D, F)                                                       \
-  attn_bwd_dq_kernel<D, F><<<g_q, kAttnThreads, 0, s>>>(a);                    \
-  attn_bwd_dkdv_kernel<D, F, 1><<<g_kv, kAttnThreads, 0, s>>>(a);              \
-  attn_bwd_dkdv_kernel<D, F, 2><<<g_kv, kAttnThreads, 0, s>>>(a);
-  if (d->head_dim == 128) {
+  const int width = a.hd > 96 ? 128 : a.hd > 64 ? 96 : 64;
+  static_assert(kBKV2 == kBQ, "one padding rule for the three backward kernels");
+  const bool pad = a.S % kBKV2 != 0 || a.hd != width;
+#define ETH_ATTN_BWD_P(D, F, P)                                                  \
+  attn_bwd_dq_kernel<D, F, P><<<g_q, kAttnThreads, 0, s>>>(a);                 \
+  attn_bwd_dkdv_kernel<D, F, 1, P><<<g_kv, kAttnThreads, 0, s>>>(a);           \
+  attn_bwd_dkdv_kernel<D, F, 2, P><<<g_kv, kAttnThreads, 0, s>>>(a);
+#define ETH_ATTN_BWD(D, F)        \
+  if (pad) {                      \
+    ETH_ATTN_BWD_P(D, F, true)    \
+  } else {                        \
+    ETH_ATTN_BWD_P(D, F, false)   \
+  }
+  if (a.hd > 96) {
     if (fp16) { ETH_ATTN_BWD(128, true) } else { ETH_ATTN_BWD(128, false) }
+  } else if (a.hd > 64) {
+    if (fp16) { ETH_ATTN_BWD(96, true) } else { ETH_ATTN_BWD(96, false) }
   } else {
     if (fp16) { ETH_ATTN_BWD(64, true) } else { ETH_ATTN_BWD(64, false) }
   }
 #undef ETH_ATTN_BWD
+#undef ETH_ATTN_BWD_P
   ETH_CHECK_LAUNCH("eth_attn_bwd");
   return ETH_OK;
 }

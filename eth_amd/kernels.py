@@ -315,8 +315,8 @@ def attention_fwd(q, k, v, out=None):
     if not (q.shape == k.shape == v.shape):
         raise ValueError("q, k, v shapes differ")
     s, b, n, d = q.shape
-    if d not in (64, 128) or s % 128:
-        raise ValueError("attention needs head_dim 64/128 and seq % 128 == 0")
+    if d % 8 or not 8 <= d <= 128 or s < 1:
+        raise ValueError(f"attention needs head_dim a multiple of 8 in [8, 128] and seq >= 1 (got {d}, {s})")
     if out is None:
         out = torch.empty(s, b, n * d, dtype=q.dtype, device=q.device)
     o4 = out.view(s, b, n, d)

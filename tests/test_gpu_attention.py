@@ -32,7 +32,11 @@ def test_sdpa_oracle_matches_explicit_softmax():
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("s,b,n,d", [(128, 2, 2, 64), (256, 1, 3, 128), (384, 2, 1, 128), (512, 2, 2, 64), (768, 1, 2, 128)])
+@pytest.mark.parametrize("s,b,n,d", [(128, 2, 2, 64), (256, 1, 3, 128), (384, 2, 1, 128), (512, 2, 2, 64),
+                                     (768, 1, 2, 128),
+                                     # ragged sequences and head dims on the padded kernels
+                                     (200, 2, 2, 80), (77, 1, 3, 64), (130, 1, 2, 128), (96, 2, 1, 96),
+                                     (300, 1, 2, 40), (64, 1, 1, 120)])
 def test_attention_fwd_bwd_interleaved_qkv(cuda, dtype, s, b, n, d):
     announce(f"attention {dtype} s={s} b={b} n={n} d={d}")
     gen = torch.Generator().manual_seed(s + n + d)
@@ -57,9 +61,9 @@ def test_attention_fwd_bwd_interleaved_qkv(cuda, dtype, s, b, n, d):
 
 
 def test_attention_rejects_unsupported_shapes(cuda):
-    x = torch.zeros(100, 1, 1, 64, dtype=torch.bfloat16, device=cuda)
+    x = torch.zeros(100, 1, 1, 100, dtype=torch.bfloat16, device=cuda)  # head_dim not a multiple of 8
     with pytest.raises(ValueError):
         K.attention_fwd(x, x, x)
-    y = torch.zeros(128, 1, 1, 96, dtype=torch.bfloat16, device=cuda)
+    y = torch.zeros(128, 1, 1, 136, dtype=torch.bfloat16, device=cuda)  # head_dim above 128
     with pytest.raises(ValueError):
         K.attention_fwd(y, y, y)

@@ -68,6 +68,14 @@ def test_middle_stage_matches_fp32_oracle(cuda, dtype):
     _stage_parity(cuda, dtype, hidden=256, heads=4, ffn=1024, layers=2, seq=128, mb=2, seed=5)
 
 
+def test_middle_stage_with_head_dim_80_and_a_ragged_sequence(cuda):
+    """The head width of the reference's "2_6B" profiler model (hidden 2560,
+    32 heads: 80, eth/profiler/model_configs.py:19) at a sequence that is not
+    a multiple of the attention block, on a narrower stage (4 heads of 80)."""
+    announce("middle stage parity, head_dim 80, seq 200")
+    _stage_parity(cuda, torch.bfloat16, hidden=320, heads=4, ffn=1280, layers=1, seq=200, mb=2, seed=6)
+
+
 def test_middle_stage_layer_at_bench_shape_matches_fp32_oracle(cuda):
     """One layer at the benchmarked shape (hidden 2048, 16 heads of 128,
     FFN 8192, seq 2048, micro-batch 4, bf16): the widths that select the
