@@ -129,6 +129,7 @@ class GradientBucketExecutor:
         }
         self._validate_local_contract()
         self._scratch = self._allocate_scratch()
+        self._norm_excluded = frozenset()
         self._tables = self._build_tables()
         self._statistics = None
         self._inv_scale = 1.0
@@ -255,7 +256,8 @@ class GradientBucketExecutor:
             for placement in bucket.placements:
                 fragment = self._fragments[placement.fragment_id]
                 binding = self._binding_specs[placement.fragment_id]
-                owned = fragment.include_in_optimizer_norm and fragment.norm_owner_rank == self.global_rank
+                owned = (fragment.include_in_optimizer_norm and fragment.norm_owner_rank == self.global_rank
+                         and binding.logical_param_id not in self._norm_excluded)
                 flags = nat.CHUNK_NORM if owned else 0
                 esize = self._runtime_bindings[binding.logical_param_id].main_grad.element_size()
                 dst = placement.destination_offset
@@ -287,6 +289,18 @@ class GradientBucketExecutor:
     def covered_gradients(self):
         """main_grad tensors this executor writes, by logical id."""
         return {lid: r.main_grad for lid, r in self._runtime_bindings.items()}
+
+    def exclude_from_norm(self, logical_param_ids):
+        """Leave these gradients out of the fused L2 partials (their partial
+        slots read 0): gradients that change after the sync, such as a tied
+        pair summed afterwards, get their statistics taken later."""
+        excluded = frozenset(logical_param_ids)
+        unknown = excluded - set(self._runtime_bindings)
+        if unknown:
+            raise ValueError(f"rank {self.global_rank} has no gradients for {sorted(unknown)}")
+        if excluded != self._norm_excluded:
+            self._norm_excluded = excluded
+            self._tables = self._build_tables()
 
     def bind_statistics(self, statistics):
         """Let execute() also unscale, flag inf/nan and collect L2 partials."""

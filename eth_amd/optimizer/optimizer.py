@@ -55,6 +55,7 @@ class MegatronOptimizer:
         self._model_to_optimizer_param = {}
         self._host_flags = None
         self._overlap = None  # (side stream, [[model params] per part]) when the update overlaps the next forward
+        self._post_sync = (None, 0)  # chunk table of norm-owned gradients summed after the sync
 
     # ----------------------------------------------------------- plumbing --
     @property
@@ -124,19 +125,52 @@ class MegatronOptimizer:
                     stream.wait_event(ev)
                     p._eth_ready_event = None
 
-    def bind_gradient_sync(self, executor):
+    def bind_gradient_sync(self, executor, resynced=()):
         """Fuse unscale / inf-nan flag / L2 partials into `executor`'s unpack.
 
         Only valid when every optimizer gradient is an fp32 main_grad the
-        executor writes (bf16 or fp32 training)."""
-        covered = {g.data_ptr() for g in executor.covered_gradients().values()}
+        executor writes (bf16 or fp32 training).  `resynced`: model
+        parameters whose main grads change after the sync (the tied word
+        embedding, summed by the stage afterwards).  The unpack still
+        unscales them -- the loss scale is a power of two, so unscaling each
+        addend first gives the bits of unscaling the sum -- but leaves them
+        out of the norm; the step then takes the norm-owned ones' sum of
+        squares and re-checks them for overflow in one pass."""
+        covered = executor.covered_gradients()
+        by_ptr = {g.data_ptr(): lid for lid, g in covered.items()}
         grads = self._bound_main_grads()
-        if any(g is None or g.dtype != torch.float32 or g.data_ptr() not in covered for g in grads):
+        if any(g is None or g.dtype != torch.float32 or g.data_ptr() not in by_ptr for g in grads):
             raise ValueError("fused gradient statistics need fp32 main grads written by the executor")
+        post = [p for p in resynced if self._norm_owned(p)]
+        if any(getattr(p, "main_grad", None) is None or p.main_grad.data_ptr() not in by_ptr for p in resynced):
+            raise ValueError("re-synced parameters must have main grads written by the executor")
+        executor.exclude_from_norm(by_ptr[p.main_grad.data_ptr()] for p in post)
+        entries = []
+        for p in post:
+            g = p.main_grad
+            split_block(g.data_ptr(), 4, 1, g.numel(), g.numel(), 0, 1.0, nat.CHUNK_NORM, entries)
+        table = chunk_table(entries)
+        self._post_sync = (nat.table_to_device(table, self._device()) if len(table) else None, len(table))
         self._executor = executor
-        self._statistics = GradientStatistics(executor.n_partials, self._device())
+        self._statistics = GradientStatistics(executor.n_partials + len(table), self._device())
         executor.bind_statistics(self._statistics)
         executor.set_inv_loss_scale(self._inv_scale())
+
+    def unbind_gradient_sync(self):
+        """Undo bind_gradient_sync: the sync only moves gradients again and
+        the step takes every statistic itself (one standalone pass)."""
+        if self._executor is not None:
+            self._executor.bind_statistics(None)
+            self._executor.exclude_from_norm(())
+        self._executor = None
+        self._statistics = None
+        self._post_sync = (None, 0)
+
+    @property
+    def grads_unscaled_by_sync(self):
+        """True when the gradient sync's unpack unscales the main grads (a
+        fused binding): after the sync they hold the unscaled gradients."""
+        return self._executor is not None
 
     def _bound_main_grads(self):
         raise NotImplementedError
@@ -209,6 +243,14 @@ class MegatronOptimizer:
             raise RuntimeError("loss scale changed between gradient sync and optimizer step")
         if fused:
             st.n_partials_used = self._executor.n_partials
+            table, n = self._post_sync
+            if n:
+                # statistics of the gradients changed after the sync (already
+                # unscaled by the unpack): sum of squares into the slots after
+                # the executor's, overflow of the sums into found_inf
+                nat.call("eth_grad_stats", nat.ptr(table), n, 1.0, 0, nat.ptr(st.found_inf), nat.ptr(st.partials),
+                         st.n_partials_used, nat.stream_ptr(self._device()))
+                st.n_partials_used += n
         elif scaler is not None or need_norm:
             st = self._standalone_statistics(unscale=scaler is not None)
         if st is not None:

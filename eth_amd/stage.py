@@ -14,6 +14,8 @@ stage's ops, and the fused unscale / flag / L2 statistics of the grad-sync
 unpack bound to the optimizer.
 """
 
+import math
+
 import torch
 
 from . import kernels as K
@@ -312,8 +314,15 @@ class FirstLastStageTrainer:
             bf16=cfg.params_dtype == torch.bfloat16, fp16=cfg.params_dtype == torch.float16,
             initial_loss_scale=initial_loss_scale,
         )
-        # tied weights: the norm / unscale run after the tied-gradient sum,
-        # so the optimizer computes its statistics itself (no fused binding)
+        if self.ddp.accumulate_allreduce_grads_in_fp32 and math.frexp(initial_loss_scale)[0] == 0.5:
+            # unscale and inf/nan flag fused into the sync's unpack; the tied
+            # word embedding, summed after the sync, gets its norm share and
+            # overflow check in one pass over the root at the step (exact
+            # because a power-of-two loss scale -- which the dynamic scaler
+            # keeps -- unscales each addend without rounding)
+            self.optimizer.bind_gradient_sync(
+                self.grad_sync.executor,
+                resynced=[self.embedding.word_embeddings.weight, self.post.word_embeddings.weight])
         self.nominal = float(cfg.micro_batch_size * cfg.seq_length)
 
     def forward_backward(self, sample_ids, labels=None, nominal=None):

@@ -152,8 +152,9 @@ def _check_first_last_gradients(tr, sample_ids, heads, unpadded_vocab=50257):
     tokens, mask, positions, _ = synthetic_gpt_batch(sample_ids, tr.cfg.seq_length, unpadded_vocab, "cpu")
     ref_losses, ref_mean, grads = ol.full_model_fwd_bwd(tokens, positions, mask, params, heads)
     assert _rel(losses, ref_losses) < 2e-2
-    scale = tr.optimizer.get_loss_scale().item()
-    # main grads hold d(sum(loss*mask)/sum(mask)) * loss_scale after the sync
+    # main grads hold d(sum(loss*mask)/sum(mask)) after the sync, times the
+    # loss scale unless the sync's unpack unscaled them
+    scale = 1.0 if tr.optimizer.grads_unscaled_by_sync else tr.optimizer.get_loss_scale().item()
     checks = [("word", tr.embedding.word_embeddings.weight, grads["word"]),
               ("pos", tr.embedding.position_embeddings.weight, grads["pos"]),
               ("head", tr.post.word_embeddings.weight, grads["word"]),
@@ -279,3 +280,52 @@ def test_c5_full_shape_trains(cuda):
             assert bool(torch.isfinite(p.main_grad).all()), name
         assert torch.equal(tr.embedding.word_embeddings.weight, tr.post.word_embeddings.weight)
     assert tr.optimizer.get_loss_scale().item() == 2.0**16
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_first_last_fused_statistics_match_the_standalone_pass(cuda, dtype):
+    """The first+last stage unscales in the sync's unpack and takes the tied
+    root's norm share after the tied sum: the step's norm, outcome and
+    updated parameters equal those of one standalone statistics pass over
+    every gradient, and an overflow that appears in the root after the sync
+    is still caught under fp16 loss scaling (the step is skipped)."""
+    announce(f"first+last fused statistics {dtype}")
+    cfg = GPTConfig(hidden_size=256, num_attention_heads=4, ffn_hidden_size=1024, num_layers=2, seq_length=128,
+                    micro_batch_size=2, padded_vocab_size=50304, params_dtype=dtype, device="cuda", seed=11)
+    kw = dict(lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01, clip_grad=0.05, initial_loss_scale=1024.0)
+    fused, plain = FirstLastStageTrainer(cfg, **kw), FirstLastStageTrainer(cfg, **kw)
+    assert fused.optimizer.grads_unscaled_by_sync
+    plain.optimizer.unbind_gradient_sync()
+    for (n1, p1), (n2, p2) in zip(fused.model.named_parameters(), plain.model.named_parameters()):
+        assert n1 == n2 and torch.equal(p1, p2)
+    for step in range(2):
+        _, _, ok_f, norm_f = fused.train_step([3, 8])
+        _, _, ok_p, norm_p = plain.train_step([3, 8])
+        assert ok_f and ok_p
+        # the sums of squares are formed in other chunks (fp32 within a
+        # chunk), so the norms agree to the 1e-6 bar of the canonical clip
+        assert abs(norm_f - norm_p) <= 1e-6 * norm_p, (step, norm_f, norm_p)
+        for (n1, p1), (_, p2) in zip(fused.model.named_parameters(), plain.model.named_parameters()):
+            # unscaling each tied addend before the sum (power-of-two scale)
+            # leaves the same bits as unscaling the sum
+            assert torch.equal(p1.main_grad, p2.main_grad), n1
+            m1 = fused.optimizer.optimizer_parameter_for_model_parameter(p1)
+            m2 = plain.optimizer.optimizer_parameter_for_model_parameter(p2)
+            assert torch.allclose(m1, m2, rtol=1e-6, atol=1e-9), n1
+    if dtype != torch.float16:
+        return  # bf16 trains without a loss scaler, hence without an overflow check
+    # overflow in the tied root after the sync
+    tr = fused
+    tr.ddp.zero_grad_buffer()
+    _, lo = tr.forward_backward([5, 9])
+    from eth_amd.loss import global_normalization_scale
+
+    tr.grad_sync.execute(global_normalization_scale(tr.nominal, lo.local_loss_weight))
+    tr.tie_gradients()
+    tr.embedding.word_embeddings.weight.main_grad[7, 3] = float("inf")
+    before = tr.embedding.word_embeddings.weight.detach().clone()
+    ok, norm, _ = tr.optimizer.step()
+    torch.cuda.synchronize()
+    assert not ok and norm is None
+    assert torch.equal(tr.embedding.word_embeddings.weight, before)
+    assert tr.optimizer.get_loss_scale().item() == 1024.0  # hysteresis 2: one overflow does not back off
