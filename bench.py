@@ -423,6 +423,9 @@ def main():
                     help="run the AdamW update in line instead of overlapped with the next step's forward")
     ap.add_argument("--first-last-only", action="store_true",
                     help="time only the configs[4] first+last stage (for its kernel profile)")
+    ap.add_argument("--hbm-only", action="store_true",
+                    help="time only the grad-sync and AdamW legs and their copy ceiling (for their "
+                         "FETCH_SIZE / WRITE_SIZE counter runs)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="after the timed steps, copy 1 GiB once (the calibration kernel of the "
                          "FETCH_SIZE / WRITE_SIZE counter runs behind roofline.traffic)")
@@ -441,6 +444,9 @@ def main():
     if args.first_last_only:
         fl = first_last_stage(torch, steps=args.steps, warmup=args.warmup)
         print(json.dumps({"first_last_stage": fl}), flush=True)
+        return
+    if args.hbm_only:
+        print(json.dumps({"hbm_path": hbm_path(torch)}), flush=True)
         return
 
     cfg = GPTConfig(hidden_size=H, num_attention_heads=HEADS, ffn_hidden_size=FFN, num_layers=LAYERS,
