@@ -267,7 +267,7 @@ def hbm_path(torch, iters=10):
     GPT-1.3B grad list ([3]), HIP-event timed."""
     from eth_amd.grad_sync import bucket_plan as bp
     from eth_amd.grad_sync.bucket_plan import ProcessGroupRegistry
-    from eth_amd.grad_sync.executor import GradientBucketExecutor, GradientStatistics
+    from eth_amd.grad_sync.executor import GradientBucketExecutor, GradientStatistics, local_all_reduce_sum
     from eth_amd.grad_sync.metadata import LocalGradientBinding
     from eth_amd.grad_sync.planner import plan_canonical_fragments
     from eth_amd.grad_sync.synthetic import descriptors_for, gpt_layer_shapes
@@ -289,7 +289,7 @@ def hbm_path(torch, iters=10):
     registry = ProcessGroupRegistry(plan.process_groups, lambda ranks: ranks)
     registry.initialize()
     bindings = [LocalGradientBinding(l, None, grads[l], grads[l].device) for l, *_ in shapes]
-    ex = GradientBucketExecutor(plan, 0, descs, bindings, registry, lambda p, h: None)
+    ex = GradientBucketExecutor(plan, 0, descs, bindings, registry, local_all_reduce_sum)
     st = GradientStatistics(ex.n_partials, dev)
     ex.bind_statistics(st)
     ex.set_inv_loss_scale(2.0**-16)

@@ -29,6 +29,15 @@ CHUNK_DTYPE = np.dtype(
         "itemsize": 40,
     }
 )
+# struct eth_bucket (40 bytes)
+BUCKET_DTYPE = np.dtype(
+    {
+        "names": ["chunks", "n_chunks", "payload", "partial_base", "dtype", "reserved"],
+        "formats": ["<u8", "<i8", "<u8", "<i8", "<i4", "<i4"],
+        "offsets": [0, 8, 16, 24, 32, 36],
+        "itemsize": 40,
+    }
+)
 # struct eth_adam_tensor (64 bytes)
 ADAM_TENSOR_DTYPE = np.dtype(
     {
@@ -54,6 +63,7 @@ SIGNATURES = {
     "eth_fill_f32": [_P, _I64, _F32, _P],
     "eth_bucket_pack": [_P, _I64, _P, _I32, _P],
     "eth_bucket_unpack": [_P, _I64, _P, _I32, _F32, _F32, _I32, _P, _P, _I64, _P],
+    "eth_bucket_sync_local": [_P, _I64, _F32, _F32, _I32, _P, _P, _P],
     "eth_grad_stats": [_P, _I64, _F32, _I32, _P, _P, _I64, _P],
     "eth_grad_norm_finalize": [_P, _I64, _F64, _P, _P],
     "eth_adam_step": [_P, _P, _I64, _F64, _F64, _F64, _I64, _I32, _P, _P, _P],

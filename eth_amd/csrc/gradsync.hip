@@ -376,6 +376,35 @@ int eth_bucket_unpack(const eth_chunk_t* chunks, int64_t n_chunks, void* payload
   return ETH_OK;
 }
 
+int eth_bucket_sync_local(const eth_bucket_t* buckets, int64_t n_buckets, float normalization_scale,
+                          float inv_loss_scale, int flags, float* found_inf, double* partials,
+                          void* stream) {
+  ETH_CHECK_ARG(n_buckets >= 0 && (n_buckets == 0 || buckets), "eth_bucket_sync_local: bad bucket array");
+  ETH_CHECK_ARG(!(flags & ETH_UNPACK_STATS) || (found_inf && partials),
+                "eth_bucket_sync_local: statistics requested without buffers");
+  // every entry is checked before anything is launched, so a bad entry
+  // leaves no half-synced pass behind
+  for (int64_t i = 0; i < n_buckets; ++i) {
+    const eth_bucket_t& b = buckets[i];
+    ETH_CHECK_ARG(valid_dtype(b.dtype), "eth_bucket_sync_local: bucket %lld has unsupported dtype %d",
+                  (long long)i, b.dtype);
+    ETH_CHECK_ARG(b.n_chunks >= 0 && b.n_chunks < (1LL << 31) && (b.n_chunks == 0 || (b.chunks && b.payload)),
+                  "eth_bucket_sync_local: bucket %lld has a bad chunk table or payload", (long long)i);
+    ETH_CHECK_ARG(b.partial_base >= 0, "eth_bucket_sync_local: bucket %lld has a negative partial base",
+                  (long long)i);
+  }
+  for (int64_t i = 0; i < n_buckets; ++i) {
+    const eth_bucket_t& b = buckets[i];
+    int status = eth_bucket_pack(b.chunks, b.n_chunks, b.payload, b.dtype, stream);
+    if (status != ETH_OK) return status;
+    const int f = b.dtype == ETH_F32 ? flags : flags & ~ETH_UNPACK_UNSCALE;
+    status = eth_bucket_unpack(b.chunks, b.n_chunks, b.payload, b.dtype, normalization_scale, inv_loss_scale, f,
+                               found_inf, partials, b.partial_base, stream);
+    if (status != ETH_OK) return status;
+  }
+  return ETH_OK;
+}
+
 int eth_grad_stats(const eth_chunk_t* chunks, int64_t n_chunks, float inv_loss_scale, int flags,
                    float* found_inf, double* partials, int64_t partial_base, void* stream) {
   ETH_CHECK_ARG(n_chunks >= 0 && n_chunks < (1LL << 31), "eth_grad_stats: bad chunk count");

@@ -16,8 +16,12 @@ and one unpack launch that also applies the normalization scale.  When an
 optimizer binds a GradientStatistics object, the same unpack launch also
 unscales the gradients, raises the inf/nan flag and writes per-chunk sums of
 squares for the global L2 norm, so the optimizer does not re-read them.
+With the identity seam (`local_all_reduce_sum`: a data-parallel group of one
+rank) and no evidence recorder, one native call issues the whole pass, so
+the host is not the bottleneck of a pass of many small buckets.
 """
 
+import ctypes
 import math
 
 import numpy as np
@@ -25,6 +29,12 @@ import torch
 
 from .. import _native as nat
 from .runtime_evidence import GradientRuntimeEvidenceRecorder
+
+
+def local_all_reduce_sum(payload, handle):
+    """The all-reduce of a process group that holds this rank alone: the
+    payload is already the sum (torch.distributed.all_reduce over one rank)."""
+    return None
 
 
 def _dtype_name(dtype):
@@ -279,6 +289,13 @@ class GradientBucketExecutor:
             tables.append((bucket, dev, len(table), partial_base))
             partial_base += len(table)
         self._n_partials = partial_base
+        # the same pass as one host array for eth_bucket_sync_local
+        local = np.zeros(len(tables), dtype=nat.BUCKET_DTYPE)
+        for i, (bucket, dev, n_chunks, base) in enumerate(tables):
+            payload = self._scratch[bucket.grad_dtype]
+            local[i] = (dev.data_ptr() if dev is not None else 0, n_chunks, payload.data_ptr(), base,
+                        nat.dtype_code(payload.dtype), 0)
+        self._local_pass = local
         return tables
 
     # ----------------------------------------------------------- statistics --
@@ -394,6 +411,23 @@ class GradientBucketExecutor:
 
     def execute(self, normalization_scale=1.0):
         self.begin(normalization_scale)
-        for i in range(len(self._tables)):
-            self.run_bucket(i)
+        if self._all_reduce_sum is local_all_reduce_sum and self._evidence is None and len(self._tables):
+            # the identity seam: one native call issues every bucket's pack
+            # and unpack (the launches run_bucket would make, in its order)
+            normalization_scale, flags = self._pass
+            stats = self._statistics
+            nat.call(
+                "eth_bucket_sync_local",
+                ctypes.c_void_p(self._local_pass.ctypes.data),
+                len(self._local_pass),
+                normalization_scale,
+                float(self._inv_scale),
+                flags,
+                nat.ptr(stats.found_inf) if stats is not None else None,
+                nat.ptr(stats.partials) if stats is not None else None,
+                nat.stream_ptr(self._device),
+            )
+        else:
+            for i in range(len(self._tables)):
+                self.run_bucket(i)
         self.end()

@@ -9,7 +9,7 @@ at world size 1 without torch.distributed.
 """
 
 from .bucket_plan import ProcessGroupRegistry, build_gradient_sync_plan
-from .executor import GradientBucketExecutor
+from .executor import GradientBucketExecutor, local_all_reduce_sum
 from .planner import plan_canonical_fragments
 
 
@@ -41,7 +41,7 @@ def initialize_gradient_sync(
     topology_hash="topology",
     all_gather_object=_single_rank_all_gather,
     create_group=lambda ranks: ranks,
-    all_reduce_sum=lambda payload, handle: None,
+    all_reduce_sum=local_all_reduce_sum,
     runtime_evidence_dir=None,
 ):
     """Plan, verify and bind gradient synchronization for this rank."""

@@ -289,31 +289,32 @@ class MegatronOptimizer:
         if host is not None:
             host[1].synchronize()
         if scaler is not None:
-            found = bool(host[0][1].item() > 0)
+            found = bool(host[0][1][0].item() > 0)
             scaler.update(found)
             self.optimizer.commit_step(not found)
             if self._executor is not None:
                 self._executor.set_inv_loss_scale(self._inv_scale())
             if found:
                 return False, None, None
-        grad_norm = float(host[0][0].item()) if need_norm else None
+        grad_norm = float(host[0][0][1].item()) if need_norm else None
         num_zeros = self.count_zeros() if self.log_num_zeros_in_grad else None
         return True, grad_norm, num_zeros
 
     def _read_back(self, st):
-        """Queue a copy of [‖g‖, found_inf] into pinned host memory on the
-        current stream; returns (host tensor, event marking the copy)."""
+        """Queue copies of stats ([Σg², ‖g‖, clip]) and found_inf into pinned
+        host memory on the current stream; returns ((stats, found_inf) host
+        tensors, event marking the copies)."""
         dev = self._device()
         if self._host_flags is None:
-            self._host_flags = (torch.empty(2, dtype=torch.float64, pin_memory=True),
-                                torch.empty(2, dtype=torch.float64, device=dev))
-        host, staging = self._host_flags
-        staging[0:1].copy_(st.stats[1:2])
-        staging[1:2].copy_(st.found_inf.reshape(-1)[0:1])
-        host.copy_(staging, non_blocking=True)
+            self._host_flags = (torch.empty(3, dtype=torch.float64, pin_memory=True),
+                                torch.empty(1, dtype=torch.float32, pin_memory=True))
+        host_stats, host_inf = self._host_flags
+        # two direct copies into pinned memory, no device staging kernels
+        host_stats.copy_(st.stats, non_blocking=True)
+        host_inf.copy_(st.found_inf.reshape(-1)[0:1], non_blocking=True)
         ev = torch.cuda.Event()
         ev.record(torch.cuda.current_stream(dev))
-        return host, ev
+        return (host_stats, host_inf), ev
 
     def zero_grad(self, set_to_none=True):
         for p in self.get_parameters():
@@ -413,18 +414,22 @@ class Float16OptimizerWithFloat16Params(MegatronOptimizer):
                 if self.params_have_main_grad:
                     g = model_param.main_grad
                     if g.dtype == torch.float32:
-                        main_param.grad = g
+                        # (the alias usually stands from the previous step)
+                        if main_param.grad is not g:
+                            main_param.grad = g
                     else:
                         # main_grad.float() (optimizer.py:392-397) into a
                         # persistent buffer: an exact widening copy
                         main_param.grad = self._fp32_grad_view(main_param).copy_(g)
                 elif model_param.grad is not None:
                     main_param.grad = model_param.grad.float()
-                model_param.grad = None
+                if model_param.grad is not None:
+                    model_param.grad = None
         if self.params_have_main_grad:
             for group in self.fp32_from_fp32_groups:
                 for p in group:
-                    p.grad = p.main_grad
+                    if p.grad is not p.main_grad:
+                        p.grad = p.main_grad
 
     def _norm_owned(self, param):
         return super()._norm_owned(param)

@@ -21,6 +21,7 @@ import torch
 from . import kernels as K
 from .grad_sync.gpt_adapter import collect_stage_metadata
 from .loss import global_normalization_scale, gpt_loss_output, sum_loss_outputs, synthetic_gpt_batch
+from .grad_sync.executor import local_all_reduce_sum
 from .grad_sync.manager import initialize_gradient_sync
 from .grad_sync.streamed import StreamedGradSync
 from .model.distributed import DistributedDataParallel
@@ -112,7 +113,7 @@ class MiddleStageTrainer:
             expected_pipeline_ids=(0,),
             sync_mode=sync_mode,
             bucket_cap_bytes=bucket_cap_bytes,
-            all_reduce_sum=all_reduce_sum or (lambda payload, handle: None),
+            all_reduce_sum=all_reduce_sum or local_all_reduce_sum,
             runtime_evidence_dir=runtime_evidence_dir,
         )
         self.optimizer = get_megatron_optimizer(

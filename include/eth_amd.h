@@ -83,6 +83,31 @@ int eth_bucket_unpack(const eth_chunk_t* chunks, int64_t n_chunks, void* payload
                       int flags, float* found_inf, double* partials,
                       int64_t partial_base, void* stream);
 
+/* One bucket of a sync pass: its chunk table, payload and first partial slot. */
+typedef struct eth_bucket {
+  const eth_chunk_t* chunks; /* device chunk table */
+  int64_t n_chunks;
+  void* payload;             /* device payload (the rank's scratch buffer) */
+  int64_t partial_base;      /* first slot of the bucket's L2 partials */
+  int32_t dtype;             /* ETH_F32 / ETH_F16 / ETH_BF16 */
+  int32_t reserved;          /* 0 */
+} eth_bucket_t;
+
+/* A whole sync pass over `n_buckets` buckets (host array, in order) whose
+ * all-reduce is the identity -- every process group of the pass holds this
+ * rank alone: for each bucket, eth_bucket_pack then eth_bucket_unpack with
+ * the pass's scale, flags and statistics buffers (ETH_UNPACK_UNSCALE applies
+ * to fp32 payloads only), the same launches in the same order, so the
+ * results are bit-identical to the per-bucket calls.  Every entry is checked
+ * before the first launch.  One host call instead of two per bucket, so the
+ * host stays ahead of the GPU through the pass.
+ * Replaces the bucket loop of GradientBucketExecutor.execute
+ * (eth/runtime/megatron/grad_sync/executor.py:248-260) for a single-rank
+ * data-parallel group. */
+int eth_bucket_sync_local(const eth_bucket_t* buckets, int64_t n_buckets,
+                          float normalization_scale, float inv_loss_scale, int flags,
+                          float* found_inf, double* partials, void* stream);
+
 /* Standalone unscale + inf/nan check + sum of squares over chunk-described
  * fp32 gradients, in place (g *= inv_scale when ETH_UNPACK_UNSCALE).  Used
  * when gradients did not pass through eth_bucket_unpack this step.

@@ -9,7 +9,7 @@ import pytest
 import torch
 
 from eth_amd.grad_sync import bucket_plan as bp
-from eth_amd.grad_sync.executor import GradientBucketExecutor, GradientStatistics
+from eth_amd.grad_sync.executor import GradientBucketExecutor, GradientStatistics, local_all_reduce_sum
 from eth_amd.grad_sync.planner import (
     CanonicalFragmentPlan,
     LocalFragmentBindingSpec,
@@ -17,6 +17,7 @@ from eth_amd.grad_sync.planner import (
     TensorSegmentSpec,
     plan_canonical_fragments,
 )
+from eth_amd.grad_sync.synthetic import single_rank_descriptor
 from oracle import gradsync as og
 from tests.conftest import announce
 from tests.helpers import (
@@ -138,7 +139,11 @@ def test_validation_errors_carry_bucket_context(cuda):
 
 def _gpt_setup(cuda, hidden, ffn, layers, cap_bytes, mode, seed, dtype=torch.float32):
     shapes = gpt_layer_shapes(hidden, ffn, layers)
-    descs = descriptors_for(shapes)
+    if dtype == torch.float32:
+        descs = descriptors_for(shapes)
+    else:
+        descs = [single_rank_descriptor(lid, shape, (op, order, lid), tp, pdim, dtype=str(dtype))
+                 for lid, shape, op, order, tp, pdim in shapes]
     fplan = plan_canonical_fragments(descs, (0,))
     plan = bp.build_gradient_sync_plan(fplan, mode, cap_bytes, "gpt", "m", "t")
     gen = torch.Generator().manual_seed(seed)
@@ -232,3 +237,61 @@ def test_strided_tp_segments_vs_oracle(cuda):
     ref = og.execute(plan, 0, {"w": Desc("w", 1)}, host, 2.0)
     np.testing.assert_array_equal(packed[0], ref[0])
     np.testing.assert_array_equal(g.cpu().numpy(), host["w"])
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_local_pass_matches_the_per_bucket_calls(cuda, dtype):
+    """eth_bucket_sync_local (the identity seam, one native call for the
+    pass) against run_bucket's two launches per bucket through a seam that
+    is not the identity object: main grads, the last payload, found_inf and
+    every L2 partial bit for bit, with a normalization scale, an unscale (fp32
+    only) and an inf planted on the second call."""
+    announce(f"grad_sync local pass vs per-bucket calls, {dtype}")
+    setups = [_gpt_setup(cuda, 64, 256, 3, 1 << 13, "block", seed=21, dtype=dtype) for _ in range(2)]
+    exs, sts = [], []
+    for seam, (plan, descs, grads, bindings) in zip((local_all_reduce_sum, lambda p, h: None), setups):
+        for g in grads.values():
+            g.mul_(4096.0)
+        ex = GradientBucketExecutor(plan, 0, descs, bindings, FakeRegistry(), seam)
+        st = GradientStatistics(ex.n_partials, cuda)
+        ex.bind_statistics(st)
+        if dtype == torch.float32:
+            ex.set_inv_loss_scale(2.0**-12)
+        exs.append(ex)
+        sts.append(st)
+    assert exs[0].n_buckets > 4
+    for call in range(2):
+        if call == 1:
+            for _, _, grads, _ in setups:
+                next(iter(grads.values())).view(-1)[17] = float("inf")
+        for ex in exs:
+            ex.execute(0.3701)
+        torch.cuda.synchronize()
+        for a, b in zip(setups[0][2].values(), setups[1][2].values()):
+            assert torch.equal(a.view(torch.int16 if dtype != torch.float32 else torch.int32),
+                               b.view(torch.int16 if dtype != torch.float32 else torch.int32))
+        name = exs[0].scratch_dtypes[0]
+        assert torch.equal(exs[0].scratch(name), exs[1].scratch(name))
+        assert sts[0].found_inf.item() == sts[1].found_inf.item() == float(call)
+        assert torch.equal(sts[0].partials, sts[1].partials)
+
+
+def test_local_pass_rejects_a_bad_entry_before_launching(cuda):
+    """A bad bucket entry (unsupported dtype) raises before any launch, so
+    the payload is left untouched."""
+    import ctypes
+
+    from eth_amd import _native as nat
+
+    announce("grad_sync local pass bad entry")
+    plan, descs, grads, bindings = _gpt_setup(cuda, 64, 256, 1, 1 << 13, "block", seed=5)
+    ex = GradientBucketExecutor(plan, 0, descs, bindings, FakeRegistry(), local_all_reduce_sum)
+    name = ex.scratch_dtypes[0]
+    ex.scratch(name).fill_(-7.0)
+    entries = ex._local_pass.copy()
+    entries[-1]["dtype"] = 9
+    with pytest.raises(ValueError, match="unsupported dtype"):
+        nat.call("eth_bucket_sync_local", ctypes.c_void_p(entries.ctypes.data), len(entries), 1.0, 1.0, 0,
+                 None, None, nat.stream_ptr(cuda))
+    torch.cuda.synchronize()
+    assert bool((ex.scratch(name) == -7.0).all())
