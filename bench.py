@@ -365,6 +365,50 @@ def hbm_path(torch, iters=10):
     return out
 
 
+def gemm_layer_products(torch, reps=10):
+    """The twelve GEMMs of one C2 layer alone, as LinearFn issues them
+    (forward X W^T with bias, data gradient dY W, weight gradient dY^T X
+    stored into an fp32 main_grad), each HIP-event timed over `reps` calls,
+    beside torch.matmul (hipBLASLt) on the same bf16 operands."""
+    from eth_amd import kernels as K
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(7)
+    T = SEQ * MB
+
+    def rnd(*shape):
+        return torch.randn(*shape, device=dev, generator=g).to(torch.bfloat16)
+
+    def timed(fn):
+        fn()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            fn()
+        b.record()
+        b.synchronize()
+        return a.elapsed_time(b) * 1e3 / reps
+
+    rows, tot, tot_lib = [], 0.0, 0.0
+    for name, n_in, n_out in (("qkv", H, 3 * H), ("proj", H, H), ("fc1", H, FFN), ("fc2", FFN, H)):
+        x, w, dy, bias = rnd(T, n_in), rnd(n_out, n_in), rnd(T, n_out), rnd(n_out)
+        mg = torch.empty(n_out, n_in, dtype=torch.float32, device=dev)
+        for kind, fn, lib, (m, n, k) in (
+            ("fwd", lambda: K.gemm(x, w.t(), bias=bias), lambda: torch.matmul(x, w.t()), (T, n_out, n_in)),
+            ("dgrad", lambda: K.gemm(dy, w), lambda: torch.matmul(dy, w), (T, n_in, n_out)),
+            ("wgrad", lambda: K.gemm(dy.t(), x, out=mg), lambda: torch.matmul(dy.t(), x), (n_out, n_in, T)),
+        ):
+            us, us_lib = timed(fn), timed(lib)
+            flops = 2.0 * m * n * k
+            rows.append({"product": f"{name} {kind}", "M": m, "N": n, "K": k, "us": us,
+                         "tflops": flops / us / 1e6, "hipblaslt_us": us_lib, "hipblaslt_tflops": flops / us_lib / 1e6})
+            tot += us
+            tot_lib += us_lib
+        del x, w, dy, bias, mg
+    return {"products": rows, "layer_us": tot, "hipblaslt_layer_us": tot_lib,
+            "layer_tflops": 3 * 2.0 * T * (H * 3 * H + H * H + 2 * H * FFN) / tot / 1e6}
+
+
 def first_last_stage(torch, steps=5, warmup=2):
     """the GPT-6.7B first+last stage in fp16 -- token +
     position embedding, 2 layers (hidden 4096, 32 heads, FFN 16384), final
@@ -423,6 +467,8 @@ def main():
                     help="run the AdamW update in line instead of overlapped with the next step's forward")
     ap.add_argument("--first-last-only", action="store_true",
                     help="time only the configs[4] first+last stage (for its kernel profile)")
+    ap.add_argument("--gemm-only", action="store_true",
+                    help="time only the twelve GEMMs of one layer alone, beside hipBLASLt (for their counter runs)")
     ap.add_argument("--hbm-only", action="store_true",
                     help="time only the grad-sync and AdamW legs and their copy ceiling (for their "
                          "FETCH_SIZE / WRITE_SIZE counter runs)")
@@ -447,6 +493,9 @@ def main():
         return
     if args.hbm_only:
         print(json.dumps({"hbm_path": hbm_path(torch)}), flush=True)
+        return
+    if args.gemm_only:
+        print(json.dumps({"gemm_layer_products": gemm_layer_products(torch)}), flush=True)
         return
 
     cfg = GPTConfig(hidden_size=H, num_attention_heads=HEADS, ffn_hidden_size=FFN, num_layers=LAYERS,
