@@ -425,9 +425,13 @@ def first_last_stage(torch, steps=5, warmup=2):
     tr = FirstLastStageTrainer(cfg, lr=1e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, clip_grad=1.0,
                                bucket_cap_bytes=32 << 20, initial_loss_scale=2.0**16)
     for i in range(warmup):
+        if i == warmup - 1:  # the freeze before the last warm-up step (see main)
+            torch.cuda.synchronize()
+            quiet_gc()
         tr.train_step([2 * i, 2 * i + 1])
+    if warmup == 0:
+        quiet_gc()
     torch.cuda.synchronize()
-    quiet_gc()
     t0 = time.perf_counter()
     oks = 0
     for i in range(steps):
@@ -505,10 +509,17 @@ def main():
     g = torch.Generator(device="cuda").manual_seed(1234)
     x = torch.randn(SEQ, MB, H, device="cuda", generator=g).to(torch.bfloat16)
     dy = (torch.randn(SEQ, MB, H, device="cuda", generator=g) * 1e-3).to(torch.bfloat16)
-    for _ in range(args.warmup):
+    # the collector freeze idles the GPU for a fraction of a second, and the
+    # shader clock ramps back up over the next step: it goes before the last
+    # warm-up step, so the timed steps start on a busy-clocked GPU
+    for i in range(args.warmup):
+        if i == args.warmup - 1:
+            torch.cuda.synchronize()
+            quiet_gc()
         tr.train_step(x, dy)
+    if args.warmup == 0:
+        quiet_gc()
     torch.cuda.synchronize()
-    quiet_gc()
 
     # timed steps: no instrumentation besides one event pair per step
     marks = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
