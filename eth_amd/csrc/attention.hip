@@ -271,13 +271,29 @@ __global__ void __launch_bounds__(kAttnThreads, 2) attn_fwd_kernel(AttnArgs a) {
       // S^T = K Q^T (raw scores; lane = query, registers = 32 of the keys)
       a_f32x16 s[2];
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
+      for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r) s[t][r] = 0.f;
-        const uint16_t* kp = Ks[st] + (t * 32 + (lane & 31)) * (D + 8) + hl * 8;
+      // all K fragments of the first 32-key tile are read before its MFMAs,
+      // each register refilled with the second tile's fragment right after
+      // its MFMA issues (order pinned: left alone, the compiler reads each
+      // fragment one or two MFMAs before its use and waits on the LDS latency)
+      {
+        const uint16_t* kp0 = Ks[st] + (lane & 31) * (D + 8) + hl * 8;
+        const uint16_t* kp1 = kp0 + 32 * (D + 8);
+        uint4 kr[KS];
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
-          s[t] = mma<FP16>(*reinterpret_cast<const uint4*>(kp + ks * 16), qf[ks], s[t]);
+        for (int ks = 0; ks < KS; ++ks) kr[ks] = *reinterpret_cast<const uint4*>(kp0 + ks * 16);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          s[0] = mma<FP16>(kr[ks], qf[ks], s[0]);
+          __builtin_amdgcn_sched_barrier(0);
+          kr[ks] = *reinterpret_cast<const uint4*>(kp1 + ks * 16);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) s[1] = mma<FP16>(kr[ks], qf[ks], s[1]);
       }
       if (kv0 + kBKV - 1 > q0) {  // diagonal block: mask keys after the query
 #pragma unroll
