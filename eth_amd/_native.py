@@ -74,6 +74,7 @@ SIGNATURES = {
     "eth_bias_gelu_fwd": [_P, _P, _P, _I64, _I64, _I32, _P],
     "eth_bias_gelu_bwd": [_P, _P, _P, _P, _I64, _I64, _I32, _P],
     "eth_bias_dropout_add_fwd": [_P, _P, _P, _P, _I64, _I64, _F32, ctypes.c_uint64, _I32, _P],
+    "eth_bda_ln_fwd": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _F32, ctypes.c_uint64, _F32, _I32, _P],
     "eth_dropout_bwd": [_P, _P, _I64, _I64, _F32, ctypes.c_uint64, _I32, _P],
     "eth_col_sum": [_P, _I64, _I64, _I64, _P, _P, _I32, _I32, _P],
     "eth_ln_bwd_residual": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I32, _I32, _P],

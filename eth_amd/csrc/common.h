@@ -128,6 +128,24 @@ __global__ void reduce_partials_kernel(const float* __restrict__ part, int group
 inline dim3 reduce_partials_grid(int cols, int slabs = 1) { return dim3((cols + 63) / 64, slabs); }
 constexpr int kReducePartialsThreads = 256;
 
+// 32-bit mix of (seed, index): the dropout keep decision of element `idx`
+// (kept when >= p * 2^32).  Shared by every kernel that applies or replays a
+// dropout mask, so they all draw the same one.
+__device__ __forceinline__ uint32_t hash_u32(uint64_t seed, uint64_t idx) {
+  uint64_t z = seed + 0x9E3779B97F4A7C15ull * (idx + 1);
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  z ^= z >> 31;
+  return (uint32_t)(z >> 32);
+}
+
+// Host side of the dropout mask: keep threshold (0 when p == 0, no mask) and
+// the 1/(1-p) scale of kept elements.
+inline void dropout_params(float p, uint32_t& thresh, float& scale) {
+  thresh = p <= 0.f ? 0u : (uint32_t)fmin(4294967295.0, (double)p * 4294967296.0);
+  scale = p <= 0.f ? 1.f : (float)(1.0 / (1.0 - (double)p));
+}
+
 inline int dtype_size(int dtype) { return dtype == ETH_F32 ? 4 : 2; }
 inline bool valid_dtype(int dtype) {
   return dtype == ETH_F32 || dtype == ETH_F16 || dtype == ETH_BF16;

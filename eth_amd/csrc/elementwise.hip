@@ -55,15 +55,6 @@ __device__ __forceinline__ float gelu_tanh_grad(float x) {
   return __builtin_fmaf(0.5f, right, left * __builtin_fmaf(-t, t, 1.0f) * kBeta * __builtin_fmaf(3.0f * kKappa, x2, 1.0f));
 }
 
-// 32-bit mix of (seed, index): keep decision for dropout.
-__device__ __forceinline__ uint32_t hash_u32(uint64_t seed, uint64_t idx) {
-  uint64_t z = seed + 0x9E3779B97F4A7C15ull * (idx + 1);
-  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
-  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
-  z ^= z >> 31;
-  return (uint32_t)(z >> 32);
-}
-
 constexpr int kEwThreads = 256;
 
 template <bool FP16>
@@ -374,11 +365,6 @@ extern "C" int eth_bias_gelu_bwd(const void* dy, const void* x, const void* bias
         (const uint16_t*)dy, (const uint16_t*)x, (const uint16_t*)bias, (uint16_t*)dx, nvec, (int)cols);
   ETH_CHECK_LAUNCH("eth_bias_gelu_bwd");
   return ETH_OK;
-}
-
-static void dropout_params(float p, uint32_t& thresh, float& scale) {
-  thresh = p <= 0.f ? 0u : (uint32_t)fmin(4294967295.0, (double)p * 4294967296.0);
-  scale = p <= 0.f ? 1.f : (float)(1.0 / (1.0 - (double)p));
 }
 
 extern "C" int eth_bias_dropout_add_fwd(const void* x, const void* bias, const void* residual,

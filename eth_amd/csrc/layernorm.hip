@@ -108,6 +108,90 @@ __global__ void __launch_bounds__(64 * kLnWaves) ln_fwd_kernel(const uint16_t* _
   }
 }
 
+// Bias-dropout-add and the LayerNorm that follows it, one wave per row:
+// h = residual + dropout(16-bit(x + b)) is rounded and stored exactly as
+// bda_fwd_kernel does (same mask: the hash of the element's flat index), and
+// the stored 16-bit h values are then normalized with ln_fwd_kernel's
+// arithmetic, so h, y, mean and rstd are bit-identical to the two kernels in
+// sequence while h is read from HBM once less.
+template <int NV, bool FP16>
+__global__ void __launch_bounds__(64 * kLnWaves) bda_ln_fwd_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ bias, const uint16_t* __restrict__ res,
+    uint16_t* __restrict__ h, const uint16_t* __restrict__ gamma, const uint16_t* __restrict__ beta,
+    uint16_t* __restrict__ y, float* __restrict__ mean, float* __restrict__ rstd, int rows, int cols, float eps,
+    uint32_t thresh, float keep_scale, uint64_t seed) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * kLnWaves + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int64_t base = (int64_t)row * cols;
+  float v[NV][8];
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = (i * 64 + lane) * 8;
+    if (c < cols) {
+      const uint4 xr = *reinterpret_cast<const uint4*>(x + base + c);
+      const uint4 rr = *reinterpret_cast<const uint4*>(res + base + c);
+      const uint4 br = *reinterpret_cast<const uint4*>(bias + c);
+      const uint16_t* xe = reinterpret_cast<const uint16_t*>(&xr);
+      const uint16_t* re = reinterpret_cast<const uint16_t*>(&rr);
+      const uint16_t* be = reinterpret_cast<const uint16_t*>(&br);
+      uint4 hr;
+      uint16_t* he = reinterpret_cast<uint16_t*>(&hr);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        float t = cvt_in<FP16>(cvt_out<FP16>(cvt_in<FP16>(xe[j]) + cvt_in<FP16>(be[j])));
+        if (thresh) {
+          const bool keep = hash_u32(seed, (uint64_t)(base + c + j)) >= thresh;
+          t = cvt_in<FP16>(cvt_out<FP16>(keep ? t * keep_scale : 0.f));
+        }
+        he[j] = cvt_out<FP16>(cvt_in<FP16>(re[j]) + t);
+        v[i][j] = cvt_in<FP16>(he[j]);
+        s += v[i][j];
+      }
+      *reinterpret_cast<uint4*>(h + base + c) = hr;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[i][j] = 0.f;
+    }
+  }
+  const float mu = wave_sum(s) / cols;
+  float q = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = (i * 64 + lane) * 8;
+    if (c < cols) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float d = v[i][j] - mu;
+        q = __builtin_fmaf(d, d, q);
+      }
+    }
+  }
+  const float var = wave_sum(q) / cols;
+  const float r = rsqrtf(var + eps);
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = (i * 64 + lane) * 8;
+    if (c < cols) {
+      const uint4 gr = *reinterpret_cast<const uint4*>(gamma + c);
+      const uint4 br = *reinterpret_cast<const uint4*>(beta + c);
+      const uint16_t* ge = reinterpret_cast<const uint16_t*>(&gr);
+      const uint16_t* be = reinterpret_cast<const uint16_t*>(&br);
+      uint4 out;
+      uint16_t* oe = reinterpret_cast<uint16_t*>(&out);
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        oe[j] = cvt_out<FP16>(__builtin_fmaf((v[i][j] - mu) * r, cvt_in<FP16>(ge[j]), cvt_in<FP16>(be[j])));
+      *reinterpret_cast<uint4*>(y + base + c) = out;
+    }
+  }
+  if (lane == 0) {
+    mean[row] = mu;
+    rstd[row] = r;
+  }
+}
+
 // Backward.  A workgroup of kLnBwdWaves waves owns rows g, g + G, g + 2G, ...;
 // T waves share a row (T = 1 up to 1024 columns, 2 up to 2048, 4 up to
 // 4096, 8 up to 8192), each covering NVW <= 2 vectors of 512 columns (the
@@ -323,6 +407,26 @@ static void launch_fwd(const uint16_t* x, const uint16_t* g, const uint16_t* b, 
   }
 }
 
+template <bool FP16>
+static void launch_bda_ln(const uint16_t* x, const uint16_t* bias, const uint16_t* res, uint16_t* h,
+                          const uint16_t* g, const uint16_t* b, uint16_t* y, float* mean, float* rstd, int rows,
+                          int cols, float eps, uint32_t thresh, float keep_scale, uint64_t seed, hipStream_t s) {
+  const int grid = (rows + kLnWaves - 1) / kLnWaves;
+  const int nv = (cols + 511) / 512;
+  switch (nv) {
+#define ETH_BDA_LN_CASE(N)                                                                                  \
+  case N:                                                                                                   \
+    bda_ln_fwd_kernel<N, FP16><<<grid, 64 * kLnWaves, 0, s>>>(x, bias, res, h, g, b, y, mean, rstd, rows, cols, \
+                                                               eps, thresh, keep_scale, seed);              \
+    break;
+    ETH_BDA_LN_CASE(1) ETH_BDA_LN_CASE(2) ETH_BDA_LN_CASE(3) ETH_BDA_LN_CASE(4) ETH_BDA_LN_CASE(5)
+    ETH_BDA_LN_CASE(6) ETH_BDA_LN_CASE(7) ETH_BDA_LN_CASE(8) ETH_BDA_LN_CASE(9) ETH_BDA_LN_CASE(10)
+    ETH_BDA_LN_CASE(11) ETH_BDA_LN_CASE(12) ETH_BDA_LN_CASE(13) ETH_BDA_LN_CASE(14) ETH_BDA_LN_CASE(15)
+    ETH_BDA_LN_CASE(16)
+#undef ETH_BDA_LN_CASE
+  }
+}
+
 template <bool FP16, bool RESID, bool CSUM>
 static void launch_bwd(const uint16_t* dy, const uint16_t* x, const float* mean, const float* rstd,
                        const uint16_t* g, const uint16_t* dres, uint16_t* dx, float* part, float* cpart,
@@ -361,6 +465,33 @@ extern "C" int eth_ln_fwd(const void* x, const void* gamma, const void* beta, vo
     launch_fwd<true>((const uint16_t*)x, (const uint16_t*)gamma, (const uint16_t*)beta, (uint16_t*)y,
                      mean, rstd, (int)rows, (int)cols, eps, s);
   ETH_CHECK_LAUNCH("eth_ln_fwd");
+  return ETH_OK;
+}
+
+extern "C" int eth_bda_ln_fwd(const void* x, const void* bias, const void* residual, void* h,
+                              const void* gamma, const void* beta, void* y, float* mean, float* rstd,
+                              int64_t rows, int64_t cols, float p, uint64_t seed, float eps, int dtype,
+                              void* stream) {
+  ETH_CHECK_ARG(dtype == ETH_BF16 || dtype == ETH_F16, "eth_bda_ln_fwd: dtype must be bf16/fp16");
+  ETH_CHECK_ARG(rows >= 0 && rows < (1LL << 31) && cols > 0 && cols <= kMaxCols && cols % 8 == 0,
+                "eth_bda_ln_fwd: cols must be a positive multiple of 8 up to %d (got %lld)", kMaxCols,
+                (long long)cols);
+  ETH_CHECK_ARG(p >= 0.f && p < 1.f, "eth_bda_ln_fwd: p must be in [0, 1)");
+  if (rows == 0) return ETH_OK;
+  ETH_CHECK_ARG(x && bias && residual && h && gamma && beta && y && mean && rstd, "eth_bda_ln_fwd: null pointer");
+  uint32_t thresh;
+  float scale;
+  dropout_params(p, thresh, scale);
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == ETH_BF16)
+    launch_bda_ln<false>((const uint16_t*)x, (const uint16_t*)bias, (const uint16_t*)residual, (uint16_t*)h,
+                         (const uint16_t*)gamma, (const uint16_t*)beta, (uint16_t*)y, mean, rstd, (int)rows,
+                         (int)cols, eps, thresh, scale, seed, s);
+  else
+    launch_bda_ln<true>((const uint16_t*)x, (const uint16_t*)bias, (const uint16_t*)residual, (uint16_t*)h,
+                        (const uint16_t*)gamma, (const uint16_t*)beta, (uint16_t*)y, mean, rstd, (int)rows,
+                        (int)cols, eps, thresh, scale, seed, s);
+  ETH_CHECK_LAUNCH("eth_bda_ln_fwd");
   return ETH_OK;
 }
 

@@ -272,6 +272,26 @@ def bias_dropout_add_fwd(x, bias, residual, p=0.0, seed=0):
     return out
 
 
+def bias_dropout_add_layer_norm_fwd(x, bias, residual, gamma, beta, p=0.0, seed=0, eps=1e-5):
+    """(h, y, mean, rstd): h = bias_dropout_add_fwd(x, bias, residual, p,
+    seed) and (y, mean, rstd) = layer_norm_fwd(h, gamma, beta, eps), bit for
+    bit, from one kernel that does not read h back."""
+    code = _check_half(x, bias, residual, gamma, beta)
+    rows, cols = _rows_cols(x)
+    if residual.shape != x.shape or not residual.is_contiguous() or bias.numel() != cols:
+        raise ValueError("shape mismatch")
+    if gamma.numel() != cols or beta.numel() != cols:
+        raise ValueError("gamma/beta must match the normalized size")
+    h = torch.empty_like(x)
+    y = torch.empty_like(x)
+    mean = torch.empty(rows, dtype=torch.float32, device=x.device)
+    rstd = torch.empty(rows, dtype=torch.float32, device=x.device)
+    nat.call("eth_bda_ln_fwd", nat.ptr(x), nat.ptr(bias), nat.ptr(residual), nat.ptr(h), nat.ptr(gamma),
+             nat.ptr(beta), nat.ptr(y), nat.ptr(mean), nat.ptr(rstd), rows, cols, float(p),
+             int(seed) & (2**64 - 1), float(eps), code, nat.stream_ptr(x.device))
+    return h, y, mean, rstd
+
+
 def dropout_bwd(dy, p, seed):
     code = _check_half(dy)
     rows, cols = _rows_cols(dy)

@@ -25,7 +25,7 @@ reach the segment.
 import torch
 from torch import nn
 
-from .flex_ops import GPTConfig, build_gpt_op_list, gen_op
+from .flex_ops import GPTConfig, ParallelDropoutOp, ParallelLayerNormOp, build_gpt_op_list, gen_op
 
 _SEGMENT_BREAK = "enc-1st-layernorm"
 
@@ -42,6 +42,15 @@ def await_parameters(op):
                 torch.cuda.current_stream(p.device).wait_event(ev)
                 seen.add(id(ev))
             p._eth_ready_event = None
+
+
+def _await_op(op):
+    """await_parameters for op, and for the LayerNorm op whose forward it runs
+    (a bias-dropout-add paired with the next LayerNorm reads its weights)."""
+    await_parameters(op)
+    ln_op = getattr(op, "fused_layernorm_op", None)
+    if ln_op is not None:
+        await_parameters(ln_op)
 
 
 def _rng_state(ops):
@@ -138,6 +147,21 @@ class FlexPipeModel(nn.Module):
             raise ValueError(f"recompute_ops must hold one 0/1 flag per op ({self.num_ops}), got {flags}")
         self.recompute_ops = flags
         self._mark_cross_stage()
+        self._pair_dropout_layernorm()
+
+    def _pair_dropout_layernorm(self):
+        """A bias-dropout-add followed in this stage by a residual-publishing
+        LayerNorm, neither in a checkpointed segment, runs as one kernel with
+        it (BiasDropoutAddLayerNormFn); the LayerNorm op then takes the
+        precomputed result.  Same values, bit for bit."""
+        for i, op in enumerate(self.ops):
+            if isinstance(op, ParallelDropoutOp):
+                nxt = self.ops[i + 1] if i + 1 < self.num_ops else None
+                fuse = (isinstance(nxt, ParallelLayerNormOp) and bool(nxt.output_extra_tensors_info)
+                        and not self.recompute_ops[i] and not self.recompute_ops[i + 1])
+                # a plain attribute, not a registered submodule: the LayerNorm's
+                # parameters keep their one name in the module tree
+                object.__setattr__(op, "fused_layernorm_op", nxt if fuse else None)
 
     def _mark_cross_stage(self):
         """An extra tensor crosses the stage when its consumer op is not here
@@ -184,14 +208,14 @@ class FlexPipeModel(nn.Module):
         hidden = inputs if self.pre_process else self.input_tensor
         if not any(self.recompute_ops):
             for op in self.ops:
-                await_parameters(op)
+                _await_op(op)
                 hidden = op(hidden, input_extra_tensors, output_extra_tensors)
         else:
             for start, end, ckpt in self.segments():
                 if ckpt:
                     hidden = self._checkpointed(start, end, hidden, input_extra_tensors, output_extra_tensors)
                 else:
-                    await_parameters(self.ops[start])
+                    _await_op(self.ops[start])
                     hidden = self.ops[start](hidden, input_extra_tensors, output_extra_tensors)
         if self.post_process:
             return hidden

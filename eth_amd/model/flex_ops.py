@@ -16,7 +16,7 @@ from dataclasses import dataclass
 import torch
 from torch import nn
 
-from .functional import BiasDropoutAddFn, BiasGeluFn, CausalAttentionFn, SplitQKVFn
+from .functional import BiasDropoutAddFn, BiasDropoutAddLayerNormFn, BiasGeluFn, CausalAttentionFn, SplitQKVFn
 from .layers import ColumnParallelLinear, LayerNorm, RowParallelLinear, init_method_normal
 
 
@@ -167,6 +167,10 @@ class ParallelDropoutOp(RopalaModule):
         self.residual_key = "hidden_states_1" if name == "enc-post-attention-dropout" else "hidden_states_2"
         self._seed = (cfg.seed * 1000003 + op_index) & (2**63 - 1)
         self._calls = 0
+        # the LayerNorm op that takes this op's output next in the same stage,
+        # when the stage runs the two back to back (set by the stage model,
+        # outside the module registry)
+        object.__setattr__(self, "fused_layernorm_op", None)
 
     def forward(self, input_tensors, input_extra_tensors, output_extra_tensors, profiling=False):
         residual = input_extra_tensors[self.residual_key]
@@ -174,7 +178,16 @@ class ParallelDropoutOp(RopalaModule):
         p = self.hidden_dropout if self.training else 0.0
         seed = self._seed + 7919 * self._calls
         self._calls += 1
-        out = BiasDropoutAddFn.apply(input_tensors["output_tensor"], bias, residual, p, seed)
+        ln_op = self.fused_layernorm_op
+        if ln_op is not None and not profiling:
+            # one pass also normalizes the output for the next op's LayerNorm,
+            # which takes the result from the tensor
+            ln = ln_op.input_layernorm
+            out, y, mean, rstd = BiasDropoutAddLayerNormFn.apply(input_tensors["output_tensor"], bias, residual, p,
+                                                                 seed, ln)
+            out._eth_ln_fwd = (ln.weight, ln.bias, ln.eps, y, mean, rstd)
+        else:
+            out = BiasDropoutAddFn.apply(input_tensors["output_tensor"], bias, residual, p, seed)
         if not profiling:
             input_extra_tensors.pop("output_bias")
             input_extra_tensors.pop(self.residual_key)

@@ -162,7 +162,15 @@ class LayerNormResidualFn(torch.autograd.Function):
     def forward(ctx, x, gamma, beta, eps):
         ctx.set_materialize_grads(False)
         xc = x.contiguous()
-        y, mean, rstd = K.layer_norm_fwd(_flat(xc), gamma, beta, eps)
+        pre = getattr(x, "_eth_ln_fwd", None)
+        if pre is not None:
+            # the bias-dropout-add that made x already normalized it for this
+            # LayerNorm (BiasDropoutAddLayerNormFn): taken once
+            del x._eth_ln_fwd
+        if pre is not None and pre[0] is gamma and pre[1] is beta and pre[2] == eps:
+            y, mean, rstd = pre[3], pre[4], pre[5]
+        else:
+            y, mean, rstd = K.layer_norm_fwd(_flat(xc), gamma, beta, eps)
         ctx.save_for_backward(xc, gamma, beta, mean, rstd)
         ctx.colsum = x.grad_fn is not None
         return y.view(x.shape), x.view_as(x)
@@ -234,25 +242,56 @@ class BiasDropoutAddFn(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, dout):
-        (bias,) = ctx.saved_tensors
-        part = getattr(dout, "_eth_colsum_part", None) if ctx.p == 0 else None
-        dout = dout.contiguous()
-        dx = K.dropout_bwd(_flat(dout), ctx.p, ctx.seed).view(dout.shape) if ctx.p > 0 else dout
-        db = None
-        if ctx.needs_input_grad[1]:
-            mg, accumulate = _fp32_accum_target(bias)
-            target = mg if mg is not None else torch.empty(bias.shape, dtype=torch.float32, device=bias.device)
-            if part is not None:
-                # column sums already produced by the LayerNorm backward that
-                # made dout (p == 0: dx is dout)
-                K.reduce_partials(part, target, accumulate=accumulate)
-            else:
-                K.col_sum(_flat(dx), target, accumulate=accumulate)
-            if mg is None:
-                db = target.to(bias.dtype)
-            else:
-                grad_written(bias)
-        return dx, db, dout, None, None
+        return _bias_dropout_add_bwd(ctx, dout)
+
+
+class BiasDropoutAddLayerNormFn(torch.autograd.Function):
+    """BiasDropoutAddFn whose output the next op normalizes with `ln` (its
+    LayerNorm module): one kernel also produces that LayerNorm's output,
+    mean and rstd, returned as non-differentiable outputs for
+    LayerNormResidualFn to take over, so the LayerNorm does not read h back.
+    Gradients are BiasDropoutAddFn's; the LayerNorm keeps its own node."""
+
+    @staticmethod
+    def forward(ctx, x, bias, residual, p, seed, ln):
+        # no zero tensors for the gradients of y, mean, rstd: they have none
+        ctx.set_materialize_grads(False)
+        h, y, mean, rstd = K.bias_dropout_add_layer_norm_fwd(
+            _flat(x.contiguous()), bias, _flat(residual.contiguous()), ln.weight, ln.bias, p=p, seed=seed,
+            eps=ln.eps)
+        ctx.p, ctx.seed = p, seed
+        ctx.save_for_backward(bias)
+        ctx.mark_non_differentiable(y, mean, rstd)
+        return h.view(x.shape), y.view(x.shape), mean, rstd
+
+    @staticmethod
+    def backward(ctx, dout, _dy, _dmean, _drstd):
+        if dout is None:
+            return None, None, None, None, None, None
+        return (*_bias_dropout_add_bwd(ctx, dout), None)
+
+
+def _bias_dropout_add_bwd(ctx, dout):
+    """Gradients of residual + dropout(x + b) for (x, bias, residual, p, seed)."""
+    (bias,) = ctx.saved_tensors
+    part = getattr(dout, "_eth_colsum_part", None) if ctx.p == 0 else None
+    dout = dout.contiguous()
+    dx = K.dropout_bwd(_flat(dout), ctx.p, ctx.seed).view(dout.shape) if ctx.p > 0 else dout
+    db = None
+    if ctx.needs_input_grad[1]:
+        mg, accumulate = _fp32_accum_target(bias)
+        target = mg if mg is not None else torch.empty(bias.shape, dtype=torch.float32, device=bias.device)
+        if part is not None:
+            # column sums already produced by the LayerNorm backward that
+            # made dout (p == 0: dx is dout)
+            K.reduce_partials(part, target, accumulate=accumulate)
+        else:
+            K.col_sum(_flat(dx), target, accumulate=accumulate)
+        if mg is None:
+            db = target.to(bias.dtype)
+        else:
+            grad_written(bias)
+    return dx, db, dout, None, None
 
 
 class SplitQKVFn(torch.autograd.Function):

@@ -132,9 +132,18 @@ class MiddleStageTrainer:
         if overlap_optimizer:
             # the update of layer l overlaps the next step's forward of the
             # layers before it (one AdamW launch per layer, in forward order)
+            # (a LayerNorm whose forward runs inside the preceding
+            # bias-dropout-add -- the next layer's first LayerNorm -- updates
+            # with that op's layer, so the fused kernel waits for no later part)
+            runs_in = {}
+            for op in self.model.language_model.ops:
+                ln_op = getattr(op, "fused_layernorm_op", None)
+                if ln_op is not None:
+                    runs_in[id(ln_op)] = op
             by_layer = {}
             for op in self.model.language_model.ops:
-                by_layer.setdefault((op.op_index - 1) // 10, []).extend(op.parameters())
+                owner = runs_in.get(id(op), op)
+                by_layer.setdefault((owner.op_index - 1) // 10, []).extend(op.parameters())
             self.optimizer.overlap_with_next_forward([by_layer[k] for k in sorted(by_layer)])
         # buckets synced during the backward, as soon as their gradients
         # exist (train_step(streamed_sync=True))

@@ -230,6 +230,18 @@ int eth_ln_bwd_residual(const void* dy, const void* x, const float* mean, const 
                         const void* gamma, const void* dresid, void* dx, float* dgamma,
                         float* dbeta, float* colsum_part, float* workspace, int64_t rows,
                         int64_t cols, int accumulate, int dtype, void* stream);
+/* The bias-dropout-add that ends a sub-block and the LayerNorm that starts
+ * the next, in one pass over the rows: h = residual + dropout(x + b, p,
+ * seed) is stored exactly as eth_bias_dropout_add_fwd stores it (same mask),
+ * and y, mean, rstd are eth_ln_fwd of the stored h, bit for bit; h is not
+ * read back from HBM.  Replaces the op pair enc-post-attention-dropout ->
+ * enc-2nd-layernorm (and enc-post-MLP-dropout -> the next layer's
+ * enc-1st-layernorm): bias_dropout_add (flex_ops.py:104-134) followed by
+ * MixedFusedLayerNorm's forward_affine (model/fused_layer_norm.py:62-89). */
+int eth_bda_ln_fwd(const void* x, const void* bias, const void* residual, void* h,
+                   const void* gamma, const void* beta, void* y, float* mean, float* rstd,
+                   int64_t rows, int64_t cols, float p, uint64_t seed, float eps, int dtype,
+                   void* stream);
 
 /* ------------------------------------------------------------------------
  * Elementwise ops of the GPT block ([rows, cols] row-major, cols % 8 == 0).

@@ -260,3 +260,25 @@ def test_bias_dropout_add_and_col_sum(cuda, dtype):
     keep_bwd = dxp.cpu().float() != 0
     assert torch.all(keep_bwd[kept])  # every element kept forward is kept backward
     assert 0.70 < keep_bwd.float().mean().item() < 0.80
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("rows,cols,p", [(4099, 2048, 0.0), (300, 1032, 0.1), (33, 8192, 0.0), (5, 8, 0.3),
+                                         (257, 4096, 0.1)])
+def test_bias_dropout_add_layer_norm_matches_the_two_kernels(cuda, dtype, rows, cols, p):
+    """eth_bda_ln_fwd against eth_bias_dropout_add_fwd followed by eth_ln_fwd
+    on the same inputs: h, y, mean and rstd bit for bit (same dropout mask,
+    same LayerNorm arithmetic on the stored h)."""
+    announce(f"bias-dropout-add + LayerNorm fused, {dtype} {rows}x{cols} p={p}")
+    gen = torch.Generator().manual_seed(rows + cols)
+    x = _rand((rows, cols), dtype, gen).to(cuda)
+    b = _rand((cols,), dtype, gen).to(cuda)
+    r = _rand((rows, cols), dtype, gen).to(cuda)
+    g = (1.0 + 0.1 * torch.randn(cols, generator=gen)).to(dtype).to(cuda)
+    be = (0.1 * torch.randn(cols, generator=gen)).to(dtype).to(cuda)
+    h, y, mean, rstd = K.bias_dropout_add_layer_norm_fwd(x, b, r, g, be, p=p, seed=77, eps=1e-5)
+    h_ref = K.bias_dropout_add_fwd(x, b, r, p=p, seed=77)
+    y_ref, mean_ref, rstd_ref = K.layer_norm_fwd(h_ref, g, be, 1e-5)
+    assert torch.equal(h.view(torch.int16), h_ref.view(torch.int16))
+    assert torch.equal(y.view(torch.int16), y_ref.view(torch.int16))
+    assert torch.equal(mean, mean_ref) and torch.equal(rstd, rstd_ref)

@@ -201,3 +201,50 @@ def test_middle_stage_training_step(cuda):
         got = tr.optimizer.optimizer_parameter_for_model_parameter(p).detach().cpu().numpy()
         np.testing.assert_allclose(got, ref_p, rtol=1e-6, atol=1e-9)
         np.testing.assert_array_equal(p.detach().float().cpu().numpy(), oadam.to_bf16(got))
+
+
+@pytest.mark.parametrize("dropout", [0.0, 0.1])
+def test_fused_dropout_layernorm_pairs_match_the_separate_ops(cuda, dropout):
+    """Each bias-dropout-add followed in the stage by a LayerNorm runs as one
+    kernel (BiasDropoutAddLayerNormFn) whose LayerNorm result the next op
+    takes over.  With the pairs undone the stage gives the same output, input
+    gradient and main grads bit for bit, with and without dropout (same mask
+    from the same per-call seed)."""
+    from eth_amd.model.flex_ops import ParallelDropoutOp
+
+    announce(f"fused dropout+LayerNorm pairs vs separate ops, p={dropout}")
+    cfg = GPTConfig(hidden_size=256, num_attention_heads=4, ffn_hidden_size=1024, num_layers=2,
+                    seq_length=128, micro_batch_size=2, params_dtype=torch.bfloat16, device="cuda", seed=51,
+                    hidden_dropout=dropout)
+    tr = MiddleStageTrainer(cfg, lr=1e-4, weight_decay=0.1, clip_grad=1.0)
+    ops = list(tr.model.language_model.ops)
+    drops = [op for op in ops if isinstance(op, ParallelDropoutOp)]
+    paired = {id(op): op.fused_layernorm_op for op in drops}
+    # post-attention -> 2nd LN in both layers, post-MLP of layer 0 -> layer 1's 1st LN; the last
+    # dropout ends the stage
+    assert sum(v is not None for v in paired.values()) == 3 and drops[-1].fused_layernorm_op is None
+    # the LayerNorm stays registered once: no parameter reached through the pairing
+    names = [n for n, _ in tr.model.named_parameters()]
+    assert not any("fused_layernorm_op" in n for n in names)
+    gen = torch.Generator().manual_seed(8)
+    x = torch.randn(128, 2, 256, generator=gen).to(torch.bfloat16).to(cuda)
+    dy = (torch.randn(128, 2, 256, generator=gen) * 1e-2).to(torch.bfloat16).to(cuda)
+    (buf,) = tr.ddp.grad_buffers.values()
+    calls = {id(op): op._calls for op in drops}
+
+    def run():
+        for op in drops:
+            op._calls = calls[id(op)]
+        tr.ddp.zero_grad_buffer()
+        out, dx = tr.forward_backward(x, dy)
+        torch.cuda.synchronize()
+        return out.clone(), dx.clone(), buf.data.clone()
+
+    fused = run()
+    for op in drops:
+        object.__setattr__(op, "fused_layernorm_op", None)
+    separate = run()
+    for op in drops:
+        object.__setattr__(op, "fused_layernorm_op", paired[id(op)])
+    for a, b in zip(fused, separate):
+        assert torch.equal(a, b)
