@@ -558,6 +558,7 @@ def main():
         "ms_per_step": ms,
         "step_ms_median": percentile(step_ms, 0.5),
         "step_ms_p90": percentile(step_ms, 0.9),
+        "step_ms": [round(v, 3) for v in step_ms],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
