@@ -30,12 +30,31 @@ from .flex_ops import GPTConfig, ParallelDropoutOp, ParallelLayerNormOp, build_g
 _SEGMENT_BREAK = "enc-1st-layernorm"
 
 
+# a pending overlapped update of the parameters of op i + _UPDATE_LEAD is
+# issued when op i is about to run: a layer's update then starts as the layer
+# before it reaches its MLP products and overlaps GEMMs, not attention
+_UPDATE_LEAD = 5
+
+
+def launch_updates(op):
+    """Issue the not yet launched parts of an overlapped update that write
+    op's parameters (an optimizer step leaves `_eth_update_launch` on them)."""
+    for p in op.parameters():
+        launch = getattr(p, "_eth_update_launch", None)
+        if launch is not None:
+            launch()
+
+
 def await_parameters(op):
     """Make the current stream wait for the pending update of op's
     parameters (an optimizer step overlapped with this forward leaves its
-    events on them), once per event."""
+    events on them), once per event; a part not launched yet is launched
+    first, since a wait on an event not yet recorded waits for nothing."""
     seen = set()
     for p in op.parameters():
+        launch = getattr(p, "_eth_update_launch", None)
+        if launch is not None:
+            launch()
         ev = getattr(p, "_eth_ready_event", None)
         if ev is not None:
             if id(ev) not in seen:
@@ -51,6 +70,13 @@ def _await_op(op):
     ln_op = getattr(op, "fused_layernorm_op", None)
     if ln_op is not None:
         await_parameters(ln_op)
+
+
+def _launch_op_updates(op):
+    launch_updates(op)
+    ln_op = getattr(op, "fused_layernorm_op", None)
+    if ln_op is not None:
+        launch_updates(ln_op)
 
 
 def _rng_state(ops):
@@ -206,12 +232,17 @@ class FlexPipeModel(nn.Module):
     def forward(self, inputs, input_extra_tensors):
         output_extra_tensors = {}
         hidden = inputs if self.pre_process else self.input_tensor
+        ops = self.ops
         if not any(self.recompute_ops):
-            for op in self.ops:
+            for i, op in enumerate(ops):
+                if i + _UPDATE_LEAD < len(ops):
+                    _launch_op_updates(ops[i + _UPDATE_LEAD])
                 _await_op(op)
                 hidden = op(hidden, input_extra_tensors, output_extra_tensors)
         else:
             for start, end, ckpt in self.segments():
+                if start + _UPDATE_LEAD < len(ops):
+                    _launch_op_updates(ops[start + _UPDATE_LEAD])
                 if ckpt:
                     hidden = self._checkpointed(start, end, hidden, input_extra_tensors, output_extra_tensors)
                 else:

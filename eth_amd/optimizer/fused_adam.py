@@ -139,10 +139,14 @@ class FusedAdamW(torch.optim.Optimizer):
 
     # ----------------------------------------------------------------- step --
     @torch.no_grad()
-    def step(self, closure=None, stats=None, found_inf=None):
+    def step(self, closure=None, stats=None, found_inf=None, deferred=False):
         """One AdamW step.  `stats` (device double[3], clip coefficient at
         index 2) and `found_inf` (device float[1]) are optional; with
-        found_inf set to non-zero the launch leaves every tensor unchanged."""
+        found_inf set to non-zero the launch leaves every tensor unchanged.
+        With `deferred` (a partitioned optimizer) nothing is launched yet:
+        launch_part(k) later issues part k, on the stream step() ran on, and
+        records part_events[k] after it; a wait on an event must come after
+        its part's launch."""
         loss = closure() if closure is not None else None
         params = self._all_params()
         if not params:
@@ -158,31 +162,40 @@ class FusedAdamW(torch.optim.Optimizer):
         # all parameters step together; the state mirrors torch's per-param step
         step = int(self.state[params[0]]["step"].item()) + 1
         device = params[0].device
-        self.part_events = []
-        for ttab, ctab, n_chunks in self._tables:
-            if n_chunks:
-                nat.call(
-                    "eth_adam_step",
-                    nat.ptr(ttab),
-                    nat.ptr(ctab),
-                    n_chunks,
-                    float(beta1),
-                    float(beta2),
-                    float(eps),
-                    step,
-                    self._model_dtype,
-                    nat.ptr(stats),
-                    nat.ptr(found_inf),
-                    nat.stream_ptr(device),
-                )
-            if self._partition:
-                ev = torch.cuda.Event()
-                ev.record(torch.cuda.current_stream(device))
-                self.part_events.append(ev)
+        if deferred and not self._partition:
+            raise ValueError("a deferred step needs a partition (set_partition)")
+        self._launch_stream = torch.cuda.current_stream(device)
+        self._launches = [
+            (nat.ptr(ttab), nat.ptr(ctab), n_chunks, float(beta1), float(beta2), float(eps), step,
+             self._model_dtype, nat.ptr(stats), nat.ptr(found_inf), nat.stream_ptr(device))
+            if n_chunks else None
+            for ttab, ctab, n_chunks in self._tables
+        ]
+        self._launched = [False] * len(self._launches)
+        self.part_events = [torch.cuda.Event() for _ in self._launches] if self._partition else []
+        if not deferred:
+            for k in range(len(self._launches)):
+                self.launch_part(k)
         self._pending_step = step
         if found_inf is None:
             self.commit_step(True)
         return loss
+
+    def launch_part(self, k):
+        """Issue part k of the last step(), once (every part when the
+        optimizer is not partitioned), on the stream step() ran on."""
+        if self._launched[k]:
+            return
+        self._launched[k] = True
+        args = self._launches[k]
+        if args is not None:
+            nat.call("eth_adam_step", *args)
+        if self._partition:
+            self.part_events[k].record(self._launch_stream)
+
+    def launch_all(self):
+        for k in range(len(getattr(self, "_launches", ()))):
+            self.launch_part(k)
 
     def commit_step(self, applied=True):
         """Advance the per-parameter step counters after a launched step

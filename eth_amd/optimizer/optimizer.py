@@ -1,3 +1,4 @@
+import functools
 """Megatron optimizer wrappers on the fused HIP path.
 
 Step contract of eth/runtime/megatron/optimizer/optimizer.py:493-531:
@@ -55,6 +56,7 @@ class MegatronOptimizer:
         self._model_to_optimizer_param = {}
         self._host_flags = None
         self._overlap = None  # (side stream, [[model params] per part]) when the update overlaps the next forward
+        self._unlaunched_parts = set()  # parts of a deferred overlapped update not issued yet
         self._post_sync = (None, 0)  # chunk table of norm-owned gradients summed after the sync
 
     # ----------------------------------------------------------- plumbing --
@@ -112,11 +114,27 @@ class MegatronOptimizer:
         self.optimizer.set_partition(parts)
         self._overlap = (torch.cuda.Stream(device=dev), [list(part) for part in model_param_parts])
 
+    def launch_update_part(self, k):
+        """Issue part k of a deferred overlapped update (once) on the side
+        stream, behind everything queued on the current stream so far."""
+        side, model_parts = self._overlap
+        if k not in self._unlaunched_parts:
+            return
+        self._unlaunched_parts.discard(k)
+        for p in model_parts[k]:
+            p._eth_update_launch = None
+        side.wait_stream(torch.cuda.current_stream(self._device()))
+        with torch.cuda.stream(side):
+            self.optimizer.launch_part(k)
+
     def join_overlapped_update(self):
-        """Make the current stream wait for every part of an overlapped update
-        that no forward op has waited for yet."""
+        """Issue the parts of an overlapped update not launched yet and make
+        the current stream wait for every part that no forward op has waited
+        for yet."""
         if self._overlap is None:
             return
+        for k in sorted(self._unlaunched_parts):
+            self.launch_update_part(k)
         stream = torch.cuda.current_stream(self._device())
         for part in self._overlap[1]:
             for p in part:
@@ -276,16 +294,25 @@ class MegatronOptimizer:
                 found_inf=st.found_inf if scaler is not None else None,
             )
         else:
+            # every part's launch is prepared now and issued later: the first
+            # layer's at once, each later one when the next forward is a few
+            # ops before it (launch_update_part), so the updates overlap the
+            # forward's GEMMs rather than its attention
             side, model_parts = self._overlap
             side.wait_stream(torch.cuda.current_stream(self._device()))
             with torch.cuda.stream(side):
                 self.optimizer.step(
                     stats=st.stats if need_norm else None,
                     found_inf=st.found_inf if scaler is not None else None,
+                    deferred=True,
                 )
-            for part, ev in zip(model_parts, self.optimizer.part_events):
+            self._unlaunched_parts = set(range(len(model_parts)))
+            for k, (part, ev) in enumerate(zip(model_parts, self.optimizer.part_events)):
+                launch = functools.partial(self.launch_update_part, k)
                 for p in part:
                     p._eth_ready_event = ev
+                    p._eth_update_launch = launch
+            self.launch_update_part(0)
         if host is not None:
             host[1].synchronize()
         if scaler is not None:

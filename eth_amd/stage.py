@@ -37,6 +37,8 @@ def save_stage_snapshot(trainer, output_dir, phase, iteration, metrics=None, clo
     with the reference's record layout (training.py:720-808 gathers the same
     three optimizer maps through the optimizer's model-parameter accessors)."""
     opt = trainer.optimizer
+    # an overlapped update still pending is issued and waited for first
+    opt.join_overlapped_update()
     state, master, hyper = {}, {}, {}
     for b in trainer.bindings:
         st = opt.state_for_model_parameter(b.parameter)

@@ -290,6 +290,9 @@ def test_update_overlapped_with_the_next_forward_is_bit_identical(cuda):
         out_o, dx_o, ok_o, n_o = over.train_step(x, dy)
         assert ok_p and ok_o and n_p == n_o
         assert torch.equal(out_p, out_o) and torch.equal(dx_p, dx_o)
+    # the later layers' updates are launched by the next forward; a reader
+    # of the parameters before it joins the update
+    over.optimizer.join_overlapped_update()
     torch.cuda.synchronize()
     for (n1, p1), (n2, p2) in zip(plain.model.named_parameters(), over.model.named_parameters()):
         assert torch.equal(p1, p2), n1
