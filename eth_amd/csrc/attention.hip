@@ -21,10 +21,11 @@
 // stored in LDS with bits 2 and 3 of the row index swapped, which makes the
 // MFMA result layout of S^T equal to the operand layout of P^T in
 // O^T = V^T P^T, so P never leaves registers.  The dK/dV kernel uses the
-// mirror image (S = Q K^T, lane = key, query rows swizzled); dQ has its own
-// kernel (recomputing P), so no atomics are needed and results are
-// deterministic.  The dQ kernel runs first and also writes
-// delta = rowsum(dO * O), which the dK/dV kernels read.
+// mirror image (S = Q K^T, lane = key, query rows swizzled) and computes S
+// and P once for both gradients, in pairs of waves that hand P over through
+// LDS; dQ has its own kernel (recomputing P), so no atomics are needed and
+// results are deterministic.  The dQ kernel runs first and also writes
+// delta = rowsum(dO * O), which the dK/dV kernel reads.
 //
 // Tiles arrive through buffer loads (fixed per-thread offsets, a scalar row
 // advance).  Operands that an MFMA needs transposed (V for O^T = V^T P^T, K
@@ -150,14 +151,19 @@ struct BufTile {
   a_rsrc_t rs;
   int32_t row_bytes;
   int rows_left;  // tensor rows (sequence length); rows past it load zeros
+  int tid;        // this thread's index among the kAttnThreads that move the tile
   // columns at or past hd load zeros (an out-of-range offset)
   __device__ __forceinline__ void init(const AttnTensor& t, int b, int h, int seq, int hd) {
+    init(t, b, h, seq, hd, threadIdx.x);
+  }
+  __device__ __forceinline__ void init(const AttnTensor& t, int b, int h, int seq, int hd, int thread) {
+    tid = thread;
     rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(t.p), (short)0, (int)t.bytes, 0x00020000);
     row_bytes = (int32_t)(t.ss * 2);
     rows_left = seq;
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
-      const int c = threadIdx.x + i * kAttnThreads;
+      const int c = tid + i * kAttnThreads;
       voff[i] = !PAD || (c % CPR) * 8 < hd
                     ? (int32_t)(((int64_t)b * t.sb + (int64_t)h * t.sh + (int64_t)(c / CPR) * t.ss + (c % CPR) * 8) * 2)
                     : kAttnOob;
@@ -166,7 +172,7 @@ struct BufTile {
   __device__ __forceinline__ void load(int r0) {
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
-      const int c = threadIdx.x + i * kAttnThreads;
+      const int c = tid + i * kAttnThreads;
       const int32_t off = !PAD || r0 + c / CPR < rows_left ? voff[i] : kAttnOob;
       v[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, off, r0 * row_bytes, 0);
     }
@@ -174,7 +180,7 @@ struct BufTile {
   __device__ __forceinline__ void store(uint16_t* lds) const {
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
-      const int c = threadIdx.x + i * kAttnThreads;
+      const int c = tid + i * kAttnThreads;
       const int r = SWZ ? swz(c / CPR) : c / CPR;
       *reinterpret_cast<a_u32x4*>(lds + r * LROW + (c % CPR) * 8) = v[i];
     }
@@ -184,7 +190,7 @@ struct BufTile {
   __device__ __forceinline__ void store_natural(uint16_t* lds) const {
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
-      const int c = threadIdx.x + i * kAttnThreads;
+      const int c = tid + i * kAttnThreads;
       *reinterpret_cast<a_u32x4*>(lds + (c / CPR) * L2 + (c % CPR) * 8) = v[i];
     }
   }
@@ -367,135 +373,150 @@ __global__ void __launch_bounds__(kAttnThreads, 2) attn_fwd_kernel(AttnArgs a) {
   if (hl == 0) a.lse[(int64_t)bh * a.S + q] = m + log2f(l);
 }
 
-// ------------------------------------------------------- backward: dK, dV --
-// PART 1: dV only, 2: dK only, 3: both.  Split, each part fits two
-// workgroups per CU (the fused kernel needs K, V fragments and both
-// accumulators live and runs one); splitting recomputes S once more.
-template <int D, bool FP16, int PART, bool PAD>
-__global__ void __launch_bounds__(kAttnThreads, PART == 3 ? 1 : 2) attn_bwd_dkdv_kernel(AttnArgs a) {
+// ------------------------------------------------ backward: dK, dV paired --
+// Eight waves: wave w < 4 (the dV wave) and wave w + 4 (the dK wave) own the
+// same 32 keys and share a SIMD.  Per step of 64 queries the dV wave computes
+// S = Q K^T and P and hands P (fp32) to its partner through LDS; the dK wave
+// meanwhile computes dP = dO V^T.  After the hand-over the dV wave adds
+// P^T dO into dV while the dK wave forms dS = P (dP - delta) and adds
+// dS^T Q into dK.  S and P are computed once per step (the split dV and dK
+// kernels each recompute them), and on every SIMD one wave's exponentials or
+// dS arithmetic overlap the other wave's MFMAs.  S = Q K^T is computed with
+// lane = key (the mirror image of the forward's layout, query rows swizzled),
+// so P and dS are already the A operands of dV += P^T dO and dK += dS^T Q.
+template <int D, bool FP16, bool PAD>
+__global__ void __launch_bounds__(2 * kAttnThreads, 1) attn_bwd_dkdv_pair_kernel(AttnArgs a) {
   constexpr int KS = D / 16, DT = D / 32;
-  constexpr bool DV = PART & 1, DK = PART & 2;
-  // Q (and dO) rows swizzled for S (and dP); the B operands of dV += P^T dO
-  // and dK += dS^T Q come from natural-order copies padded to D + 32
-  // through transposing reads
   constexpr int QN = tr_row(D);
   __shared__ __attribute__((aligned(16))) uint16_t Qs[kBQ2 * (D + 8)];
-  __shared__ __attribute__((aligned(16))) uint16_t dOs[DK ? kBQ2 * (D + 8) : 8];
-  __shared__ __attribute__((aligned(16))) uint16_t Qn[DK ? kBQ2 * QN : 8];
-  __shared__ __attribute__((aligned(16))) uint16_t dOn[DV ? kBQ2 * QN : 8];
+  __shared__ __attribute__((aligned(16))) uint16_t dOs[kBQ2 * (D + 8)];
+  __shared__ __attribute__((aligned(16))) uint16_t Qn[kBQ2 * QN];
+  __shared__ __attribute__((aligned(16))) uint16_t dOn[kBQ2 * QN];
+  // P of a step's two 32-query tiles per key group: registers 4g..4g+3 of a
+  // lane as 16 contiguous bytes, the 64 lanes side by side
+  __shared__ a_u32x4 Ps[4][2][4][64];
   __shared__ float lse_s[kBQ2], del_s[kBQ2];
 
   const int BH = a.B * a.H;
   const int bh = blockIdx.x % BH, kb = blockIdx.x / BH;
   const int b = bh / a.H, h = bh % a.H;
   const int lane = threadIdx.x & 63, hl = lane >> 5;
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+  const int w = wv & 3;
+  const bool dkw = wv >= 4;                        // the dK wave of its pair
+  const int rt = threadIdx.x & (kAttnThreads - 1);  // thread index within the role
   const int k0 = kb * kBKV2 + w * 32;
   const int key = k0 + (lane & 31);
 
-  uint4 kf[KS], vf[KS];
+  // B operands of the first product: K rows (S = Q K^T) in the dV wave, V
+  // rows (dP = dO V^T) in the dK wave
+  uint4 kf[KS];
   {
-    const uint16_t* kp = row_ptr(a.k, key, b, h);
-    const uint16_t* vp = row_ptr(a.v, key, b, h);
+    const uint16_t* kp = row_ptr(dkw ? a.v : a.k, key, b, h);
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      kf[ks] = load_row16<PAD>(kp, key < a.S, ks * 16 + hl * 8, a.hd);
-      if constexpr (DK) vf[ks] = load_row16<PAD>(vp, key < a.S, ks * 16 + hl * 8, a.hd);
-    }
+    for (int ks = 0; ks < KS; ++ks) kf[ks] = load_row16<PAD>(kp, key < a.S, ks * 16 + hl * 8, a.hd);
   }
-  a_f32x16 dk[DT], dv[DT];
+  a_f32x16 acc[DT];  // dV in the dV wave, dK in the dK wave
 #pragma unroll
   for (int t = 0; t < DT; ++t)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) dk[t][r] = dv[t][r] = 0.f;
+    for (int r = 0; r < 16; ++r) acc[t][r] = 0.f;
 
-  BufTile<kBQ2, D, D + 8, true, PAD> qt, dt;
-  qt.init(a.q, b, h, a.S, a.hd);
-  dt.init(a.dout, b, h, a.S, a.hd);
+  // the dV waves move the Q rows, the dK waves the dO rows; the next step's
+  // rows, and its queries' lse (dV) or delta (dK), load during this step
+  BufTile<kBQ2, D, D + 8, true, PAD> tile;
+  tile.init(dkw ? a.dout : a.q, b, h, a.S, a.hd, rt);
   const int qtr = tr_lane(lane, QN);
   const int first = (kb * kBKV2) / kBQ2, nq = (a.S + kBQ2 - 1) / kBQ2;
-  // the next step's Q / dO rows, and its queries' lse and delta, are loaded
-  // while this step computes; a padding query gets lse = 1e30, so P = 0
-  float lse_n = 0.f, del_n = 0.f;
+  float stat_n = 0.f;
   auto load_stats = [&](int qs) __attribute__((always_inline)) {
-    if (threadIdx.x < kBQ2) {
-      const bool real = !PAD || qs + (int)threadIdx.x < a.S;
-      lse_n = real ? a.lse[(int64_t)bh * a.S + qs + threadIdx.x] : 1e30f;
-      if constexpr (DK) del_n = real ? a.delta[(int64_t)bh * a.S + qs + threadIdx.x] : 0.f;
+    if (rt < kBQ2) {
+      const bool real = !PAD || qs + rt < a.S;  // a padding query gets lse = 1e30, so P = 0
+      const int64_t i = (int64_t)bh * a.S + qs + rt;
+      stat_n = dkw ? (real ? a.delta[i] : 0.f) : (real ? a.lse[i] : 1e30f);
     }
   };
-  qt.load(first * kBQ2);
-  dt.load(first * kBQ2);
+  tile.load(first * kBQ2);
   load_stats(first * kBQ2);
   for (int qb = first; qb < nq; ++qb) {
     const int qs0 = qb * kBQ2;
     __syncthreads();  // previous step's LDS readers are done
-    qt.store(Qs);
-    if constexpr (DK) {
-      qt.template store_natural<QN>(Qn);
-      dt.store(dOs);
-    }
-    if constexpr (DV) dt.template store_natural<QN>(dOn);
-    if (threadIdx.x < kBQ2) {
-      lse_s[threadIdx.x] = lse_n;
-      if constexpr (DK) del_s[threadIdx.x] = del_n;
+    if (dkw) {
+      tile.store(dOs);
+      tile.template store_natural<QN>(dOn);
+      if (rt < kBQ2) del_s[rt] = stat_n;
+    } else {
+      tile.store(Qs);
+      tile.template store_natural<QN>(Qn);
+      if (rt < kBQ2) lse_s[rt] = stat_n;
     }
     __syncthreads();
     if (qb + 1 < nq) {
-      qt.load(qs0 + kBQ2);
-      dt.load(qs0 + kBQ2);
+      tile.load(qs0 + kBQ2);
       load_stats(qs0 + kBQ2);
     }
-    if (qs0 + kBQ2 - 1 < k0) continue;  // every query of the step precedes this wave's keys
+    // a pair whose keys all follow every query of the step skips the work
+    // but not the barriers
+    const bool active = qs0 + kBQ2 - 1 >= k0;
     const bool diag = qs0 < k0 + 31;
-    // one 32-query tile at a time: S = Q K^T and dP = dO V^T (lane = key),
-    // then dV += P^T dO and dK += dS^T Q over those 32 queries
+    a_f32x16 x[2];  // S, then P (dV wave); dP, then dS (dK wave)
+    if (active) {
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      a_f32x16 s, dp;
+      for (int t = 0; t < 2; ++t) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) s[r] = dp[r] = 0.f;
-      const uint16_t* qp = Qs + (t * 32 + (lane & 31)) * (D + 8) + hl * 8;
-      const uint16_t* op = dOs + (t * 32 + (lane & 31)) * (D + 8) + hl * 8;
+        for (int r = 0; r < 16; ++r) x[t][r] = 0.f;
+        const uint16_t* ap = (dkw ? dOs : Qs) + (t * 32 + (lane & 31)) * (D + 8) + hl * 8;
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        s = mma<FP16>(*reinterpret_cast<const uint4*>(qp + ks * 16), kf[ks], s);
-        if constexpr (DK) dp = mma<FP16>(*reinterpret_cast<const uint4*>(op + ks * 16), vf[ks], dp);
+        for (int ks = 0; ks < KS; ++ks) x[t] = mma<FP16>(*reinterpret_cast<const uint4*>(ap + ks * 16), kf[ks], x[t]);
+        if (!dkw) {
+          // P; query index of register r = t*32 + swz_row(r, hl); the causal
+          // mask only on the steps that cross the diagonal
+          auto probs = [&](auto masked) __attribute__((always_inline)) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int qi = t * 32 + swz_row(r, hl);
+              float p = fast_exp2(__builtin_fmaf(x[t][r], a.scale_log2, -lse_s[qi]));
+              if (decltype(masked)::value && key > qs0 + qi) p = 0.f;
+              x[t][r] = p;
+            }
+          };
+          if (diag)
+            probs(std::true_type{});
+          else
+            probs(std::false_type{});
+#pragma unroll
+          for (int g = 0; g < 4; ++g)
+            Ps[w][t][g][lane] = a_u32x4{__float_as_uint(x[t][4 * g]), __float_as_uint(x[t][4 * g + 1]),
+                                        __float_as_uint(x[t][4 * g + 2]), __float_as_uint(x[t][4 * g + 3])};
+        }
       }
-      // P and dS (fp32); query index of register r = t*32 + swz_row(r, hl).
-      // The causal mask is applied only on the steps that cross the
-      // diagonal (a wave-uniform branch): elsewhere its compares and selects
-      // would cost more VALU time than the exponentials.
-      auto probs = [&](auto masked) __attribute__((always_inline)) {
+    }
+    __syncthreads();  // P handed over
+    if (active) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int qi = t * 32 + swz_row(r, hl);
-          float p = fast_exp2(__builtin_fmaf(s[r], a.scale_log2, -lse_s[qi]));
-          if (decltype(masked)::value && key > qs0 + qi) p = 0.f;
-          s[r] = p;
-          if constexpr (DK) dp[r] = p * (dp[r] - del_s[qi]);
+      for (int t = 0; t < 2; ++t) {
+        if (dkw) {
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const a_u32x4 pv = Ps[w][t][g][lane];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int r = 4 * g + e;
+              const float p = __uint_as_float(pv[e]);
+              x[t][r] = p * (x[t][r] - del_s[t * 32 + swz_row(r, hl)]);
+            }
+          }
         }
-      };
-      if (diag)
-        probs(std::true_type{});
-      else
-        probs(std::false_type{});
+        // dV += P^T dO (dV wave) or dK += dS^T Q (dK wave) over the tile's
+        // 32 queries, two k-steps of 16
+        const uint16_t* bp = (dkw ? Qn : dOn) + qtr;
 #pragma unroll
-      for (int k2 = 0; k2 < 2; ++k2) {
-        const int kk = t * 2 + k2, e0 = k2 * 8;
-        if constexpr (DV) {
-          const uint4 pa = make_uint4(pack2<FP16>(s[e0 + 0], s[e0 + 1]), pack2<FP16>(s[e0 + 2], s[e0 + 3]),
-                                      pack2<FP16>(s[e0 + 4], s[e0 + 5]), pack2<FP16>(s[e0 + 6], s[e0 + 7]));
-          const uint16_t* dop = dOn + qtr + kk * 16 * QN;
+        for (int k2 = 0; k2 < 2; ++k2) {
+          const int kk = t * 2 + k2, e0 = k2 * 8;
+          const uint4 pa = make_uint4(pack2<FP16>(x[t][e0 + 0], x[t][e0 + 1]), pack2<FP16>(x[t][e0 + 2], x[t][e0 + 3]),
+                                      pack2<FP16>(x[t][e0 + 4], x[t][e0 + 5]), pack2<FP16>(x[t][e0 + 6], x[t][e0 + 7]));
 #pragma unroll
-          for (int d2 = 0; d2 < DT; ++d2) dv[d2] = mma<FP16>(pa, tr_frag(dop + d2 * 32, QN), dv[d2]);
-        }
-        if constexpr (DK) {
-          const uint4 sa = make_uint4(pack2<FP16>(dp[e0 + 0], dp[e0 + 1]), pack2<FP16>(dp[e0 + 2], dp[e0 + 3]),
-                                      pack2<FP16>(dp[e0 + 4], dp[e0 + 5]), pack2<FP16>(dp[e0 + 6], dp[e0 + 7]));
-          const uint16_t* qtp = Qn + qtr + kk * 16 * QN;
-#pragma unroll
-          for (int d2 = 0; d2 < DT; ++d2) dk[d2] = mma<FP16>(sa, tr_frag(qtp + d2 * 32, QN), dk[d2]);
+          for (int d2 = 0; d2 < DT; ++d2) acc[d2] = mma<FP16>(pa, tr_frag(bp + kk * 16 * QN + d2 * 32, QN), acc[d2]);
         }
       }
     }
@@ -508,8 +529,10 @@ __global__ void __launch_bounds__(kAttnThreads, PART == 3 ? 1 : 2) attn_bwd_dkdv
       const int kr = k0 + acc_row(r, hl);
       const int d = t * 32 + (lane & 31);
       if (PAD && (kr >= a.S || d >= a.hd)) continue;
-      if constexpr (DK) row_ptr(a.dk, kr, b, h)[d] = from_f<FP16>(dk[t][r] * a.scale);
-      if constexpr (DV) row_ptr(a.dv, kr, b, h)[d] = from_f<FP16>(dv[t][r]);
+      if (dkw)
+        row_ptr(a.dk, kr, b, h)[d] = from_f<FP16>(acc[t][r] * a.scale);
+      else
+        row_ptr(a.dv, kr, b, h)[d] = from_f<FP16>(acc[t][r]);
     }
 }
 
@@ -766,8 +789,7 @@ extern "C" int eth_attn_bwd(const eth_attn_desc_t* d, const void* q, const void*
   const bool pad = a.S % kBKV2 != 0 || a.hd != width;
 #define ETH_ATTN_BWD_P(D, F, P)                                                  \
   attn_bwd_dq_kernel<D, F, P><<<g_q, kAttnThreads, 0, s>>>(a);                 \
-  attn_bwd_dkdv_kernel<D, F, 1, P><<<g_kv, kAttnThreads, 0, s>>>(a);           \
-  attn_bwd_dkdv_kernel<D, F, 2, P><<<g_kv, kAttnThreads, 0, s>>>(a);
+  attn_bwd_dkdv_pair_kernel<D, F, P><<<g_kv, 2 * kAttnThreads, 0, s>>>(a);
 #define ETH_ATTN_BWD(D, F)        \
   if (pad) {                      \
     ETH_ATTN_BWD_P(D, F, true)    \

@@ -57,6 +57,10 @@ class MegatronOptimizer:
         self._host_flags = None
         self._overlap = None  # (side stream, [[model params] per part]) when the update overlaps the next forward
         self._unlaunched_parts = set()  # parts of a deferred overlapped update not issued yet
+        # parts of a deferred update issued by step() itself, before the host
+        # waits for the read-back: the GPU work queued while the host returns
+        # and starts the next forward
+        self.eager_update_parts = 3
         self._post_sync = (None, 0)  # chunk table of norm-owned gradients summed after the sync
 
     # ----------------------------------------------------------- plumbing --
@@ -312,7 +316,8 @@ class MegatronOptimizer:
                 for p in part:
                     p._eth_ready_event = ev
                     p._eth_update_launch = launch
-            self.launch_update_part(0)
+            for k in range(min(self.eager_update_parts, len(model_parts))):
+                self.launch_update_part(k)
         if host is not None:
             host[1].synchronize()
         if scaler is not None:
