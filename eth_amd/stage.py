@@ -136,17 +136,24 @@ class MiddleStageTrainer:
             # layers before it (one AdamW launch per layer, in forward order)
             # (a LayerNorm whose forward runs inside the preceding
             # bias-dropout-add -- the next layer's first LayerNorm -- updates
-            # with that op's layer, so the fused kernel waits for no later part)
+            # with that op's layer, so the fused kernel waits for no later part).
+            # The stage's first layer updates in two parts, its attention half
+            # (ops 1-6 of the layer) and its MLP half, so that only the first
+            # precedes the forward and the second runs under its attention.
+            ops = self.model.language_model.ops
             runs_in = {}
-            for op in self.model.language_model.ops:
+            for op in ops:
                 ln_op = getattr(op, "fused_layernorm_op", None)
                 if ln_op is not None:
                     runs_in[id(ln_op)] = op
-            by_layer = {}
-            for op in self.model.language_model.ops:
+            first_layer = (ops[0].op_index - 1) // 10
+            parts = {}
+            for op in ops:
                 owner = runs_in.get(id(op), op)
-                by_layer.setdefault((owner.op_index - 1) // 10, []).extend(op.parameters())
-            self.optimizer.overlap_with_next_forward([by_layer[k] for k in sorted(by_layer)])
+                layer = (owner.op_index - 1) // 10
+                mlp_half = layer == first_layer and (owner.op_index - 1) % 10 >= 6
+                parts.setdefault((layer, mlp_half), []).extend(op.parameters())
+            self.optimizer.overlap_with_next_forward([parts[k] for k in sorted(parts)])
         # buckets synced during the backward, as soon as their gradients
         # exist (train_step(streamed_sync=True))
         self._streamed = None
