@@ -290,6 +290,10 @@ class MegatronOptimizer:
         # before the update kernel, so it waits for the statistics only, not
         # for the update (the next step's launches overlap the update)
         host = None
+        if self._overlap is not None:
+            # the overlapped update needs the statistics on the device, not
+            # the copies to the host queued next
+            self._overlap[0].wait_stream(torch.cuda.current_stream(self._device()))
         if st is not None and (need_norm or scaler is not None):
             host = self._read_back(st)
         if self._overlap is None:
@@ -303,7 +307,6 @@ class MegatronOptimizer:
             # ops before it (launch_update_part), so the updates overlap the
             # forward's GEMMs rather than its attention
             side, model_parts = self._overlap
-            side.wait_stream(torch.cuda.current_stream(self._device()))
             with torch.cuda.stream(side):
                 self.optimizer.step(
                     stats=st.stats if need_norm else None,

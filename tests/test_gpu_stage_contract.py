@@ -273,6 +273,32 @@ def test_trainer_evidence_snapshot_and_runtime_record(cuda, tmp_path):
         assert set(r["optimizer_hyperparameters"]) == {"beta1", "beta2", "epsilon", "weight_decay"}
 
 
+def test_snapshot_after_an_overlapped_update_sees_the_updated_parameters(cuda, tmp_path):
+    """With the update overlapped, a step leaves the later layers' AdamW
+    launches to the next forward; a post_step snapshot taken before that
+    forward issues and waits for them, so it records the parameters, fp32
+    masters and AdamW moments of the in-line update bit for bit."""
+    announce("snapshot after an overlapped update")
+    gen = torch.Generator().manual_seed(31)
+    plain = MiddleStageTrainer(_cfg(layers=3))
+    over = MiddleStageTrainer(_cfg(layers=3), overlap_optimizer=True)
+    _randomize(plain, gen)
+    _copy_weights(plain, over)
+    x, dy = _inputs(gen)
+    plain.train_step(x, dy)
+    over.train_step(x, dy)
+    snaps = [load_rank_snapshot(tr.record_evidence(tmp_path / name, "post_step", 1))
+             for name, tr in (("plain", plain), ("over", over))]
+    torch.cuda.synchronize()
+    assert len(snaps[0]["records"]) == len(snaps[1]["records"]) > 0
+    for r0, r1 in zip(snaps[0]["records"], snaps[1]["records"]):
+        assert r0["descriptor"]["logical_param_id"] == r1["descriptor"]["logical_param_id"]
+        for key in ("parameter", "optimizer_parameter"):
+            assert torch.equal(r0[key], r1[key]), (key, r0["descriptor"]["logical_param_id"])
+        for key in ("exp_avg", "exp_avg_sq"):
+            assert torch.equal(r0["optimizer_state"][key], r1["optimizer_state"][key]), key
+
+
 def test_update_overlapped_with_the_next_forward_is_bit_identical(cuda):
     """AdamW on a side stream, one launch per layer, each layer's next
     forward waiting only for its own weights: three steps give the outputs,
