@@ -409,7 +409,7 @@ def gemm_layer_products(torch, reps=10):
             "layer_tflops": 3 * 2.0 * T * (H * 3 * H + H * H + 2 * H * FFN) / tot / 1e6}
 
 
-def first_last_stage(torch, steps=5, warmup=2):
+def first_last_stage(torch, steps=5, warmup=2, overlap_optimizer=True):
     """the GPT-6.7B first+last stage in fp16 -- token +
     position embedding, 2 layers (hidden 4096, 32 heads, FFN 16384), final
     LN, tied LM head over the padded vocabulary (50304) and vocab cross
@@ -423,7 +423,8 @@ def first_last_stage(torch, steps=5, warmup=2):
     cfg = GPTConfig(hidden_size=h, num_attention_heads=heads, ffn_hidden_size=f, num_layers=layers, seq_length=s,
                     micro_batch_size=b, padded_vocab_size=V, params_dtype=torch.float16, device="cuda", seed=1234)
     tr = FirstLastStageTrainer(cfg, lr=1e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, clip_grad=1.0,
-                               bucket_cap_bytes=32 << 20, initial_loss_scale=2.0**16)
+                               bucket_cap_bytes=32 << 20, initial_loss_scale=2.0**16,
+                               overlap_optimizer=overlap_optimizer)
     for i in range(warmup):
         if i == warmup - 1:  # the freeze before the last warm-up step (see main)
             torch.cuda.synchronize()
@@ -492,7 +493,7 @@ def main():
     from eth_amd.stage import MiddleStageTrainer
 
     if args.first_last_only:
-        fl = first_last_stage(torch, steps=args.steps, warmup=args.warmup)
+        fl = first_last_stage(torch, steps=args.steps, warmup=args.warmup, overlap_optimizer=not args.inline_update)
         print(json.dumps({"first_last_stage": fl}), flush=True)
         return
     if args.hbm_only:
@@ -612,7 +613,7 @@ def main():
     if not args.no_hbm_path:
         result["hbm_path"] = hbm_path(torch)
     if not args.no_first_last:
-        result["first_last_stage"] = first_last_stage(torch)
+        result["first_last_stage"] = first_last_stage(torch, overlap_optimizer=not args.inline_update)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(torch)
     print(json.dumps(result), flush=True)

@@ -132,28 +132,7 @@ class MiddleStageTrainer:
             # 16-bit main grads are widened and unscaled by the optimizer
             self.optimizer.bind_gradient_sync(self.grad_sync.executor)
         if overlap_optimizer:
-            # the update of layer l overlaps the next step's forward of the
-            # layers before it (one AdamW launch per layer, in forward order)
-            # (a LayerNorm whose forward runs inside the preceding
-            # bias-dropout-add -- the next layer's first LayerNorm -- updates
-            # with that op's layer, so the fused kernel waits for no later part).
-            # The stage's first layer updates in two parts, its attention half
-            # (ops 1-6 of the layer) and its MLP half, so that only the first
-            # precedes the forward and the second runs under its attention.
-            ops = self.model.language_model.ops
-            runs_in = {}
-            for op in ops:
-                ln_op = getattr(op, "fused_layernorm_op", None)
-                if ln_op is not None:
-                    runs_in[id(ln_op)] = op
-            first_layer = (ops[0].op_index - 1) // 10
-            parts = {}
-            for op in ops:
-                owner = runs_in.get(id(op), op)
-                layer = (owner.op_index - 1) // 10
-                mlp_half = layer == first_layer and (owner.op_index - 1) % 10 >= 6
-                parts.setdefault((layer, mlp_half), []).extend(op.parameters())
-            self.optimizer.overlap_with_next_forward([parts[k] for k in sorted(parts)])
+            self.optimizer.overlap_with_next_forward(update_parts(self.model.language_model.ops))
         # buckets synced during the backward, as soon as their gradients
         # exist (train_step(streamed_sync=True))
         self._streamed = None
@@ -305,6 +284,34 @@ class MiddleStageTrainer:
         return [layers[k] for k in sorted(layers)]
 
 
+def update_parts(ops):
+    """Parameters of a stage's ops in the parts an overlapped AdamW update
+    launches, in the order the next forward reads them: one part per
+    transformer layer (ops before the first layer, such as the embedding,
+    form one part; ops after the last, such as the final LayerNorm and the
+    LM head, belong to the last layer's index and form the last part).  A
+    LayerNorm whose forward runs inside the preceding bias-dropout-add (the
+    next layer's first LayerNorm) updates with that op's layer, so the fused
+    kernel waits for no later part.  The first transformer layer updates in
+    two parts, its attention half (ops 1-6 of the layer) and its MLP half,
+    so that only the first precedes its forward and the second runs under
+    its attention."""
+    runs_in = {}
+    for op in ops:
+        ln_op = getattr(op, "fused_layernorm_op", None)
+        if ln_op is not None:
+            runs_in[id(ln_op)] = op
+    layers = [(op.op_index - 1) // 10 for op in ops]
+    first_layer = max(0, min(layers))
+    parts = {}
+    for op in ops:
+        owner = runs_in.get(id(op), op)
+        layer = (owner.op_index - 1) // 10
+        mlp_half = layer == first_layer and (owner.op_index - 1) % 10 >= 6
+        parts.setdefault((layer, mlp_half), []).extend(op.parameters())
+    return [parts[k] for k in sorted(parts) if parts[k]]
+
+
 class FirstLastStageTrainer:
     """A stage holding the whole GPT model (embedding, layers, final LN, LM
     head + cross entropy) on one rank: BASELINE configs[0] (fp32 plumbing
@@ -312,7 +319,8 @@ class FirstLastStageTrainer:
 
     def __init__(self, cfg: GPTConfig, lr=1e-4, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01, clip_grad=1.0,
                  sync_mode="block", bucket_cap_bytes=1024 * 1024, initial_loss_scale=2.0**16, unpadded_vocab=50257,
-                 recompute_ops=None, runtime_evidence_dir=None, accumulate_allreduce_grads_in_fp32=True):
+                 recompute_ops=None, runtime_evidence_dir=None, accumulate_allreduce_grads_in_fp32=True,
+                 overlap_optimizer=False):
         self.cfg = cfg
         self.unpadded_vocab = unpadded_vocab
         n_ops = 10 * cfg.num_layers + 3
@@ -342,6 +350,11 @@ class FirstLastStageTrainer:
             self.optimizer.bind_gradient_sync(
                 self.grad_sync.executor,
                 resynced=[self.embedding.word_embeddings.weight, self.post.word_embeddings.weight])
+        if overlap_optimizer:
+            # the update of each part overlaps the next step's forward up to
+            # that part's first op; the tied head copy, read last, updates
+            # under the whole forward
+            self.optimizer.overlap_with_next_forward(update_parts(ops))
         self.nominal = float(cfg.micro_batch_size * cfg.seq_length)
 
     def forward_backward(self, sample_ids, labels=None, nominal=None):
@@ -365,6 +378,7 @@ class FirstLastStageTrainer:
     def train_step(self, sample_ids, labels=None):
         self.ddp.zero_grad_buffer(defer=True)
         losses, lo = self.forward_backward(sample_ids, labels)
+        self.optimizer.join_overlapped_update()
         self.ddp.settle_grad_buffer()
         self.grad_sync.execute(global_normalization_scale(self.nominal, lo.local_loss_weight))
         self.tie_gradients()
@@ -387,6 +401,7 @@ class FirstLastStageTrainer:
             l, lo = self.forward_backward(ids, lab, nominal=nominal)
             losses.append(l)
             outs.append(lo)
+        self.optimizer.join_overlapped_update()
         self.ddp.settle_grad_buffer()
         numerator, weight = sum_loss_outputs(outs)
         self.grad_sync.execute(global_normalization_scale(nominal, weight))

@@ -283,6 +283,32 @@ def test_c5_full_shape_trains(cuda):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_first_last_update_overlapped_with_the_next_forward_is_bit_identical(cuda, dtype):
+    """The first+last stage with its AdamW update split into parts
+    (embedding; the first layer's attention and MLP halves; the next layer;
+    the final LayerNorm with the tied head copy) launched under the next
+    forward: three steps give the losses, norms and parameters of the in-line
+    update bit for bit, and the tied copies stay equal."""
+    announce(f"first+last overlapped update {dtype}")
+    cfg = GPTConfig(hidden_size=256, num_attention_heads=4, ffn_hidden_size=1024, num_layers=2, seq_length=128,
+                    micro_batch_size=2, padded_vocab_size=50304, params_dtype=dtype, device="cuda", seed=13)
+    kw = dict(lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01, clip_grad=0.05, initial_loss_scale=1024.0)
+    plain, over = FirstLastStageTrainer(cfg, **kw), FirstLastStageTrainer(cfg, overlap_optimizer=True, **kw)
+    assert len(over.optimizer._overlap[1]) == 5
+    for step in range(3):
+        ids = [3 + step, 8 + step]
+        l_p, _, ok_p, n_p = plain.train_step(ids)
+        l_o, _, ok_o, n_o = over.train_step(ids)
+        assert ok_p and ok_o and n_p == n_o, (step, n_p, n_o)
+        assert torch.equal(l_p, l_o), step
+    over.optimizer.join_overlapped_update()
+    torch.cuda.synchronize()
+    for (n1, p1), (_, p2) in zip(plain.model.named_parameters(), over.model.named_parameters()):
+        assert torch.equal(p1, p2), n1
+    assert torch.equal(over.embedding.word_embeddings.weight, over.post.word_embeddings.weight)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_first_last_fused_statistics_match_the_standalone_pass(cuda, dtype):
     """The first+last stage unscales in the sync's unpack and takes the tied
     root's norm share after the tied sum: the step's norm, outcome and
