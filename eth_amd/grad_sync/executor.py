@@ -97,8 +97,13 @@ class GradientStatistics:
         self.n_partials_used = n_partials
         self.fresh = False
         self.inv_scale_used = None
+        # called before the buffers are rewritten: an update still reading
+        # the previous step's values is issued and waited for first
+        self.before_reuse = None
 
     def reset(self):
+        if self.before_reuse is not None:
+            self.before_reuse()
         nat.call("eth_fill_f32", nat.ptr(self.found_inf), 1, 0.0, nat.stream_ptr(self.device))
 
     def finalize(self, max_norm):

@@ -57,6 +57,7 @@ class MegatronOptimizer:
         self._host_flags = None
         self._overlap = None  # (side stream, [[model params] per part]) when the update overlaps the next forward
         self._unlaunched_parts = set()  # parts of a deferred overlapped update not issued yet
+        self._join_pending = False  # an overlapped update not yet joined by the current stream
         # parts of a deferred update issued by step() itself, before the host
         # waits for the read-back: the GPU work queued while the host returns
         # and starts the next forward
@@ -135,8 +136,9 @@ class MegatronOptimizer:
         """Issue the parts of an overlapped update not launched yet and make
         the current stream wait for every part that no forward op has waited
         for yet."""
-        if self._overlap is None:
+        if self._overlap is None or not self._join_pending:
             return
+        self._join_pending = False
         for k in sorted(self._unlaunched_parts):
             self.launch_update_part(k)
         stream = torch.cuda.current_stream(self._device())
@@ -175,6 +177,7 @@ class MegatronOptimizer:
         self._post_sync = (nat.table_to_device(table, self._device()) if len(table) else None, len(table))
         self._executor = executor
         self._statistics = GradientStatistics(executor.n_partials + len(table), self._device())
+        self._statistics.before_reuse = self.join_overlapped_update
         executor.bind_statistics(self._statistics)
         executor.set_inv_loss_scale(self._inv_scale())
 
@@ -314,6 +317,7 @@ class MegatronOptimizer:
                     deferred=True,
                 )
             self._unlaunched_parts = set(range(len(model_parts)))
+            self._join_pending = True
             for k, (part, ev) in enumerate(zip(model_parts, self.optimizer.part_events)):
                 launch = functools.partial(self.launch_update_part, k)
                 for p in part:

@@ -299,6 +299,32 @@ def test_snapshot_after_an_overlapped_update_sees_the_updated_parameters(cuda, t
             assert torch.equal(r0["optimizer_state"][key], r1["optimizer_state"][key]), key
 
 
+def test_a_sync_and_step_without_a_forward_issue_the_pending_update_first(cuda):
+    """A step leaves its last layers' AdamW parts for the next forward.  If
+    a gradient sync and another step follow without a forward (the sync
+    resets the found-inf flag and the step rewrites the clip coefficient the
+    pending parts read), the parts are issued and waited for before the
+    statistics are reused: the parameters match the in-line update's."""
+    announce("sync and step without a forward after an overlapped update")
+    gen = torch.Generator().manual_seed(37)
+    plain = MiddleStageTrainer(_cfg(layers=3))
+    over = MiddleStageTrainer(_cfg(layers=3), overlap_optimizer=True)
+    assert over.optimizer.eager_update_parts < len(over.optimizer._overlap[1])
+    _randomize(plain, gen)
+    _copy_weights(plain, over)
+    x, dy = _inputs(gen)
+    for tr in (plain, over):
+        tr.train_step(x, dy)
+    for tr in (plain, over):
+        tr.grad_sync.execute(0.5)
+        ok, _, _ = tr.optimizer.step()
+        assert ok
+    over.optimizer.join_overlapped_update()
+    torch.cuda.synchronize()
+    for (n1, p1), (_, p2) in zip(plain.model.named_parameters(), over.model.named_parameters()):
+        assert torch.equal(p1, p2), n1
+
+
 def test_update_overlapped_with_the_next_forward_is_bit_identical(cuda):
     """AdamW on a side stream, one launch per layer, each layer's next
     forward waiting only for its own weights: three steps give the outputs,
