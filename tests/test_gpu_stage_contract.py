@@ -325,6 +325,41 @@ def test_a_sync_and_step_without_a_forward_issue_the_pending_update_first(cuda):
         assert torch.equal(p1, p2), n1
 
 
+@pytest.mark.parametrize("mode", ["recompute", "microbatches"])
+def test_overlapped_update_with_recompute_and_microbatches(cuda, mode):
+    """The overlapped update under activation recompute (each checkpointed
+    segment waits for its parameters, in the forward and again in its
+    replay) and under two microbatches per step (the first microbatch's
+    forward waits for every part): three steps match the in-line update of
+    the same trainer bit for bit."""
+    announce(f"overlapped update with {mode}")
+    gen = torch.Generator().manual_seed(41)
+    kw = {"recompute_ops": ([0] + [1] * 6 + [0] * 3) * 3} if mode == "recompute" else {}
+    plain = MiddleStageTrainer(_cfg(layers=3), **kw)
+    over = MiddleStageTrainer(_cfg(layers=3), overlap_optimizer=True, **kw)
+    _randomize(plain, gen)
+    _copy_weights(plain, over)
+    for _ in range(3):
+        if mode == "recompute":
+            x, dy = _inputs(gen)
+            out_p, dx_p, ok_p, n_p = plain.train_step(x, dy)
+            out_o, dx_o, ok_o, n_o = over.train_step(x, dy)
+            assert torch.equal(out_p, out_o) and torch.equal(dx_p, dx_o)
+        else:
+            mbs = [{"input_tensors": {"hidden_states": x}, "output_grads": {"hidden_states": dy}}
+                   for x, dy in (_inputs(gen) for _ in range(2))]
+            res_p, ok_p, n_p = plain.train_step_microbatches(mbs)
+            res_o, ok_o, n_o = over.train_step_microbatches(mbs)
+            for rp, ro in zip(res_p, res_o):
+                assert torch.equal(rp[0]["hidden_states"], ro[0]["hidden_states"])
+                assert torch.equal(rp[2]["hidden_states"], ro[2]["hidden_states"])
+        assert ok_p and ok_o and n_p == n_o
+    over.optimizer.join_overlapped_update()
+    torch.cuda.synchronize()
+    for (n1, p1), (_, p2) in zip(plain.model.named_parameters(), over.model.named_parameters()):
+        assert torch.equal(p1, p2), n1
+
+
 def test_update_overlapped_with_the_next_forward_is_bit_identical(cuda):
     """AdamW on a side stream, one launch per layer, each layer's next
     forward waiting only for its own weights: three steps give the outputs,
