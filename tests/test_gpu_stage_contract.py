@@ -361,10 +361,11 @@ def test_overlapped_update_with_recompute_and_microbatches(cuda, mode):
 
 
 def test_update_overlapped_with_the_next_forward_is_bit_identical(cuda):
-    """AdamW on a side stream, one launch per layer, each layer's next
-    forward waiting only for its own weights: three steps give the outputs,
-    input gradients, norms and parameters of the in-line update bit for
-    bit."""
+    """AdamW on a side stream, one launch per part (a layer; the first
+    layer in two halves), the later parts issued by the next forward a few
+    ops before their first use and every op waiting only for its own
+    weights: three steps give the outputs, input gradients, norms and
+    parameters of the in-line update bit for bit."""
     announce("optimizer update overlapped with the next forward")
     gen = torch.Generator().manual_seed(12)
     plain = MiddleStageTrainer(_cfg(layers=3))
