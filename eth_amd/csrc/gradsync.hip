@@ -296,10 +296,27 @@ __global__ void __launch_bounds__(kReducePartialsThreads)
   }
 }
 
-__global__ void fill_kernel(float* dst, int64_t n, float v) {
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
-       i += (int64_t)gridDim.x * blockDim.x)
-    dst[i] = v;
+// dst[0, n) = v: up to three scalars to the first 16-byte boundary, then
+// kFillVec nontemporal 16-byte stores per thread in one trip (short
+// workgroups keep HBM busy), then the scalar tail; workgroup 0 writes the
+// scalars
+constexpr int kFillThreads = 256, kFillVec = 4;
+typedef float ff32x4_t __attribute__((ext_vector_type(4)));
+__global__ void __launch_bounds__(kFillThreads) fill_kernel(float* dst, int64_t n, float v) {
+  const int64_t head = min(n, (int64_t)(((16 - ((uintptr_t)dst & 15)) & 15) / 4));
+  const int64_t nv = (n - head) / 4;
+  ff32x4_t* dv = reinterpret_cast<ff32x4_t*>(dst + head);
+  const ff32x4_t x = {v, v, v, v};
+  const int64_t i0 = (int64_t)blockIdx.x * (kFillThreads * kFillVec) + threadIdx.x;
+#pragma unroll
+  for (int u = 0; u < kFillVec; ++u) {
+    const int64_t i = i0 + u * kFillThreads;
+    if (i < nv) __builtin_nontemporal_store(x, dv + i);
+  }
+  if (blockIdx.x == 0) {
+    if (threadIdx.x < head) dst[threadIdx.x] = v;
+    for (int64_t i = head + nv * 4 + threadIdx.x; i < n; i += kFillThreads) dst[i] = v;
+  }
 }
 
 }  // namespace eth
@@ -328,9 +345,10 @@ int eth_reduce_partials(const float* part, int64_t groups, int64_t cols, int64_t
 int eth_fill_f32(float* dst, int64_t n, float value, void* stream) {
   ETH_CHECK_ARG(n >= 0 && (n == 0 || dst), "eth_fill_f32: bad arguments");
   if (n == 0) return ETH_OK;
-  int64_t blocks = (n + 255) / 256;
-  if (blocks > 4096) blocks = 4096;
-  fill_kernel<<<(int)blocks, 256, 0, (hipStream_t)stream>>>(dst, n, value);
+  int64_t blocks = (n / 4 + kFillThreads * kFillVec - 1) / (kFillThreads * kFillVec);
+  if (blocks < 1) blocks = 1;  // the scalars alone
+  ETH_CHECK_ARG(blocks < (1LL << 31), "eth_fill_f32: too many elements (%lld)", (long long)n);
+  fill_kernel<<<(int)blocks, kFillThreads, 0, (hipStream_t)stream>>>(dst, n, value);
   ETH_CHECK_LAUNCH("eth_fill_f32");
   return ETH_OK;
 }

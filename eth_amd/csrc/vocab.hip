@@ -256,20 +256,42 @@ __global__ void __launch_bounds__(kXentThreads) xent_bwd_kernel(const uint16_t* 
     }
 }
 
-// a = b = a + b over n fp32 elements (tied-embedding gradient sum)
-__global__ void tied_sum_kernel(float* __restrict__ a, float* __restrict__ b, int64_t n) {
+// a = b = a + b over n fp32 elements (tied-embedding gradient sum).  One
+// trip per thread over kTiedVec 16-byte vectors of each operand, all loads
+// in flight before the adds, nontemporal (each byte is touched once here):
+// many short workgroups keep HBM busier than a grid-stride loop.
+constexpr int kTiedThreads = 256, kTiedVec = 2;
+typedef float tf32x4_t __attribute__((ext_vector_type(4)));
+__global__ void __launch_bounds__(kTiedThreads) tied_sum_kernel(float* __restrict__ a, float* __restrict__ b,
+                                                                int64_t n) {
   const int64_t nv = n / 4;
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < nv; i += (int64_t)gridDim.x * blockDim.x) {
-    float4 x = reinterpret_cast<float4*>(a)[i], y = reinterpret_cast<const float4*>(b)[i];
-    x.x += y.x; x.y += y.y; x.z += y.z; x.w += y.w;
-    reinterpret_cast<float4*>(a)[i] = x;
-    reinterpret_cast<float4*>(b)[i] = x;
+  tf32x4_t* av = reinterpret_cast<tf32x4_t*>(a);
+  tf32x4_t* bv = reinterpret_cast<tf32x4_t*>(b);
+  const int64_t i0 = (int64_t)blockIdx.x * (kTiedThreads * kTiedVec) + threadIdx.x;
+  tf32x4_t x[kTiedVec], y[kTiedVec];
+#pragma unroll
+  for (int u = 0; u < kTiedVec; ++u) {
+    const int64_t i = i0 + u * kTiedThreads;
+    if (i < nv) {
+      x[u] = __builtin_nontemporal_load(av + i);
+      y[u] = __builtin_nontemporal_load(bv + i);
+    }
   }
-  for (int64_t i = nv * 4 + blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
-    const float v = a[i] + b[i];
-    a[i] = v;
-    b[i] = v;
+#pragma unroll
+  for (int u = 0; u < kTiedVec; ++u) {
+    const int64_t i = i0 + u * kTiedThreads;
+    if (i < nv) {
+      const tf32x4_t v = x[u] + y[u];
+      __builtin_nontemporal_store(v, av + i);
+      __builtin_nontemporal_store(v, bv + i);
+    }
   }
+  if (blockIdx.x == 0)  // the last n % 4 elements
+    for (int64_t i = nv * 4 + threadIdx.x; i < n; i += kTiedThreads) {
+      const float v = a[i] + b[i];
+      a[i] = v;
+      b[i] = v;
+    }
 }
 
 // the same over 16-bit gradients: the sum is formed in fp32 and rounded
@@ -291,10 +313,10 @@ extern "C" int eth_tied_grad_sum(float* root, float* copy, int64_t n, void* stre
   ETH_CHECK_ARG((((uintptr_t)root) & 15) == 0 && (((uintptr_t)copy) & 15) == 0,
                 "eth_tied_grad_sum: buffers must be 16-byte aligned");
   if (n == 0) return ETH_OK;
-  int64_t blocks = (n / 4 + 255) / 256;
-  if (blocks > 8192) blocks = 8192;
-  if (blocks < 1) blocks = 1;
-  tied_sum_kernel<<<(int)blocks, 256, 0, (hipStream_t)stream>>>(root, copy, n);
+  int64_t blocks = (n / 4 + kTiedThreads * kTiedVec - 1) / (kTiedThreads * kTiedVec);
+  if (blocks < 1) blocks = 1;  // the scalar tail alone
+  ETH_CHECK_ARG(blocks < (1LL << 31), "eth_tied_grad_sum: too many elements (%lld)", (long long)n);
+  tied_sum_kernel<<<(int)blocks, kTiedThreads, 0, (hipStream_t)stream>>>(root, copy, n);
   ETH_CHECK_LAUNCH("eth_tied_grad_sum");
   return ETH_OK;
 }

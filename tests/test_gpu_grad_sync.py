@@ -295,3 +295,20 @@ def test_local_pass_rejects_a_bad_entry_before_launching(cuda):
                  None, None, nat.stream_ptr(cuda))
     torch.cuda.synchronize()
     assert bool((ex.scratch(name) == -7.0).all())
+
+
+@pytest.mark.parametrize("n", [1, 2, 3, 4, 5, 7, 8, 1023, 1024 * 4 + 3, 1 << 20, (1 << 20) + 5])
+def test_fill_every_alignment_and_length(cuda, n):
+    """eth_fill_f32 writes exactly [0, n) at each 4-byte offset from a 16-byte
+    boundary (a scalar head, 16-byte stores, a scalar tail) and nothing either
+    side of it."""
+    from eth_amd import _native as nat
+
+    for off in range(4):
+        announce(f"fill n={n} offset={off}")
+        buf = torch.full((n + 16,), -1.0, dtype=torch.float32, device=cuda)
+        view = buf[off:off + n]
+        nat.call("eth_fill_f32", nat.ptr(view), n, 2.5, nat.stream_ptr(cuda))
+        host = buf.cpu()
+        assert torch.all(host[off:off + n] == 2.5)
+        assert torch.all(host[:off] == -1.0) and torch.all(host[off + n:] == -1.0)
