@@ -17,7 +17,7 @@ ETH_OK, ETH_ERR_INVALID, ETH_ERR_HIP = 0, 1, 2
 ETH_F32, ETH_F16, ETH_BF16 = 0, 1, 2
 
 CHUNK_ELEMS = 16384
-CHUNK_NORM = 1
+CHUNK_NORM, CHUNK_SHADOWED = 1, 2
 UNPACK_WRITEBACK, UNPACK_UNSCALE, UNPACK_STATS = 1, 2, 4
 
 # struct eth_chunk (40 bytes)

@@ -134,6 +134,7 @@ __global__ void __launch_bounds__(kThreads) unpack_kernel(const eth_chunk_t* __r
                                                           int64_t partial_base) {
   __shared__ float red[kThreads / 64];
   const eth_chunk_t c = chunks[blockIdx.x];
+  if (c.flags & ETH_CHUNK_SHADOWED) flags &= ~ETH_UNPACK_WRITEBACK;
   T* dstp = reinterpret_cast<T*>(c.src);
   T* pay = payload + c.dst;
   const int64_t n = (int64_t)c.rows * c.row_len;

@@ -266,7 +266,17 @@ class GradientBucketExecutor:
     def _build_tables(self):
         tables = []
         partial_base = 0
-        for bucket in self._rank_buckets():
+        buckets = list(self._rank_buckets())
+        # payload prefix of each scratch buffer that a later bucket of the pass
+        # (in plan order) packs over: the normalization write-back of chunks
+        # inside it is overwritten unread, so the unpack skips it and a pass
+        # still leaves the scratch exactly as the reference's payload.mul_ does
+        covered = [0] * len(buckets)
+        reach = {}
+        for i in range(len(buckets) - 1, -1, -1):
+            covered[i] = reach.get(buckets[i].grad_dtype, 0)
+            reach[buckets[i].grad_dtype] = max(covered[i], buckets[i].exact_numel)
+        for bucket, shadow in zip(buckets, covered):
             entries = []
             for placement in bucket.placements:
                 fragment = self._fragments[placement.fragment_id]
@@ -289,6 +299,8 @@ class GradientBucketExecutor:
                     copied += n
                 if copied != fragment.numel:
                     raise self._bucket_error(bucket, f"packed {copied} elements, expected {fragment.numel}", binding)
+            entries = [ent[:6] + (ent[6] | nat.CHUNK_SHADOWED,) if ent[1] + ent[3] * ent[4] <= shadow else ent
+                       for ent in entries]
             table = chunk_table(entries)
             dev = nat.table_to_device(table, self._device) if len(table) else None
             tables.append((bucket, dev, len(table), partial_base))

@@ -11,7 +11,9 @@ stream (default priority) that first waits for the streams that wrote the
 gradients.  Buckets whose parameters received no gradient are zero-settled
 and synced at the end.  The per-bucket work is exactly executor.run_bucket,
 so the payloads, main grads and statistics are those of execute(); only the
-time they are computed at moves.  What it overlaps with the backward is the
+time they are computed at moves.  (The scratch a streamed pass leaves behind
+can differ where a plan-order pass would have packed over a chunk, whose
+normalization write-back the unpack skips; nothing reads it.)  What it overlaps with the backward is the
 all-reduce seam's communication; the local pack/unpack memory traffic itself
 competes with the backward's kernels (on one GPU it costs the GEMMs about
 what it hides).

@@ -48,10 +48,14 @@ typedef struct eth_chunk {
   int32_t rows;        /* rows in the chunk (1 for a contiguous run) */
   int32_t row_len;     /* contiguous elements per row */
   float scale;         /* LocalFragmentBindingSpec.contribution_scale */
-  int32_t flags;       /* ETH_CHUNK_NORM: counts toward the optimizer L2 norm */
+  int32_t flags;       /* ETH_CHUNK_NORM | ETH_CHUNK_SHADOWED */
 } eth_chunk_t;
 
-#define ETH_CHUNK_NORM 1
+#define ETH_CHUNK_NORM 1     /* counts toward the optimizer L2 norm */
+#define ETH_CHUNK_SHADOWED 2 /* a later bucket of the same pass packs over this
+                              * chunk's payload range: its unpack skips the
+                              * ETH_UNPACK_WRITEBACK store, which nothing could
+                              * read before it is overwritten */
 
 /* Pack: payload[dst + i] = src[i] * scale (the multiply is skipped when
  * scale == 1, so the copy is bit-exact).
@@ -62,7 +66,8 @@ int eth_bucket_pack(const eth_chunk_t* chunks, int64_t n_chunks, void* payload,
 
 /* Unpack after the bucket's all-reduce:
  *   v = payload[i] * normalization_scale       (skipped when == 1)
- *   if (flags & ETH_UNPACK_WRITEBACK) payload[i] = v
+ *   if (flags & ETH_UNPACK_WRITEBACK) payload[i] = v  (not in ETH_CHUNK_SHADOWED
+ *                                                      chunks)
  *   g = v * inv_loss_scale                      (only with ETH_UNPACK_UNSCALE)
  *   src[i] = g;  found_inf |= !isfinite(v);  partials[chunk] = sum g^2 over
  *   ETH_CHUNK_NORM chunks (only with ETH_UNPACK_STATS).

@@ -104,6 +104,49 @@ def test_scratch_reuse_leaves_short_bucket_tail(cuda):
     assert seen == rec["expected_numels"]
 
 
+@pytest.mark.parametrize("large_first", [True, False])
+@pytest.mark.parametrize("local", [True, False])
+def test_normalized_pass_leaves_the_reference_scratch(cuda, large_first, local):
+    """With a normalization scale the reference multiplies each bucket's
+    payload in place before its unpack (executor.py:247-261), so a pass
+    leaves the scratch holding, at every offset, the normalized payload of
+    the last bucket reaching it.  The unpack skips the write-back of chunks a
+    later bucket packs over; the scratch a pass leaves is still exactly that
+    (8- and 4-element buckets in both orders, both seams)."""
+    announce(f"grad_sync normalized scratch, large_first={large_first} local={local}")
+    group = ProcessGroupSpec("pg", (0,), "gradient_sync")
+    order = (0, 1) if large_first else (1, 0)
+    frags = (named_fragment("large", "large-param", "pg", 8, order[0]),
+             named_fragment("small", "small-param", "pg", 4, order[1]))
+    bindings = (
+        LocalFragmentBindingSpec(0, "large", "large-param", (TensorSegmentSpec(0, 8, (8,), 0, 8, 8),), 1.0),
+        LocalFragmentBindingSpec(0, "small", "small-param", (TensorSegmentSpec(0, 4, (4,), 0, 4, 4),), 1.0),
+    )
+    plan = bp.build_gradient_sync_plan(CanonicalFragmentPlan((group,), frags, ((0, bindings),), "h"), "tensor", 1024, "gpt", "m", "t")
+    large = torch.arange(1, 9, dtype=torch.float32, device=cuda) * 3.0
+    small = -torch.arange(1, 5, dtype=torch.float32, device=cuda)
+    add = 0.0 if local else 100.0
+
+    def all_reduce_sum(payload, handle):
+        payload.add_(add)
+
+    seam = local_all_reduce_sum if local else all_reduce_sum
+    ex = GradientBucketExecutor(plan, 0, (Desc("large-param", 0), Desc("small-param", 0)),
+                                (runtime_binding("large-param", large), runtime_binding("small-param", small)),
+                                FakeRegistry(), seam)
+    assert ex.n_buckets == 2
+    l0, s0 = large.clone(), small.clone()
+    scale = 0.3701
+    ex.execute(scale)
+    torch.cuda.synchronize()
+    ln, sn = (l0 + add) * scale, (s0 + add) * scale
+    assert torch.equal(large, ln) and torch.equal(small, sn)
+    sizes = [t[0].exact_numel for t in ex._tables]  # buckets in execution order
+    assert sizes == ([8, 4] if large_first else [4, 8])
+    want = torch.cat([sn, ln[4:]]) if large_first else ln.clone()
+    assert torch.equal(ex.scratch("float32")[:8], want)
+
+
 def test_replicated_half_contribution_scale(cuda):
     announce("grad_sync replicated fp16 x0.5")
     rec = KA["executor_replicated_half"]
