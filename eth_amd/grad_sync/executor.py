@@ -84,6 +84,26 @@ def chunk_table(entries):
     return table
 
 
+def shadowed_prefixes(buckets):
+    """Per bucket of a pass in plan order, the payload prefix (elements) of
+    its scratch buffer that a later bucket of the same grad dtype packs over.
+    The normalization write-back of a chunk inside that prefix is overwritten
+    unread, so the unpack may skip it and the pass still leaves the scratch as
+    the reference's in-place payload.mul_ does (executor.py:247-261)."""
+    covered = [0] * len(buckets)
+    reach = {}
+    for i in range(len(buckets) - 1, -1, -1):
+        covered[i] = reach.get(buckets[i].grad_dtype, 0)
+        reach[buckets[i].grad_dtype] = max(covered[i], buckets[i].exact_numel)
+    return covered
+
+
+def mark_shadowed(entries, shadow):
+    """Set ETH_CHUNK_SHADOWED on the chunk entries (split_block tuples) lying
+    wholly inside the first `shadow` payload elements."""
+    return [e[:6] + (e[6] | nat.CHUNK_SHADOWED,) if e[1] + e[3] * e[4] <= shadow else e for e in entries]
+
+
 class GradientStatistics:
     """Device-side found_inf flag, per-chunk L2 partials and the finalized
     [sum of squares, norm, clip coefficient] of one optimizer step."""
@@ -267,16 +287,7 @@ class GradientBucketExecutor:
         tables = []
         partial_base = 0
         buckets = list(self._rank_buckets())
-        # payload prefix of each scratch buffer that a later bucket of the pass
-        # (in plan order) packs over: the normalization write-back of chunks
-        # inside it is overwritten unread, so the unpack skips it and a pass
-        # still leaves the scratch exactly as the reference's payload.mul_ does
-        covered = [0] * len(buckets)
-        reach = {}
-        for i in range(len(buckets) - 1, -1, -1):
-            covered[i] = reach.get(buckets[i].grad_dtype, 0)
-            reach[buckets[i].grad_dtype] = max(covered[i], buckets[i].exact_numel)
-        for bucket, shadow in zip(buckets, covered):
+        for bucket, shadow in zip(buckets, shadowed_prefixes(buckets)):
             entries = []
             for placement in bucket.placements:
                 fragment = self._fragments[placement.fragment_id]
@@ -299,9 +310,7 @@ class GradientBucketExecutor:
                     copied += n
                 if copied != fragment.numel:
                     raise self._bucket_error(bucket, f"packed {copied} elements, expected {fragment.numel}", binding)
-            entries = [ent[:6] + (ent[6] | nat.CHUNK_SHADOWED,) if ent[1] + ent[3] * ent[4] <= shadow else ent
-                       for ent in entries]
-            table = chunk_table(entries)
+            table = chunk_table(mark_shadowed(entries, shadow))
             dev = nat.table_to_device(table, self._device) if len(table) else None
             tables.append((bucket, dev, len(table), partial_base))
             partial_base += len(table)

@@ -226,3 +226,23 @@ def test_oracle_bf16_rounding():
     x = np.array([1.0, 1.00390625, 1.01171875, -3.5, np.inf], dtype=np.float32)
     ref = torch.tensor(x).to(torch.bfloat16).float().numpy()
     np.testing.assert_array_equal(oadam.to_bf16(x), ref)
+
+
+def test_shadowed_prefixes_and_chunk_marks():
+    """The payload prefix a later bucket of the same dtype packs over, per
+    bucket in plan order, and the chunks marked inside it (hand-worked)."""
+    from collections import namedtuple
+
+    from eth_amd import _native as nat
+    from eth_amd.grad_sync.executor import mark_shadowed, shadowed_prefixes
+
+    B = namedtuple("B", "grad_dtype exact_numel")
+    buckets = [B("f32", 10), B("bf16", 50), B("f32", 30), B("f32", 20), B("bf16", 5), B("f32", 4)]
+    assert shadowed_prefixes(buckets) == [30, 5, 20, 4, 0, 0]
+    assert shadowed_prefixes([]) == []
+    # (src, dst, stride, rows, row_len, scale, flags): payload ranges [0, 8), [8, 20), [20, 30)
+    entries = [(0, 0, 8, 1, 8, 1.0, nat.CHUNK_NORM), (0, 8, 4, 3, 4, 1.0, 0), (0, 20, 10, 1, 10, 1.0, 0)]
+    flags = [e[6] for e in mark_shadowed(entries, 20)]
+    assert flags == [nat.CHUNK_NORM | nat.CHUNK_SHADOWED, nat.CHUNK_SHADOWED, 0]
+    assert [e[6] for e in mark_shadowed(entries, 19)] == [nat.CHUNK_NORM | nat.CHUNK_SHADOWED, 0, 0]
+    assert mark_shadowed(entries, 0) == entries
