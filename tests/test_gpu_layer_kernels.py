@@ -282,3 +282,18 @@ def test_bias_dropout_add_layer_norm_matches_the_two_kernels(cuda, dtype, rows, 
     assert torch.equal(h.view(torch.int16), h_ref.view(torch.int16))
     assert torch.equal(y.view(torch.int16), y_ref.view(torch.int16))
     assert torch.equal(mean, mean_ref) and torch.equal(rstd, rstd_ref)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("n", [1, 3, 4, 5, 2047, 2049, 4096 * 3 + 7, (1 << 20) + 5])
+def test_tied_grad_sum_ragged_lengths(cuda, dtype, n):
+    """Both copies become root + copy, bit for bit against torch's sum (one
+    rounding to the dtype), at lengths that leave a scalar tail, fill part of
+    a workgroup or fit in one vector."""
+    announce(f"tied grad sum n={n} {dtype}")
+    g = torch.Generator(device=cuda).manual_seed(n)
+    root = torch.randn(n, device=cuda, generator=g).to(dtype)
+    copy = torch.randn(n, device=cuda, generator=g).to(dtype)
+    want = (root.float() + copy.float()).to(dtype)
+    K.tied_grad_sum(root, copy)
+    assert torch.equal(root, want) and torch.equal(copy, want)
