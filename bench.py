@@ -43,8 +43,6 @@ PEAK_HBM_GBPS = 8000.0     # MI355X HBM3E
 H, HEADS, FFN, SEQ, MB, LAYERS = 2048, 16, 8192, 2048, 4, 6
 # the committed FETCH_SIZE / WRITE_SIZE counter summary of the GEMM launches
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemm_traffic_stage_step_gpt1p3b.md")
-# host threads for the CPU baseline: the GPU box's CPU share per GPU
-CPU_THREADS_CAP = 16
 
 
 def quiet_gc():
@@ -161,6 +159,17 @@ def cpu_info():
     return {"model": model, "logical_cpus": logical, "physical_cores": physical, "affinity_cpus": affinity}
 
 
+def cpu_threads(info):
+    """Every CPU this process may run on (its affinity set), bounded by
+    OMP_NUM_THREADS when the environment sets it: a GPU box exports its CPU
+    share per GPU there, and the host may hold more cores than that share."""
+    threads = info["affinity_cpus"] or info["logical_cpus"] or 1
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        threads = min(threads, int(omp))
+    return max(1, threads)
+
+
 def cpu_baseline(torch):
     """This build's torch-CPU fp32 restatement (the oracle) of the reference
     sequence on the host: the whole 6-layer stage forward+backward at the
@@ -173,7 +182,7 @@ def cpu_baseline(torch):
     from oracle import layer as ol
 
     info = cpu_info()
-    threads = max(1, min(CPU_THREADS_CAP, info["affinity_cpus"] or 1))
+    threads = cpu_threads(info)
     torch.set_num_threads(threads)
     gen = torch.Generator().manual_seed(0)
 
@@ -252,7 +261,7 @@ def cpu_baseline(torch):
         "sample": (
             f"one full step of the 6-layer stage in fp32 torch-CPU (oracle restatement): fwd+bwd at s {SEQ} b {MB} "
             f"{t_fwd_bwd:.2f} s, grad sync + unscale + L2 + AdamW over 302M params {t_tail:.2f} s; "
-            f"{threads} threads (the box's CPU share per GPU) on {info['model']}"
+            f"{threads} threads (the CPUs this process may use, bounded by OMP_NUM_THREADS) on {info['model']}"
         ),
         "cpu": info,
         "grad_sync_gbps": 16.0 * n_elem / t_sync / 1e9,
@@ -413,9 +422,17 @@ def first_last_stage(torch, steps=5, warmup=2, overlap_optimizer=True):
     """the GPT-6.7B first+last stage in fp16 -- token +
     position embedding, 2 layers (hidden 4096, 32 heads, FFN 16384), final
     LN, tied LM head over the padded vocabulary (50304) and vocab cross
-    entropy on the reference's synthetic batch (labels 0), seq 2048,
-    micro-batch 2; dynamic loss scale (2^16), grad sync, tied-gradient sum,
-    unscale + clip 1.0, AdamW with the fp16 model copy."""
+    entropy on the reference's synthetic batch, seq 2048, micro-batch 2;
+    dynamic loss scale (2^16), grad sync, tied-gradient sum, unscale + clip
+    1.0, AdamW with the fp16 model copy.
+
+    Labels are drawn uniformly over the vocabulary from a seed, fresh for
+    every step (made before the timing).  The reference's labels = 0
+    (flex_ops.py:1962) would stop training after the first update: every
+    gradient pushes the same logit, and AdamW's first step saturates the
+    fp16 softmax, so later steps would run on a zero loss and zero
+    gradients.  Each timed step's mean loss and gradient norm are reported,
+    read after the timed region."""
     from eth_amd.model.flex_ops import GPTConfig
     from eth_amd.stage import FirstLastStageTrainer
 
@@ -425,21 +442,26 @@ def first_last_stage(torch, steps=5, warmup=2, overlap_optimizer=True):
     tr = FirstLastStageTrainer(cfg, lr=1e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, clip_grad=1.0,
                                bucket_cap_bytes=32 << 20, initial_loss_scale=2.0**16,
                                overlap_optimizer=overlap_optimizer)
+    gen = torch.Generator(device="cuda").manual_seed(4321)
+    labels = [torch.randint(0, 50257, (b, s), generator=gen, device="cuda") for _ in range(warmup + steps)]
     for i in range(warmup):
         if i == warmup - 1:  # the freeze before the last warm-up step (see main)
             torch.cuda.synchronize()
             quiet_gc()
-        tr.train_step([2 * i, 2 * i + 1])
+        tr.train_step([2 * i, 2 * i + 1], labels[i])
     if warmup == 0:
         quiet_gc()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    oks = 0
+    oks, means, norms = 0, [], []
     for i in range(steps):
-        _, _, ok, _ = tr.train_step([2 * (warmup + i), 2 * (warmup + i) + 1])
+        _, lo, ok, norm = tr.train_step([2 * (warmup + i), 2 * (warmup + i) + 1], labels[warmup + i])
         oks += bool(ok)
+        means.append(lo.local_loss_sum / lo.local_loss_weight)  # device scalars, read after the timing
+        norms.append(norm)
     torch.cuda.synchronize()
     ms = 1e3 * (time.perf_counter() - t0) / steps
+    step_losses = [float(m.item()) for m in means]
     T = s * b
     flops = step_flops(layers, s, b, h, f) + 3 * 2.0 * T * h * V  # + LM head fwd, dgrad, wgrad
     tflops = flops / (ms * 1e-3) / 1e12
@@ -452,6 +474,9 @@ def first_last_stage(torch, steps=5, warmup=2, overlap_optimizer=True):
         "ms_per_step": ms,
         "steps": steps,
         "steps_applied": oks,
+        "labels": "uniform over [0, 50257) from seed 4321, fresh per step",
+        "step_mean_loss": step_losses,
+        "step_grad_norm": norms,
         "step_tflops": tflops,
         "step_mfma_frac": tflops / PEAK_BF16_TFLOPS,
         "dtype": "f16",

@@ -19,6 +19,7 @@ ETH_F32, ETH_F16, ETH_BF16 = 0, 1, 2
 CHUNK_ELEMS = 16384
 CHUNK_NORM, CHUNK_SHADOWED = 1, 2
 UNPACK_WRITEBACK, UNPACK_UNSCALE, UNPACK_STATS = 1, 2, 4
+STATS_SCALED_OVERFLOW = 8
 
 # struct eth_chunk (40 bytes)
 CHUNK_DTYPE = np.dtype(
@@ -65,6 +66,7 @@ SIGNATURES = {
     "eth_bucket_unpack": [_P, _I64, _P, _I32, _F32, _F32, _I32, _P, _P, _I64, _P],
     "eth_bucket_sync_local": [_P, _I64, _F32, _F32, _I32, _P, _P, _P],
     "eth_grad_stats": [_P, _I64, _F32, _I32, _P, _P, _I64, _P],
+    "eth_widen_grad_stats": [_P, _I64, _P, _I32, _F32, _I32, _P, _P, _I64, _P],
     "eth_grad_norm_finalize": [_P, _I64, _F64, _P, _P],
     "eth_adam_step": [_P, _P, _I64, _F64, _F64, _F64, _I64, _I32, _P, _P, _P],
     "eth_gemm": [_P, _I64, _I32, _P, _I64, _I32, _P, _I64, _I32, _P, _I64, _I64, _I64, _I32, _I32, _F32, _P],

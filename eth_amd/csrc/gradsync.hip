@@ -197,6 +197,9 @@ __global__ void __launch_bounds__(kThreads) stats_kernel(const eth_chunk_t* __re
   float* g = reinterpret_cast<float*>(c.src);
   const int64_t n = (int64_t)c.rows * c.row_len;
   const bool unscale = flags & ETH_UNPACK_UNSCALE;
+  // the scaled-overflow check multiplies by the loss scale (passed in `inv`)
+  // without storing; with unscaling it is meaningless and ignored
+  const float chk = (!unscale && (flags & ETH_STATS_SCALED_OVERFLOW)) ? inv : 1.0f;
   float sq = 0.f;
   bool bad = false;
   if (c.rows == 1 && aligned16(g)) {
@@ -204,7 +207,7 @@ __global__ void __launch_bounds__(kThreads) stats_kernel(const eth_chunk_t* __re
     float4* gv = reinterpret_cast<float4*>(g);
     for (int64_t i = threadIdx.x; i < nv; i += kThreads) {
       float4 x = gv[i];
-      bad |= !isfinite(x.x) | !isfinite(x.y) | !isfinite(x.z) | !isfinite(x.w);
+      bad |= !isfinite(x.x * chk) | !isfinite(x.y * chk) | !isfinite(x.z * chk) | !isfinite(x.w * chk);
       if (unscale) {
         x.x *= inv; x.y *= inv; x.z *= inv; x.w *= inv;
         gv[i] = x;
@@ -213,7 +216,7 @@ __global__ void __launch_bounds__(kThreads) stats_kernel(const eth_chunk_t* __re
     }
     for (int64_t i = nv * 4 + threadIdx.x; i < n; i += kThreads) {
       float x = g[i];
-      bad |= !isfinite(x);
+      bad |= !isfinite(x * chk);
       if (unscale) g[i] = x = x * inv;
       sq += x * x;
     }
@@ -222,7 +225,7 @@ __global__ void __launch_bounds__(kThreads) stats_kernel(const eth_chunk_t* __re
       const int64_t r = i / c.row_len, col = i - r * c.row_len;
       float* e = g + r * c.src_stride + col;
       float x = *e;
-      bad |= !isfinite(x);
+      bad |= !isfinite(x * chk);
       if (unscale) *e = x = x * inv;
       sq += x * x;
     }
@@ -231,6 +234,66 @@ __global__ void __launch_bounds__(kThreads) stats_kernel(const eth_chunk_t* __re
   float tot = block_sum<kThreads>(sq, red);
   if (threadIdx.x == 0)
     partials[partial_base + blockIdx.x] = (c.flags & ETH_CHUNK_NORM) ? (double)tot : 0.0;
+}
+
+// ------------------------------------- widening copy + statistics ---
+// 16-bit main grads (chunk.src, strided rows) into contiguous fp32 gradients
+// out[chunk.dst ...]: g = float(x) (exact), then the unscale / flag / sum of
+// squares of stats_kernel on g, in the same pass (R 2 B + W 4 B per element
+// instead of a copy and a separate read-modify-write).
+__global__ void __launch_bounds__(kThreads) widen_stats_kernel(const eth_chunk_t* __restrict__ chunks,
+                                                               float* __restrict__ out, int dtype, float inv,
+                                                               int flags, float* __restrict__ found_inf,
+                                                               double* __restrict__ partials,
+                                                               int64_t partial_base) {
+  __shared__ float red[kThreads / 64];
+  const eth_chunk_t c = chunks[blockIdx.x];
+  const uint16_t* src = reinterpret_cast<const uint16_t*>(c.src);
+  float* g = out + c.dst;
+  const int64_t n = (int64_t)c.rows * c.row_len;
+  const bool unscale = flags & ETH_UNPACK_UNSCALE;
+  float sq = 0.f;
+  bool bad = false;
+  if (c.rows == 1 && aligned16(src) && aligned16(g)) {
+    const int64_t nv = n / 8;
+    for (int64_t i = threadIdx.x; i < nv; i += kThreads) {
+      const uint4 a = reinterpret_cast<const uint4*>(src)[i];
+      const uint16_t* e = reinterpret_cast<const uint16_t*>(&a);
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        float x = Elem<uint16_t>::get(e[j], dtype);
+        bad |= !isfinite(x);
+        if (unscale) x *= inv;
+        sq += x * x;
+        v[j] = x;
+      }
+      reinterpret_cast<float4*>(g)[2 * i] = make_float4(v[0], v[1], v[2], v[3]);
+      reinterpret_cast<float4*>(g)[2 * i + 1] = make_float4(v[4], v[5], v[6], v[7]);
+    }
+    for (int64_t i = nv * 8 + threadIdx.x; i < n; i += kThreads) {
+      float x = Elem<uint16_t>::get(src[i], dtype);
+      bad |= !isfinite(x);
+      if (unscale) x *= inv;
+      sq += x * x;
+      g[i] = x;
+    }
+  } else {
+    for (int64_t i = threadIdx.x; i < n; i += kThreads) {
+      const int64_t r = i / c.row_len, col = i - r * c.row_len;
+      float x = Elem<uint16_t>::get(src[r * c.src_stride + col], dtype);
+      bad |= !isfinite(x);
+      if (unscale) x *= inv;
+      sq += x * x;
+      g[i] = x;
+    }
+  }
+  if (flags & ETH_UNPACK_STATS) {
+    if (bad) *found_inf = 1.0f;
+    float tot = block_sum<kThreads>(sq, red);
+    if (threadIdx.x == 0)
+      partials[partial_base + blockIdx.x] = (c.flags & ETH_CHUNK_NORM) ? (double)tot : 0.0;
+  }
 }
 
 // ---------------------------------------------------------- finalize ---
@@ -433,6 +496,21 @@ int eth_grad_stats(const eth_chunk_t* chunks, int64_t n_chunks, float inv_loss_s
   stats_kernel<<<(int)n_chunks, kThreads, 0, (hipStream_t)stream>>>(
       chunks, inv_loss_scale, flags, found_inf, partials, partial_base);
   ETH_CHECK_LAUNCH("eth_grad_stats");
+  return ETH_OK;
+}
+
+int eth_widen_grad_stats(const eth_chunk_t* chunks, int64_t n_chunks, float* out, int dtype,
+                         float inv_loss_scale, int flags, float* found_inf, double* partials,
+                         int64_t partial_base, void* stream) {
+  ETH_CHECK_ARG(dtype == ETH_BF16 || dtype == ETH_F16, "eth_widen_grad_stats: dtype must be bf16/fp16");
+  ETH_CHECK_ARG(n_chunks >= 0 && n_chunks < (1LL << 31), "eth_widen_grad_stats: bad chunk count");
+  if (n_chunks == 0) return ETH_OK;
+  ETH_CHECK_ARG(chunks && out, "eth_widen_grad_stats: null table or output");
+  ETH_CHECK_ARG(!(flags & ETH_UNPACK_STATS) || (found_inf && partials && partial_base >= 0),
+                "eth_widen_grad_stats: statistics need found_inf and partials");
+  widen_stats_kernel<<<(int)n_chunks, kThreads, 0, (hipStream_t)stream>>>(
+      chunks, out, dtype, inv_loss_scale, flags, found_inf, partials, partial_base);
+  ETH_CHECK_LAUNCH("eth_widen_grad_stats");
   return ETH_OK;
 }
 

@@ -76,18 +76,22 @@ __global__ void __launch_bounds__(256) embedding_fwd_kernel(const int64_t* __res
 // in that order and adds the sum into the fp32 main grad once: no atomics,
 // and the same bits on every run.  The keys fit 32 bits when
 // bits(V - 1) + bits(T - 1) <= 32; T <= kEmbSortMax keeps the LDS image at
-// 128 KB (static; gfx950 gives a workgroup up to 160 KB).
+// 128 KB (static; gfx950 gives a workgroup up to 160 KB).  Longer inputs
+// run as consecutive chunks of whole sequence positions (at most
+// kEmbSortMax dout rows each), one sort + accumulate per chunk in sequence
+// order: each table row then receives one ordered sum per chunk.
 constexpr int kEmbSortThreads = 1024;
 constexpr int kEmbSortMax = 32768;
 
 __device__ __forceinline__ int64_t clamp_id(int64_t v, int64_t n) { return v < 0 ? 0 : (v >= n ? n - 1 : v); }
 
 // blockIdx.x = 0 sorts the token ids into keys[0, T), 1 the position ids
-// into keys[T, 2T)
+// into keys[T, 2T); sample b's ids start at ids + b * ld
 __global__ void __launch_bounds__(kEmbSortThreads) embedding_sort_kernel(const int64_t* __restrict__ tok,
                                                                         const int64_t* __restrict__ pid,
                                                                         uint32_t* __restrict__ keys, int B, int S,
-                                                                        int64_t V, int64_t P, int row_bits, int n2) {
+                                                                        int64_t ld, int64_t V, int64_t P,
+                                                                        int row_bits, int n2) {
   __shared__ uint32_t sk[kEmbSortMax];
   const int T = B * S;
   const int64_t* ids = blockIdx.x == 0 ? tok : pid;
@@ -96,7 +100,7 @@ __global__ void __launch_bounds__(kEmbSortThreads) embedding_sort_kernel(const i
     uint32_t k = 0xFFFFFFFFu;
     if (i < T) {
       const int si = i / B, bi = i - si * B;  // dout row i holds (s, b)
-      k = ((uint32_t)clamp_id(ids[(int64_t)bi * S + si], lim) << row_bits) | (uint32_t)i;
+      k = ((uint32_t)clamp_id(ids[(int64_t)bi * ld + si], lim) << row_bits) | (uint32_t)i;
     }
     sk[i] = k;
   }
@@ -354,8 +358,15 @@ extern "C" int eth_embedding_fwd(const int64_t* tokens, const int64_t* positions
   return ETH_OK;
 }
 
+// sequence positions per chunk: whole positions, at most kEmbSortMax dout rows
+static int64_t emb_chunk_seq(int64_t batch, int64_t seq) {
+  const int64_t sc = kEmbSortMax / batch;
+  return sc < seq ? sc : seq;
+}
+
 extern "C" int64_t eth_embedding_bwd_workspace(int64_t batch, int64_t seq) {
-  return batch > 0 && seq > 0 ? 2 * batch * seq * (int64_t)sizeof(uint32_t) : 0;
+  if (batch <= 0 || seq <= 0 || batch > kEmbSortMax) return 0;
+  return 2 * batch * emb_chunk_seq(batch, seq) * (int64_t)sizeof(uint32_t);
 }
 
 extern "C" int eth_embedding_bwd(const int64_t* tokens, const int64_t* positions, const void* dout,
@@ -365,30 +376,35 @@ extern "C" int eth_embedding_bwd(const int64_t* tokens, const int64_t* positions
   ETH_CHECK_ARG(batch > 0 && seq > 0 && hidden > 0 && hidden % 8 == 0 && vocab > 0 && max_pos > 0,
                 "eth_embedding_bwd: bad shape");
   ETH_CHECK_ARG(tokens && positions && dout && workspace && (dword || dpos), "eth_embedding_bwd: null pointer");
-  const int64_t T = batch * seq;
-  ETH_CHECK_ARG(T <= kEmbSortMax, "eth_embedding_bwd: at most %d tokens per call (got %lld)", kEmbSortMax,
-                (long long)T);
-  const int row_bits = bits_for(T);
+  ETH_CHECK_ARG(batch <= kEmbSortMax, "eth_embedding_bwd: at most %d samples per call (got %lld)", kEmbSortMax,
+                (long long)batch);
+  // consecutive chunks of whole sequence positions, each <= kEmbSortMax rows
+  const int64_t sc = emb_chunk_seq(batch, seq);
+  const int row_bits = bits_for(batch * sc);
   ETH_CHECK_ARG(row_bits + bits_for(vocab) <= 32 && row_bits + bits_for(max_pos) <= 32,
                 "eth_embedding_bwd: ids and rows do not fit a 32-bit sort key");
   ETH_CHECK_ARG(((uintptr_t)dword & 15) == 0 && ((uintptr_t)dpos & 15) == 0 && ((uintptr_t)workspace & 3) == 0,
                 "eth_embedding_bwd: gradient tables must be 16-byte aligned");
-  int n2 = 1;
-  while (n2 < T) n2 <<= 1;
-  if (n2 < 2) n2 = 2;
   hipStream_t s = (hipStream_t)stream;
   uint32_t* keys = (uint32_t*)workspace;
-  embedding_sort_kernel<<<2, kEmbSortThreads, 0, s>>>(tokens, positions, keys, (int)batch, (int)seq, vocab,
-                                                        max_pos, row_bits, n2);
-  ETH_CHECK_LAUNCH("eth_embedding_bwd (sort)");
-  dim3 grid((unsigned)T, (unsigned)((hidden + 2047) / 2048), 2);
-  if (dtype == ETH_BF16)
-    embedding_accum_kernel<false><<<grid, 256, 0, s>>>(keys, (const uint16_t*)dout, dword, dpos, (int)T,
-                                                       (int)hidden, row_bits);
-  else
-    embedding_accum_kernel<true><<<grid, 256, 0, s>>>(keys, (const uint16_t*)dout, dword, dpos, (int)T,
-                                                      (int)hidden, row_bits);
-  ETH_CHECK_LAUNCH("eth_embedding_bwd");
+  const uint16_t* d = (const uint16_t*)dout;
+  for (int64_t s0 = 0; s0 < seq; s0 += sc) {
+    const int64_t len = seq - s0 < sc ? seq - s0 : sc;
+    const int64_t T = batch * len;
+    int n2 = 1;
+    while (n2 < T) n2 <<= 1;
+    if (n2 < 2) n2 = 2;
+    embedding_sort_kernel<<<2, kEmbSortThreads, 0, s>>>(tokens + s0, positions + s0, keys, (int)batch, (int)len,
+                                                          seq, vocab, max_pos, row_bits, n2);
+    ETH_CHECK_LAUNCH("eth_embedding_bwd (sort)");
+    dim3 grid((unsigned)T, (unsigned)((hidden + 2047) / 2048), 2);
+    const uint16_t* dc = d + s0 * batch * hidden;  // dout rows [s0 * B, (s0 + len) * B)
+    if (dtype == ETH_BF16)
+      embedding_accum_kernel<false><<<grid, 256, 0, s>>>(keys, dc, dword, dpos, (int)T, (int)hidden, row_bits);
+    else
+      embedding_accum_kernel<true><<<grid, 256, 0, s>>>(keys, dc, dword, dpos, (int)T, (int)hidden, row_bits);
+    ETH_CHECK_LAUNCH("eth_embedding_bwd");
+  }
   return ETH_OK;
 }
 
@@ -464,19 +480,23 @@ extern "C" int eth_xent_bwd(const void* logits, int64_t ld, const int64_t* label
                     ldd % 8 == 0,
                 "eth_xent_bwd: bad shape");
   if (rows == 0) return ETH_OK;
-  ETH_CHECK_ARG(rows <= 65535, "eth_xent_bwd: at most 65535 rows per launch");
   ETH_CHECK_ARG(logits && labels && lse && dloss && dlogits, "eth_xent_bwd: null pointer");
   const int64_t nv = vocab / 8;
   int gx = (int)((nv + kXentThreads - 1) / kXentThreads);
   if (gx > 16) gx = 16;
-  dim3 grid(gx, (unsigned)rows);
   hipStream_t s = (hipStream_t)stream;
-  if (dtype == ETH_BF16)
-    xent_bwd_kernel<false><<<grid, kXentThreads, 0, s>>>((const uint16_t*)logits, ld, labels, lse, dloss,
-                                                         (uint16_t*)dlogits, ldd, vocab);
-  else
-    xent_bwd_kernel<true><<<grid, kXentThreads, 0, s>>>((const uint16_t*)logits, ld, labels, lse, dloss,
-                                                        (uint16_t*)dlogits, ldd, vocab);
-  ETH_CHECK_LAUNCH("eth_xent_bwd");
+  // rows go on the grid's y dimension (at most 65535 per launch)
+  constexpr int64_t kRowsPerLaunch = 65535;
+  for (int64_t r0 = 0; r0 < rows; r0 += kRowsPerLaunch) {
+    const int64_t n = rows - r0 < kRowsPerLaunch ? rows - r0 : kRowsPerLaunch;
+    dim3 grid(gx, (unsigned)n);
+    const uint16_t* z = (const uint16_t*)logits + r0 * ld;
+    uint16_t* dz = (uint16_t*)dlogits + r0 * ldd;
+    if (dtype == ETH_BF16)
+      xent_bwd_kernel<false><<<grid, kXentThreads, 0, s>>>(z, ld, labels + r0, lse + r0, dloss + r0, dz, ldd, vocab);
+    else
+      xent_bwd_kernel<true><<<grid, kXentThreads, 0, s>>>(z, ld, labels + r0, lse + r0, dloss + r0, dz, ldd, vocab);
+    ETH_CHECK_LAUNCH("eth_xent_bwd");
+  }
   return ETH_OK;
 }

@@ -1,4 +1,3 @@
-import functools
 """Megatron optimizer wrappers on the fused HIP path.
 
 Step contract of eth/runtime/megatron/optimizer/optimizer.py:493-531:
@@ -15,6 +14,8 @@ coefficient and the overflow flag from device memory and writes the model
 copy itself.  The host reads the flag and the norm once, after everything is
 queued.
 """
+
+import functools
 
 import numpy as np
 import torch
@@ -116,6 +117,12 @@ class MegatronOptimizer:
         ones; every result is the same as with the update in line."""
         dev = self._device()
         parts = [[self.optimizer_parameter_for_model_parameter(p) for p in part] for part in model_param_parts]
+        placed = {id(p) for part in parts for p in part}
+        missing = [p for g in self.optimizer.param_groups for p in g["params"] if id(p) not in placed]
+        if missing:
+            # the deferred launches only cover the given parts: a parameter in
+            # none of them would never be updated
+            raise ValueError(f"overlapped update parts miss {len(missing)} optimizer parameter(s)")
         self.optimizer.set_partition(parts)
         self._overlap = (torch.cuda.Stream(device=dev), [list(part) for part in model_param_parts])
 
@@ -207,42 +214,74 @@ class MegatronOptimizer:
     def _norm_owned(self, param):
         return not getattr(param, "shared", False) or getattr(param, "shared_root", False)
 
-    def _standalone_statistics(self, unscale):
+    def _widen_sources(self):
+        """{id(optimizer parameter): 16-bit main grad} of the gradients the
+        step still has to widen into the parameter's fp32 grad (none here)."""
+        return {}
+
+    def _widen_target(self):
+        """The fp32 buffer the widened gradients are views of."""
+        raise NotImplementedError
+
+    def _standalone_statistics(self, unscale, stats=True):
+        """One statistics pass over every optimizer gradient: unscale (when
+        `unscale`), overflow flag and per-chunk sums of squares (when
+        `stats`).  Gradients still held as 16-bit main grads are widened into
+        their fp32 grads in the same pass (eth_widen_grad_stats); the others
+        are done in place (eth_grad_stats).  Returns the statistics, or None
+        without `stats`."""
+        widen = self._widen_sources()
         params = [p for p in self.get_parameters() if p.grad is not None]
-        key = tuple((p.grad.data_ptr(), p.grad.numel()) for p in params)
+        key = tuple((p.grad.data_ptr(), p.grad.numel(), widen[id(p)].data_ptr() if id(p) in widen else 0)
+                    for p in params)
         if key != self._stats_key:
-            entries = []
+            wide, plain, code = [], [], None
+            base = self._widen_target().data_ptr() if widen else 0
             for p in params:
                 g = p.grad
                 if g.dtype != torch.float32 or not g.is_contiguous():
                     raise ValueError("optimizer gradients must be contiguous fp32")
                 flags = nat.CHUNK_NORM if self._norm_owned(p) else 0
-                split_block(g.data_ptr(), 4, 1, g.numel(), g.numel(), 0, 1.0, flags, entries)
-            table = chunk_table(entries)
-            self._stats_tables = (nat.table_to_device(table, self._device()) if len(table) else None, len(table))
+                src = widen.get(id(p))
+                if src is None:
+                    split_block(g.data_ptr(), 4, 1, g.numel(), g.numel(), 0, 1.0, flags, plain)
+                    continue
+                if src.shape != g.shape or not src.is_contiguous():
+                    raise ValueError("16-bit main grads must be contiguous and shaped like their parameters")
+                if code is not None and nat.dtype_code(src.dtype) != code:
+                    raise ValueError("16-bit main grads of one optimizer must share a dtype")
+                code = nat.dtype_code(src.dtype)
+                dst = (g.data_ptr() - base) // 4
+                split_block(src.data_ptr(), 2, 1, src.numel(), src.numel(), dst, 1.0, flags, wide)
+            self._stats_tables = tuple(
+                (nat.table_to_device(chunk_table(e), self._device()) if e else None, len(e)) for e in (wide, plain))
+            self._widen_code = code
             self._stats_key = key
-            if self._statistics is None or self._statistics.n_partials < len(table):
-                self._statistics = GradientStatistics(len(table), self._device())
+            n_total = len(wide) + len(plain)
+            if self._statistics is None or self._statistics.n_partials < n_total:
+                self._statistics = GradientStatistics(n_total, self._device())
                 if self._executor is not None:
                     self._executor.bind_statistics(None)
                     self._executor = None
-        table, n = self._stats_tables
+        (wtable, nw), (table, n) = self._stats_tables
         st = self._statistics
-        st.reset()
+        if stats:
+            st.reset()
         flags = nat.UNPACK_UNSCALE if unscale else 0
-        nat.call(
-            "eth_grad_stats",
-            nat.ptr(table),
-            n,
-            float(self._inv_scale()),
-            flags,
-            nat.ptr(st.found_inf),
-            nat.ptr(st.partials),
-            0,
-            nat.stream_ptr(self._device()),
-        )
-        # partials past this table's chunks must not leak into the norm
-        st.n_partials_used = n
+        stream = nat.stream_ptr(self._device())
+        if nw:
+            nat.call("eth_widen_grad_stats", nat.ptr(wtable), nw, self._widen_target().data_ptr(), self._widen_code,
+                     float(self._inv_scale()), flags | (nat.UNPACK_STATS if stats else 0), nat.ptr(st.found_inf),
+                     nat.ptr(st.partials), 0, stream)
+        if not stats:
+            if unscale:
+                raise ValueError("unscaling without statistics is not a step of this optimizer")
+            return None
+        if n:
+            nat.call("eth_grad_stats", nat.ptr(table), n, float(self._inv_scale()), flags, nat.ptr(st.found_inf),
+                     nat.ptr(st.partials), nw, stream)
+        # partials past this pass's chunks must not leak into the norm
+        st.n_partials_used = nw + n
         return st
 
     def count_zeros(self):
@@ -272,12 +311,19 @@ class MegatronOptimizer:
             if n:
                 # statistics of the gradients changed after the sync (already
                 # unscaled by the unpack): sum of squares into the slots after
-                # the executor's, overflow of the sums into found_inf
-                nat.call("eth_grad_stats", nat.ptr(table), n, 1.0, 0, nat.ptr(st.found_inf), nat.ptr(st.partials),
-                         st.n_partials_used, nat.stream_ptr(self._device()))
+                # the executor's; found_inf where a sum, loss-scaled again,
+                # is not finite -- the reference sums the scaled addends
+                # (training.py:997-1004) and flags that overflow at step()
+                scale = scaler.host_scale if scaler is not None else 1.0
+                nat.call("eth_grad_stats", nat.ptr(table), n, float(scale), nat.STATS_SCALED_OVERFLOW,
+                         nat.ptr(st.found_inf), nat.ptr(st.partials), st.n_partials_used,
+                         nat.stream_ptr(self._device()))
                 st.n_partials_used += n
         elif scaler is not None or need_norm:
             st = self._standalone_statistics(unscale=scaler is not None)
+        elif self._widen_sources():
+            # 16-bit main grads still to be widened, no statistics wanted
+            self._standalone_statistics(unscale=False, stats=False)
         if st is not None:
             st.fresh = False
         if need_norm:
@@ -413,6 +459,8 @@ class Float16OptimizerWithFloat16Params(MegatronOptimizer):
         self.bf16 = bf16
         self.grad_scaler = grad_scaler
         self._f32_grads = {}
+        self._f32_flat = None
+        self._widen = {}  # {id(master): 16-bit main grad} widened by this step's statistics pass
         self.use_contiguous_buffers_in_ddp = use_contiguous_buffers_in_ddp
         model_dtypes = {p.dtype for p in half}
         if len(model_dtypes) > 1:
@@ -440,6 +488,7 @@ class Float16OptimizerWithFloat16Params(MegatronOptimizer):
             masters = [m for g in self.fp32_from_float16_groups for m in g]
             sizes = [(m.numel() + 3) // 4 * 4 for m in masters]  # 16-byte aligned views
             flat = torch.empty(sum(sizes), dtype=torch.float32, device=masters[0].device)
+            self._f32_flat = flat
             off = 0
             for m, n in zip(masters, sizes):
                 self._f32_grads[id(m)] = flat[off : off + m.numel()].view(m.shape)
@@ -447,7 +496,14 @@ class Float16OptimizerWithFloat16Params(MegatronOptimizer):
             view = self._f32_grads[id(main_param)]
         return view
 
+    def _widen_sources(self):
+        return self._widen
+
+    def _widen_target(self):
+        return self._f32_flat
+
     def _copy_model_grads_to_main_grads(self):
+        self._widen = {}
         for mg, fg in zip(self.float16_groups, self.fp32_from_float16_groups):
             for model_param, main_param in zip(mg, fg):
                 if self.params_have_main_grad:
@@ -458,8 +514,10 @@ class Float16OptimizerWithFloat16Params(MegatronOptimizer):
                             main_param.grad = g
                     else:
                         # main_grad.float() (optimizer.py:392-397) into a
-                        # persistent buffer: an exact widening copy
-                        main_param.grad = self._fp32_grad_view(main_param).copy_(g)
+                        # persistent buffer: an exact widening copy, which the
+                        # step's statistics pass makes (eth_widen_grad_stats)
+                        main_param.grad = self._fp32_grad_view(main_param)
+                        self._widen[id(main_param)] = g
                 elif model_param.grad is not None:
                     main_param.grad = model_param.grad.float()
                 if model_param.grad is not None:

@@ -14,6 +14,7 @@ stage's ops, and the fused unscale / flag / L2 statistics of the grad-sync
 unpack bound to the optimizer.
 """
 
+import dataclasses
 import math
 
 import torch
@@ -39,20 +40,31 @@ def save_stage_snapshot(trainer, output_dir, phase, iteration, metrics=None, clo
     opt = trainer.optimizer
     # an overlapped update still pending is issued and waited for first
     opt.join_overlapped_update()
+    loss_scale = float(opt.get_loss_scale().item())
+    bindings = list(trainer.bindings)
+    if phase == "post_sync" and opt.grads_unscaled_by_sync and loss_scale != 1.0:
+        # The reference records post_sync before optimizer.step(), with the
+        # main grads still loss-scaled (training.py:1005-1020); here the
+        # sync's unpack has already unscaled them in place.  The scale is a
+        # power of two, so multiplying back restores the scaled values
+        # exactly (short of an fp32 overflow, which the step then flags).
+        if loss_scale != 2.0 ** round(math.log2(loss_scale)):
+            raise ValueError(f"post_sync evidence needs a power-of-two loss scale, got {loss_scale}")
+        bindings = [dataclasses.replace(b, main_grad=b.main_grad * loss_scale) for b in bindings]
     state, master, hyper = {}, {}, {}
     for b in trainer.bindings:
         st = opt.state_for_model_parameter(b.parameter)
         state[b.logical_param_id] = {k: st[k] for k in ("step", "exp_avg", "exp_avg_sq") if k in st}
         master[b.logical_param_id] = opt.optimizer_parameter_for_model_parameter(b.parameter)
         hyper[b.logical_param_id] = opt.hyperparameters_for_model_parameter(b.parameter)
-    base_clock = {"learning_rate": opt.param_groups[0]["lr"], "loss_scale": float(opt.get_loss_scale().item())}
+    base_clock = {"learning_rate": opt.param_groups[0]["lr"], "loss_scale": loss_scale}
     return save_rank_snapshot(
         output_dir,
         phase=phase,
         iteration=iteration,
         global_rank=0,
         descriptors=trainer.descriptors,
-        runtime_bindings=trainer.bindings,
+        runtime_bindings=bindings,
         optimizer_state_by_logical=state,
         optimizer_parameter_by_logical=master,
         optimizer_hyperparameters_by_logical=hyper,

@@ -118,10 +118,31 @@ int eth_bucket_sync_local(const eth_bucket_t* buckets, int64_t n_buckets,
  * when gradients did not pass through eth_bucket_unpack this step.
  * Replaces torch._amp_foreach_non_finite_check_and_unscale_
  * (optimizer/optimizer.py:452-453) + the canonical L2 statistic
- * (grad_sync/optimizer_semantics.py:584-587). */
+ * (grad_sync/optimizer_semantics.py:584-587).
+ * With ETH_STATS_SCALED_OVERFLOW (and without ETH_UNPACK_UNSCALE) the
+ * gradients are left as they are and `inv_loss_scale` carries the loss
+ * scale instead: found_inf is also set where g * scale is not finite, i.e.
+ * where the loss-scaled value of an already unscaled gradient (a tied
+ * embedding sum formed after the unpack) would have overflowed. */
+#define ETH_STATS_SCALED_OVERFLOW 8
 int eth_grad_stats(const eth_chunk_t* chunks, int64_t n_chunks, float inv_loss_scale,
                    int flags, float* found_inf, double* partials, int64_t partial_base,
                    void* stream);
+
+/* The fp16-contract widening copy fused with the statistics: 16-bit main
+ * grads (`dtype` bf16 / fp16; chunk.src, strided rows as in a bucket table)
+ * into contiguous fp32 gradients out[chunk.dst ...], g = float(x) (exact),
+ * then, as eth_grad_stats does on g: g *= inv_loss_scale with
+ * ETH_UNPACK_UNSCALE; found_inf and partials[partial_base + chunk] with
+ * ETH_UNPACK_STATS.  One pass instead of a copy and an in-place unscale.
+ * Replaces main_param.grad = main_grad.float() of
+ * Float16OptimizerWithFloat16Params._copy_model_grads_to_main_grads
+ * (optimizer/optimizer.py:388-404) fused with
+ * torch._amp_foreach_non_finite_check_and_unscale_ (:452-453) and the
+ * canonical L2 statistic (grad_sync/optimizer_semantics.py:584-587). */
+int eth_widen_grad_stats(const eth_chunk_t* chunks, int64_t n_chunks, float* out, int dtype,
+                         float inv_loss_scale, int flags, float* found_inf, double* partials,
+                         int64_t partial_base, void* stream);
 
 /* Reduce `n` per-chunk partials into stats[0] = sum of squares (double) and
  * stats[1] = L2 norm; stats[2] = clip coefficient max_norm/(norm+1e-6)
@@ -321,13 +342,17 @@ int eth_attn_bwd(const eth_attn_desc_t* desc, const void* q, const void* k, cons
  * eth_embedding_bwd: fp32 dword[tok] += dout, dpos[pos] += dout, bitwise
  *   deterministic: the ids are sorted with their dout rows (in `workspace`
  *   of eth_embedding_bwd_workspace(batch, seq) bytes) and each table row is
- *   summed by one workgroup in dout-row order; batch * seq <= 32768, and
- *   bits(vocab - 1) + bits(batch * seq - 1) <= 32.  Either table may be NULL.
+ *   summed by one workgroup in dout-row order.  Inputs of more than 32768
+ *   tokens run as consecutive chunks of whole sequence positions (at most
+ *   32768 dout rows each, in sequence order), each adding its own ordered
+ *   sums; batch <= 32768, and bits(vocab - 1) + bits(rows per chunk - 1)
+ *   <= 32.  Either table may be NULL.
  *   Replaces the embedding's autograd backward (embedding_dense_backward, a
  *   sort + segmented reduction) and the main_grad.add_ hook of
  *   model/distributed.py:116-123.
  * eth_xent_fwd / eth_xent_bwd: per-row loss = logsumexp(z) - z[label] from
- *   16-bit logits [rows, ld], saving lse; dz = (softmax - onehot) * dloss.
+ *   16-bit logits [rows, ld], saving lse; dz = (softmax - onehot) * dloss
+ *   (any row count: eth_xent_bwd launches 65535 rows at a time).
  *   Replace vocab_parallel_cross_entropy(logits.float(), labels)
  *   (mpu/cross_entropy.py:36-115; flex_ops.py:1976-1981).
  * Out-of-range ids are clamped and flagged in *bad_index (set to 1).

@@ -103,13 +103,19 @@ def vocab_cross_entropy(logits, labels):
     return torch.log(torch.exp(shifted).sum(dim=-1)) - target
 
 
-def embedding_grad_ordered(tokens, positions, dout, word_grad, pos_grad):
+EMBEDDING_CHUNK_ROWS = 32768
+
+
+def embedding_grad_ordered(tokens, positions, dout, word_grad, pos_grad, chunk_rows=EMBEDDING_CHUNK_ROWS):
     """F.embedding's backward into fp32 main grads, restated with a fixed
     summation order (numpy fp32): every table row receives the fp32 sum of
     its dout rows taken in ascending dout-row order (row = s * b_size + b
-    of dout [s, b, h]), added once to its previous value.  Ids outside the
-    table are clamped, as the kernels do.  `word_grad` / `pos_grad` are
-    numpy fp32 tables updated in place (either may be None).
+    of dout [s, b, h]), added once to its previous value.  Inputs of more
+    than `chunk_rows` rows are taken in consecutive chunks of whole sequence
+    positions (floor(chunk_rows / b_size) positions each), each chunk adding
+    its own ordered sums in turn.  Ids outside the table are clamped, as the
+    kernels do.  `word_grad` / `pos_grad` are numpy fp32 tables updated in
+    place (either may be None).
     (flex_ops.py:450-485 forward; the backward is autograd's
     embedding_dense_backward plus the main_grad hook of
     model/distributed.py:116-123.)"""
@@ -117,17 +123,19 @@ def embedding_grad_ordered(tokens, positions, dout, word_grad, pos_grad):
 
     s, b, h = dout.shape
     rows = np.ascontiguousarray(dout, dtype=np.float32).reshape(s * b, h)
+    step = max(1, chunk_rows // b) * b
     for table, ids in ((word_grad, tokens), (pos_grad, positions)):
         if table is None:
             continue
         ids = np.clip(np.asarray(ids, dtype=np.int64), 0, table.shape[0] - 1)
         by_row = ids.T.reshape(-1)  # dout row s*b_size + b holds ids[b, s]
-        sums = {}
-        for r in range(s * b):
-            t = int(by_row[r])
-            sums[t] = sums.get(t, np.zeros(h, dtype=np.float32)) + rows[r]
-        for t, acc in sums.items():
-            table[t] += acc
+        for r0 in range(0, s * b, step):
+            sums = {}
+            for r in range(r0, min(r0 + step, s * b)):
+                t = int(by_row[r])
+                sums[t] = sums.get(t, np.zeros(h, dtype=np.float32)) + rows[r]
+            for t, acc in sums.items():
+                table[t] += acc
     return word_grad, pos_grad
 
 

@@ -111,3 +111,44 @@ def test_first_last_stage_in_the_reference_fp16_contract(cuda, tmp_path):
     # a packaged step runs too, and the next one reuses the fp32 gradient buffer
     _, _, ok2, norm2 = tr.train_step([5, 9])
     assert ok2 and np.isfinite(norm2)
+
+
+def test_fp16_main_grads_are_widened_unscaled_and_measured_in_one_pass(cuda):
+    """The optimizer's fp32 copy of fp16 main grads (main_grad.float(),
+    optimizer.py:392-397) is made by the statistics pass itself: after the
+    step every master's grad is the fp16 main grad widened and multiplied by
+    1/loss_scale, bit for bit as torch computes it; the norm is the oracle's
+    L2 over the norm-owned grads (the tied head copy excluded); a +inf in an
+    fp16 main grad skips the step."""
+    announce("fp16 main grads: widening fused with unscale and statistics")
+    cfg = GPTConfig(hidden_size=256, num_attention_heads=4, ffn_hidden_size=1024, num_layers=2, seq_length=128,
+                    micro_batch_size=2, padded_vocab_size=50304, params_dtype=torch.float16, device="cuda", seed=19)
+    tr = FirstLastStageTrainer(cfg, lr=1e-4, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01, clip_grad=1.0,
+                               initial_loss_scale=1024.0, accumulate_allreduce_grads_in_fp32=False)
+    opt = tr.optimizer
+    for attempt in ("finite", "overflow"):
+        tr.ddp.zero_grad_buffer()
+        _, lo = tr.forward_backward([3, 8])
+        tr.grad_sync.execute(global_normalization_scale(tr.nominal, lo.local_loss_weight))
+        tr.tie_gradients()
+        if attempt == "overflow":
+            qkv = next(op for op in tr.model.language_model.ops if op.name == "enc-attention-qkv")
+            qkv.query_key_value.weight.main_grad[1, 2] = float("inf")
+        torch.cuda.synchronize()
+        host = {name: p.main_grad.detach().cpu().clone() for name, p in tr.model.named_parameters()}
+        ok, norm, _ = opt.step()
+        torch.cuda.synchronize()
+        if attempt == "overflow":
+            assert (ok, norm) == (False, None)
+            continue
+        assert ok and norm is not None
+        owned = []
+        for name, p in tr.model.named_parameters():
+            m = opt.optimizer_parameter_for_model_parameter(p)
+            assert m.grad.dtype == torch.float32
+            want = host[name].float() * torch.tensor(1.0 / 1024.0)
+            assert torch.equal(m.grad.cpu(), want), name
+            if opt._norm_owned(m):
+                owned.append(want.numpy())
+        assert len(owned) == len(host) - 1  # the tied head copy is not norm-owned
+        assert norm == pytest.approx(og.l2_norm(owned), rel=1e-6)

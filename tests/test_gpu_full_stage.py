@@ -89,14 +89,53 @@ def test_embedding_backward_is_deterministic_with_repeated_tokens(cuda, dtype):
     assert torch.equal(outs[0][0], torch.from_numpy(ref_w))
     assert torch.equal(outs[0][1], torch.from_numpy(ref_p))
     assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
-    # one table only, and the token limit of one call
+    # one table only
     dw = start.to(cuda)
     K.embedding_bwd(tok.to(cuda), pid.to(cuda), dout.to(cuda), dw, None)
     assert torch.equal(dw.cpu(), outs[0][0])
-    big = torch.zeros(2, 16385, dtype=torch.int64, device=cuda)
-    with pytest.raises(ValueError):
-        K.embedding_bwd(big, big, torch.zeros(16385, 2, 8, dtype=dtype, device=cuda),
-                        torch.zeros(4, 8, device=cuda), None)
+
+
+@pytest.mark.parametrize("b,s", [(3, 12000), (32, 2048)])
+def test_embedding_backward_beyond_one_sort_chunk(cuda, b, s):
+    """More tokens than one LDS sort holds (32768): consecutive chunks of
+    whole sequence positions, bit-exact against the oracle's chunked
+    ordered sum, with heavily repeated ids across the chunk edges (b 32,
+    s 2048 is a first stage at micro-batch 32)."""
+    announce(f"embedding backward in chunks b {b} s {s}")
+    gen = torch.Generator().manual_seed(22)
+    h, V = 64, 50304
+    tok = torch.randint(0, 5, (b, s), generator=gen)
+    tok[:, ::3] = torch.randint(0, V, (b, (s + 2) // 3), generator=gen)
+    pid = torch.arange(s).expand(b, s).contiguous()
+    dout = torch.randn(s, b, h, generator=gen).to(torch.bfloat16)
+    start = torch.randn(V, h, generator=gen) * 0.01
+    ref_w = start.numpy().copy()
+    ref_p = np.zeros((s, h), dtype=np.float32)
+    ol.embedding_grad_ordered(tok.numpy(), pid.numpy(), dout.float().numpy(), ref_w, ref_p)
+    dw, dp = start.to(cuda), torch.zeros(s, h, device=cuda)
+    K.embedding_bwd(tok.to(cuda), pid.to(cuda), dout.to(cuda), dw, dp)
+    torch.cuda.synchronize()
+    assert torch.equal(dw.cpu(), torch.from_numpy(ref_w))
+    assert torch.equal(dp.cpu(), torch.from_numpy(ref_p))
+
+
+def test_cross_entropy_backward_beyond_one_launch(cuda):
+    """70,000 rows (past the 65,535 rows of one launch's grid) against the
+    fp64 oracle's gradient, every row including the last launch's."""
+    announce("cross entropy backward, 70000 rows")
+    gen = torch.Generator().manual_seed(23)
+    rows, V = 70000, 64
+    z = (torch.randn(rows, V, generator=gen) * 2).to(torch.bfloat16)
+    lab = torch.randint(0, V, (rows,), generator=gen)
+    bad = torch.zeros(1, dtype=torch.int32, device=cuda)
+    loss, lse = K.xent_fwd(z.to(cuda), lab.to(cuda), bad)
+    g = torch.rand(rows, generator=gen)
+    dz = K.xent_bwd(z.to(cuda), lab.to(cuda), lse, g.to(cuda)).cpu()
+    zr = z.double().requires_grad_(True)
+    ol.vocab_cross_entropy(zr, lab).backward(g.double())
+    err = (dz.double() - zr.grad).abs().amax(dim=1)
+    assert (err <= 2**-7 * zr.grad.abs().amax(dim=1) + 1e-30).all()
+    assert bad.item() == 0
 
 
 def test_embedding_dropout_draws_a_mask_per_call_and_backward_replays_it(cuda):
@@ -355,3 +394,16 @@ def test_first_last_fused_statistics_match_the_standalone_pass(cuda, dtype):
     assert not ok and norm is None
     assert torch.equal(tr.embedding.word_embeddings.weight, before)
     assert tr.optimizer.get_loss_scale().item() == 1024.0  # hysteresis 2: one overflow does not back off
+    # a tied sum that is finite once unscaled but whose loss-scaled value
+    # overflows fp32: the reference sums the scaled addends (inf) and skips
+    # the step, and so does the fused path; the second overflow backs off
+    tr.ddp.zero_grad_buffer()
+    _, lo = tr.forward_backward([5, 9])
+    tr.grad_sync.execute(global_normalization_scale(tr.nominal, lo.local_loss_weight))
+    tr.tie_gradients()
+    tr.embedding.word_embeddings.weight.main_grad[7, 3] = 1e36  # x 1024 > fp32 max
+    ok, norm, _ = tr.optimizer.step()
+    torch.cuda.synchronize()
+    assert not ok and norm is None
+    assert torch.equal(tr.embedding.word_embeddings.weight, before)
+    assert tr.optimizer.get_loss_scale().item() == 512.0

@@ -142,11 +142,53 @@ def test_overlapped_weight_gradients_match_single_stream(cuda):
     assert torch.equal(dx, xi.grad)
 
 
+def _check_step_against_oracle(tr, x, dy, masters_before, step, lr, clip):
+    """After tr.train_step: the main grads the step used (the synced,
+    unscaled gradients the unpack wrote back) against the fp32 layer oracle
+    on the pre-step weights, and the fp32 masters against the oracle's
+    L2 norm / clip / AdamW chain applied to those gradients (1e-6)."""
+    layers = tr.layer_parameters()
+    # the model's 16-bit weights before the step are the bf16 rounding of the masters
+    host = [{k: torch.from_numpy(oadam.to_bf16(masters_before[li][k])) for k in layer} for li, layer in enumerate(layers)]
+    _, _, ref_grads = ol.middle_stage_fwd_bwd(x.float().cpu(), host, 4, dy.float().cpu())
+    grads = [{k: p.main_grad.detach().cpu().numpy().copy() for k, p in layer.items()} for layer in layers]
+    for li, layer in enumerate(grads):
+        for k, g in layer.items():
+            assert _rel(torch.from_numpy(g), ref_grads[li][k]) < 5e-2, (li, k)
+    ref_norm = og.l2_norm([g for layer in grads for g in layer.values()])
+    coef = og.clip_coefficient(ref_norm, clip)
+    for li, layer in enumerate(layers):
+        for k, p in layer.items():
+            wd = 0.1 if k.endswith("_w") and not k.startswith("ln") else 0.0
+            m_prev, v_prev = masters_before[li][k + ".m"], masters_before[li][k + ".v"]
+            ref_p, _, _ = oadam.adamw_step(masters_before[li][k], grads[li][k], m_prev, v_prev, step, lr, 0.9, 0.95,
+                                           1e-8, wd, clip_coef=coef)
+            got = tr.optimizer.optimizer_parameter_for_model_parameter(p).detach().cpu().numpy()
+            np.testing.assert_allclose(got, ref_p, rtol=1e-6, atol=1e-9, err_msg=f"layer {li} {k}")
+    return ref_norm
+
+
+def _optimizer_snapshot(tr):
+    """fp32 masters and AdamW moments per layer and oracle name (numpy)."""
+    snap = []
+    for layer in tr.layer_parameters():
+        d = {}
+        for k, p in layer.items():
+            d[k] = tr.optimizer.optimizer_parameter_for_model_parameter(p).detach().cpu().numpy().copy()
+            st = tr.optimizer.state_for_model_parameter(p)
+            d[k + ".m"] = st["exp_avg"].detach().cpu().numpy().copy() if "exp_avg" in st else np.zeros_like(d[k])
+            d[k + ".v"] = st["exp_avg_sq"].detach().cpu().numpy().copy() if "exp_avg_sq" in st else np.zeros_like(d[k])
+        snap.append(d)
+    return snap
+
+
 def test_streamed_grad_sync_matches_sync_after_backward(cuda):
     """Two identical stages, two steps each: buckets synced during the
     backward (streamed, the default) and the whole sync after it (the
     reference order) give bit-identical norms, master weights and bf16
-    weights."""
+    weights; and each streamed step matches the oracle chain: its gradients
+    the fp32 layer oracle, its norm, clip and AdamW update the grad-sync and
+    AdamW oracles applied to those gradients."""
     announce("streamed grad sync vs sync after backward")
     cfg = GPTConfig(hidden_size=256, num_attention_heads=4, ffn_hidden_size=1024, num_layers=2,
                     seq_length=128, micro_batch_size=2, params_dtype=torch.bfloat16, device="cuda", seed=41)
@@ -156,12 +198,15 @@ def test_streamed_grad_sync_matches_sync_after_backward(cuda):
     batches = [(torch.randn(128, 2, 256, generator=gen).to(torch.bfloat16).to(cuda),
                 (torch.randn(128, 2, 256, generator=gen) * 1e-1).to(torch.bfloat16).to(cuda)) for _ in range(2)]
     norms = [[], []]
-    for x, dy in batches:
+    for step, (x, dy) in enumerate(batches, start=1):
+        before = _optimizer_snapshot(trs[0])
         for i, tr in enumerate(trs):
             _, _, ok, norm = tr.train_step(x, dy, streamed_sync=(i == 0))
             assert ok
             norms[i].append(norm)
-    torch.cuda.synchronize()
+        torch.cuda.synchronize()
+        ref_norm = _check_step_against_oracle(trs[0], x, dy, before, step, 1e-3, 0.5)
+        assert norms[0][-1] == pytest.approx(ref_norm, rel=1e-6)
     assert norms[0] == norms[1]
     for pa, pb in zip(trs[0].model.parameters(), trs[1].model.parameters()):
         assert torch.equal(pa, pb)

@@ -61,6 +61,37 @@ def _randomize(tr, gen):
     tr.optimizer.reload_model_params()
 
 
+def _check_against_oracle(whole, x, dy, out, dx, grads):
+    """The stage's output, input gradient and main grads (`grads`: per layer,
+    oracle parameter name -> tensor) against the fp32 CPU oracle of the
+    uncut stage on `whole`'s weights: output and input gradient within 2e-2,
+    each gradient's norm within 2e-2 and its relative error within 5e-2
+    (the north-star bars)."""
+    host = [{k: p.detach().float().cpu() for k, p in layer.items()} for layer in whole.layer_parameters()]
+    ref_out, ref_dx, ref_grads = ol.middle_stage_fwd_bwd(x.float().cpu(), host, HEADS, dy.float().cpu())
+    assert _rel(out, ref_out) < 2e-2
+    assert _rel(dx, ref_dx) < 2e-2
+    assert len(grads) == len(ref_grads)
+    for li, ref in enumerate(ref_grads):
+        assert sorted(grads[li]) == sorted(ref)
+        for k, r in ref.items():
+            g = grads[li][k]
+            gn, rn = g.double().norm().item(), r.double().norm().item()
+            assert abs(gn - rn) <= 2e-2 * rn + 1e-12, (li, k, gn, rn)
+            assert _rel(g, r) < 5e-2, (li, k, _rel(g, r))
+
+
+def _layer_main_grads(*trainers):
+    """{layer: {oracle name: main grad}} merged over stages that together
+    cover whole layers (a cut layer's ops come from two trainers)."""
+    merged = {}
+    for tr in trainers:
+        for li, layer in enumerate(tr.layer_parameters()):
+            first = (min(op.op_index for op in tr.model.language_model.ops) - 1) // 10
+            merged.setdefault(first + li, {}).update({k: p.main_grad for k, p in layer.items()})
+    return [merged[k] for k in sorted(merged)]
+
+
 def _inputs(gen, dtype=torch.bfloat16, mb=MB):
     x = torch.randn(SEQ, mb, H, generator=gen).to(dtype).cuda()
     dy = (torch.randn(SEQ, mb, H, generator=gen) * 1e-2).to(dtype).cuda()
@@ -73,7 +104,9 @@ def test_stage_cut_inside_a_layer_gives_the_uncut_gradients(cuda):
     projection bias (output_bias) cross the cut as side-channel tensors.
     Outputs, the input gradient and every main grad equal the uncut stage's
     bit for bit, except the projection bias, whose gradient crosses the cut
-    as a bf16 tensor (as in the reference) instead of straight into fp32."""
+    as a bf16 tensor (as in the reference) instead of straight into fp32;
+    and the cut pair's outputs, input gradient and main grads match the fp32
+    oracle of the whole stage."""
     announce("stage cut inside a layer")
     gen = torch.Generator().manual_seed(3)
     whole = MiddleStageTrainer(_cfg())
@@ -111,6 +144,8 @@ def test_stage_cut_inside_a_layer_gives_the_uncut_gradients(cuda):
             else:
                 assert torch.equal(g, p.main_grad), (op.op_index, n)
     assert len(cut) == len(gw)
+    _check_against_oracle(whole, x, dy, b_out["hidden_states"], a_in_grads["hidden_states"],
+                          _layer_main_grads(first, second))
 
 
 def test_microbatches_accumulate_main_grads(cuda):
@@ -149,7 +184,9 @@ def test_recompute_is_bit_identical(cuda, pattern, dropout):
     """Activation recompute over whole layers, or over the middle of each
     layer (ops 1-6: QKV to the 2nd LayerNorm, so side-channel tensors cross
     the segment edges), gives the outputs, input gradient and main grads of
-    the plain stage bit for bit, with dropout masks replayed."""
+    the plain stage bit for bit, with dropout masks replayed; without
+    dropout the recomputed stage also matches the fp32 oracle (which has no
+    dropout)."""
     announce(f"recompute {pattern} dropout {dropout}")
     gen = torch.Generator().manual_seed(6)
     flags = {"all": [1] * 20, "attention-only": ([0] + [1] * 6 + [0] * 3) * 2}[pattern]
@@ -171,6 +208,8 @@ def test_recompute_is_bit_identical(cuda, pattern, dropout):
         assert torch.equal(gp[name], gc[name]), name
     if dropout:
         assert any(getattr(op, "_calls", 0) for op in ckpt.model.language_model.ops)
+    else:
+        _check_against_oracle(ckpt, x, dy, out_c, dx_c, _layer_main_grads(ckpt))
 
 
 def test_first_last_microbatches_match_the_fp64_oracle(cuda):
@@ -271,6 +310,47 @@ def test_trainer_evidence_snapshot_and_runtime_record(cuda, tmp_path):
         assert r["optimizer_parameter"].dtype == torch.float32
         assert r["optimizer_state"]["step"].item() == 1.0
         assert set(r["optimizer_hyperparameters"]) == {"beta1", "beta2", "epsilon", "weight_decay"}
+
+
+def test_post_sync_evidence_holds_the_loss_scaled_gradients(cuda, tmp_path):
+    """fp16 first+last stage with loss scale 2^16 and the unscale fused into
+    the sync's unpack: the post_sync snapshot records the main grads as the
+    reference does before optimizer.step() -- still loss-scaled -- so each
+    equals its pre_sync value times the normalization scale, and the tied
+    word embedding the (scaled) sum of its two copies', bit for bit; the
+    clock carries the loss scale."""
+    announce("post_sync evidence under loss scaling")
+    from eth_amd.loss import global_normalization_scale
+
+    cfg = GPTConfig(hidden_size=H, num_attention_heads=HEADS, ffn_hidden_size=FFN, num_layers=2, seq_length=SEQ,
+                    micro_batch_size=MB, padded_vocab_size=50304, params_dtype=torch.float16, device="cuda", seed=17)
+    tr = FirstLastStageTrainer(cfg, initial_loss_scale=2.0**16)
+    assert tr.optimizer.grads_unscaled_by_sync
+    tr.ddp.zero_grad_buffer()
+    _, lo = tr.forward_backward([3, 8])
+    pre = load_rank_snapshot(tr.record_evidence(tmp_path, "pre_sync", 1))
+    ns = np.float32(global_normalization_scale(tr.nominal, lo.local_loss_weight).item())
+    assert ns != 1.0
+    tr.grad_sync.execute(float(ns))
+    tr.tie_gradients()
+    post = load_rank_snapshot(tr.record_evidence(tmp_path, "post_sync", 1))
+    torch.cuda.synchronize()
+    assert post["clock"]["loss_scale"] == 2.0**16
+    by_ptr = {b.main_grad.data_ptr(): b.logical_param_id for b in tr.bindings}
+    word = by_ptr[tr.embedding.word_embeddings.weight.main_grad.data_ptr()]
+    head = by_ptr[tr.post.word_embeddings.weight.main_grad.data_ptr()]
+    pre_g = {r["descriptor"]["logical_param_id"]: r["main_grad"] for r in pre["records"]}
+    nst = torch.tensor(ns)
+    for r in post["records"]:
+        lid = r["descriptor"]["logical_param_id"]
+        if lid in (word, head):
+            expect = pre_g[word] * nst + pre_g[head] * nst
+        else:
+            expect = pre_g[lid] * nst
+        assert torch.equal(r["main_grad"], expect), lid
+    # the trainer's own main grads stay unscaled for the step
+    g = tr.embedding.position_embeddings.weight.main_grad
+    assert torch.equal(g.cpu() * 2.0**16, pre_g[by_ptr[g.data_ptr()]] * nst)
 
 
 def test_snapshot_after_an_overlapped_update_sees_the_updated_parameters(cuda, tmp_path):

@@ -325,3 +325,33 @@ def test_ordered_embedding_grad_equals_index_add():
             assert torch.allclose(torch.from_numpy(word).double(), ref_w, rtol=2**-23, atol=0)
         else:
             assert torch.allclose(torch.from_numpy(word).double(), ref_w, rtol=0, atol=1e-5)
+
+
+def test_chunked_ordered_embedding_grad_sums_every_chunk():
+    """The chunked order (consecutive chunks of whole sequence positions):
+    with small-integer gradients and zero tables every partial sum is
+    exact, so any chunk size gives index_add exactly (a dropped or repeated
+    chunk fails); a chunk covering the whole input is the unchunked order."""
+    import numpy as np
+
+    gen = torch.Generator().manual_seed(13)
+    s, b, h, V = 11, 3, 8, 5
+    tok = torch.randint(0, V, (b, s), generator=gen)
+    pos = torch.arange(s).expand(b, s).contiguous()
+    dout = torch.randint(-8, 9, (s, b, h), generator=gen).float()
+    flat = dout.transpose(0, 1).reshape(-1, h).double()
+    ref_w = torch.zeros(V, h, dtype=torch.float64).index_add(0, tok.reshape(-1), flat)
+    ref_p = torch.zeros(s, h, dtype=torch.float64).index_add(0, pos.reshape(-1), flat)
+    for chunk in (1, 3, 7, 12, 33, 1 << 20):
+        word, posg = np.zeros((V, h), dtype=np.float32), np.zeros((s, h), dtype=np.float32)
+        ol.embedding_grad_ordered(tok.numpy(), pos.numpy(), dout.numpy(), word, posg, chunk_rows=chunk)
+        assert torch.equal(torch.from_numpy(word).double(), ref_w), chunk
+        assert torch.equal(torch.from_numpy(posg).double(), ref_p), chunk
+    # random gradients into a random table: one chunk over everything is the
+    # default order bit for bit
+    dout = torch.randn(s, b, h, generator=gen)
+    start = torch.randn(V, h, generator=gen).numpy()
+    a, c = start.copy(), start.copy()
+    ol.embedding_grad_ordered(tok.numpy(), pos.numpy(), dout.numpy(), a, None)
+    ol.embedding_grad_ordered(tok.numpy(), pos.numpy(), dout.numpy(), c, None, chunk_rows=s * b)
+    assert np.array_equal(a, c)
