@@ -51,10 +51,9 @@ __device__ __forceinline__ bool aligned16(const T* p) {
 }
 
 // ---------------------------------------------------------------- pack ---
+// payload[c.dst + i] = src[i] * c.scale for one chunk (the whole workgroup)
 template <typename T>
-__global__ void __launch_bounds__(kThreads) pack_kernel(const eth_chunk_t* __restrict__ chunks,
-                                                        T* __restrict__ payload, int dtype) {
-  const eth_chunk_t c = chunks[blockIdx.x];
+__device__ __forceinline__ void pack_chunk(const eth_chunk_t& c, T* __restrict__ payload, int dtype) {
   const T* src = reinterpret_cast<const T*>(c.src);
   T* dst = payload + c.dst;
   const float scale = c.scale;
@@ -107,22 +106,89 @@ __global__ void __launch_bounds__(kThreads) pack_kernel(const eth_chunk_t* __res
   }
 }
 
-// -------------------------------------------------------------- unpack ---
-// One element of the fused unpack; returns g*g for the norm statistic.
 template <typename T>
-__device__ __forceinline__ float unpack_one(T& pay, T& out, float norm, float inv, int flags,
-                                            int dtype, bool& bad) {
+__global__ void __launch_bounds__(kThreads) pack_kernel(const eth_chunk_t* __restrict__ chunks,
+                                                        T* __restrict__ payload, int dtype) {
+  pack_chunk<T>(chunks[blockIdx.x], payload, dtype);
+}
+
+// -------------------------------------------------------------- unpack ---
+// One element of the fused unpack: v = payload * norm (rounded to T when
+// norm != 1), stored to *keep when keep is given; the gradient g = v (times
+// inv with ETH_UNPACK_UNSCALE) to out.  Returns g*g for the norm statistic.
+template <typename T>
+__device__ __forceinline__ float unpack_one(T pay, T* keep, T& out, float norm, float inv, int flags, int dtype,
+                                            bool& bad) {
   float v = Elem<T>::get(pay, dtype);
+  T vb = pay;
   if (norm != 1.0f) {
-    T r = Elem<T>::put(v * norm, dtype);
-    v = Elem<T>::get(r, dtype);
-    if (flags & ETH_UNPACK_WRITEBACK) pay = r;
+    vb = Elem<T>::put(v * norm, dtype);
+    v = Elem<T>::get(vb, dtype);
   }
+  if (keep) *keep = vb;
   float g = v;
   if (flags & ETH_UNPACK_UNSCALE) g = v * inv;  // fp32 only (checked on host)
   bad |= !isfinite(v);
   out = Elem<T>::put(g, dtype);
   return g * g;
+}
+
+// One chunk of the unpack: payload values from `src` (the chunk's payload
+// range), the normalized payload values to `keep` (the same range of a
+// payload buffer, possibly `src` itself; nullptr: not kept), gradients to the
+// chunk's main_grad block.
+template <typename T>
+__device__ __forceinline__ void unpack_chunk(const eth_chunk_t& c, const T* src, T* keep, float norm, float inv,
+                                             int flags, int dtype, float& sq, bool& bad) {
+  T* dstp = reinterpret_cast<T*>(c.src);
+  const int64_t n = (int64_t)c.rows * c.row_len;
+  constexpr int VW = Elem<T>::kVec;
+  typedef typename Elem<T>::V V;
+  if (c.rows == 1 && aligned16(dstp) && aligned16(src) && (keep == nullptr || aligned16(keep))) {
+    // kPipe 16-byte loads in flight per thread; main_grad is not read again
+    // before the optimizer, after every bucket (nontemporal stores)
+    const int nv = (int)(n / VW);
+    const gs_v4* p = reinterpret_cast<const gs_v4*>(src);
+    gs_v4* kp = reinterpret_cast<gs_v4*>(keep);
+    gs_v4* d = reinterpret_cast<gs_v4*>(dstp);
+    auto one_vec = [&](gs_v4 xv, int idx) __attribute__((always_inline)) {
+      V x = __builtin_bit_cast(V, xv), k, y;
+      T* xe = reinterpret_cast<T*>(&x);
+      T* ke = reinterpret_cast<T*>(&k);
+      T* ye = reinterpret_cast<T*>(&y);
+#pragma unroll
+      for (int j = 0; j < VW; ++j) sq += unpack_one<T>(xe[j], ke + j, ye[j], norm, inv, flags, dtype, bad);
+      if (kp) kp[idx] = __builtin_bit_cast(gs_v4, k);
+      __builtin_nontemporal_store(__builtin_bit_cast(gs_v4, y), d + idx);
+    };
+    int i = threadIdx.x;
+    for (; i + (kPipe - 1) * kThreads < nv; i += kPipe * kThreads) {
+      gs_v4 x[kPipe];
+#pragma unroll
+      for (int u = 0; u < kPipe; ++u) x[u] = p[i + u * kThreads];
+#pragma unroll
+      for (int u = 0; u < kPipe; ++u) one_vec(x[u], i + u * kThreads);
+    }
+    for (; i < nv; i += kThreads) one_vec(p[i], i);
+    for (int64_t i = (int64_t)nv * VW + threadIdx.x; i < n; i += kThreads)
+      sq += unpack_one<T>(src[i], keep ? keep + i : nullptr, dstp[i], norm, inv, flags, dtype, bad);
+  } else {
+    for (int64_t i = threadIdx.x; i < n; i += kThreads) {
+      const int64_t r = i / c.row_len, col = i - r * c.row_len;
+      sq += unpack_one<T>(src[i], keep ? keep + i : nullptr, dstp[r * c.src_stride + col], norm, inv, flags, dtype,
+                          bad);
+    }
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void unpack_stats(const eth_chunk_t& c, int flags, float sq, bool bad, float* found_inf,
+                                             double* partials, int64_t slot, float* red) {
+  if (flags & ETH_UNPACK_STATS) {
+    if (bad) *found_inf = 1.0f;
+    float tot = block_sum<kThreads>(sq, red);
+    if (threadIdx.x == 0) partials[slot] = (c.flags & ETH_CHUNK_NORM) ? (double)tot : 0.0;
+  }
 }
 
 template <typename T>
@@ -134,56 +200,42 @@ __global__ void __launch_bounds__(kThreads) unpack_kernel(const eth_chunk_t* __r
                                                           int64_t partial_base) {
   __shared__ float red[kThreads / 64];
   const eth_chunk_t c = chunks[blockIdx.x];
-  if (c.flags & ETH_CHUNK_SHADOWED) flags &= ~ETH_UNPACK_WRITEBACK;
-  T* dstp = reinterpret_cast<T*>(c.src);
+  // the normalized payload is written back in place (the reference's
+  // payload.mul_), except where a later bucket of the pass packs over it
+  const bool wb = (flags & ETH_UNPACK_WRITEBACK) && norm != 1.0f && !(c.flags & ETH_CHUNK_SHADOWED);
   T* pay = payload + c.dst;
-  const int64_t n = (int64_t)c.rows * c.row_len;
-  constexpr int VW = Elem<T>::kVec;
-  typedef typename Elem<T>::V V;
   float sq = 0.f;
   bool bad = false;
-  if (c.rows == 1 && aligned16(dstp) && aligned16(pay)) {
-    // kPipe 16-byte loads in flight per thread; main_grad is not read again
-    // before the optimizer, after every bucket (nontemporal stores)
-    const int nv = (int)(n / VW);
-    gs_v4* p = reinterpret_cast<gs_v4*>(pay);
-    gs_v4* d = reinterpret_cast<gs_v4*>(dstp);
-    const bool wb = (flags & ETH_UNPACK_WRITEBACK) && norm != 1.0f;
-    auto one_vec = [&](gs_v4& xv, int idx) __attribute__((always_inline)) {
-      V x = __builtin_bit_cast(V, xv), y;
-      T* xe = reinterpret_cast<T*>(&x);
-      T* ye = reinterpret_cast<T*>(&y);
-#pragma unroll
-      for (int j = 0; j < VW; ++j) sq += unpack_one<T>(xe[j], ye[j], norm, inv, flags, dtype, bad);
-      if (wb) p[idx] = __builtin_bit_cast(gs_v4, x);
-      __builtin_nontemporal_store(__builtin_bit_cast(gs_v4, y), d + idx);
-    };
-    int i = threadIdx.x;
-    for (; i + (kPipe - 1) * kThreads < nv; i += kPipe * kThreads) {
-      gs_v4 x[kPipe];
-#pragma unroll
-      for (int u = 0; u < kPipe; ++u) x[u] = p[i + u * kThreads];
-#pragma unroll
-      for (int u = 0; u < kPipe; ++u) one_vec(x[u], i + u * kThreads);
-    }
-    for (; i < nv; i += kThreads) {
-      gs_v4 x = p[i];
-      one_vec(x, i);
-    }
-    for (int64_t i = (int64_t)nv * VW + threadIdx.x; i < n; i += kThreads)
-      sq += unpack_one<T>(pay[i], dstp[i], norm, inv, flags, dtype, bad);
-  } else {
-    for (int64_t i = threadIdx.x; i < n; i += kThreads) {
-      const int64_t r = i / c.row_len, col = i - r * c.row_len;
-      sq += unpack_one<T>(pay[i], dstp[r * c.src_stride + col], norm, inv, flags, dtype, bad);
-    }
+  unpack_chunk<T>(c, pay, wb ? pay : nullptr, norm, inv, flags, dtype, sq, bad);
+  unpack_stats<T>(c, flags, sq, bad, found_inf, partials, partial_base + blockIdx.x, red);
+}
+
+// ------------------------------------------------------ staged local pass ---
+// One launch of the staged single-rank pass: workgroups [0, nu) unpack bucket
+// k-1 from its staging half `ustage`, the rest pack bucket k into the other
+// half `pstage`, so the two touch different memory.  A chunk that no later
+// bucket packs over (not ETH_CHUNK_SHADOWED) also stores its payload values v
+// into the bucket's own payload `upay` -- the values the per-bucket sequence
+// leaves there -- so that buffer ends the pass as that sequence leaves it.
+template <typename T>
+__global__ void __launch_bounds__(kThreads) staged_step_kernel(const eth_chunk_t* __restrict__ uchunks, int nu,
+                                                               const T* __restrict__ ustage, T* __restrict__ upay,
+                                                               const eth_chunk_t* __restrict__ pchunks,
+                                                               T* __restrict__ pstage, int dtype, float norm,
+                                                               float inv, int flags, float* __restrict__ found_inf,
+                                                               double* __restrict__ partials,
+                                                               int64_t partial_base) {
+  __shared__ float red[kThreads / 64];
+  if ((int)blockIdx.x >= nu) {  // uniform per workgroup
+    pack_chunk<T>(pchunks[blockIdx.x - nu], pstage, dtype);
+    return;
   }
-  if (flags & ETH_UNPACK_STATS) {
-    if (bad) *found_inf = 1.0f;
-    float tot = block_sum<kThreads>(sq, red);
-    if (threadIdx.x == 0)
-      partials[partial_base + blockIdx.x] = (c.flags & ETH_CHUNK_NORM) ? (double)tot : 0.0;
-  }
+  const eth_chunk_t c = uchunks[blockIdx.x];
+  float sq = 0.f;
+  bool bad = false;
+  unpack_chunk<T>(c, ustage + c.dst, (c.flags & ETH_CHUNK_SHADOWED) ? nullptr : upay + c.dst, norm, inv, flags,
+                  dtype, sq, bad);
+  unpack_stats<T>(c, flags, sq, bad, found_inf, partials, partial_base + blockIdx.x, red);
 }
 
 // ------------------------------------------------- standalone statistics ---
@@ -383,6 +435,33 @@ __global__ void __launch_bounds__(kFillThreads) fill_kernel(float* dst, int64_t 
   }
 }
 
+template <typename T>
+static void staged_launch(const eth_bucket_t* u, const void* ustage, const eth_bucket_t* p, void* pstage,
+                          float norm, float inv, int flags, float* found_inf, double* partials, hipStream_t s) {
+  const int nu = u ? (int)u->n_chunks : 0, np = p ? (int)p->n_chunks : 0;
+  staged_step_kernel<T><<<nu + np, kThreads, 0, s>>>(
+      u ? u->chunks : nullptr, nu, (const T*)ustage, u ? (T*)u->payload : nullptr, p ? p->chunks : nullptr,
+      (T*)pstage, u ? u->dtype : p->dtype, norm, inv, flags, found_inf, partials, u ? u->partial_base : 0);
+}
+
+static void staged_step(const eth_bucket_t* u, const void* ustage, const eth_bucket_t* p, void* pstage, float norm,
+                        float inv, int flags, float* found_inf, double* partials, hipStream_t s) {
+  if (u && u->n_chunks == 0) u = nullptr;
+  if (p && p->n_chunks == 0) p = nullptr;
+  if (!u && !p) return;
+  if (u && p && u->dtype != p->dtype) {  // one dtype per launch
+    staged_step(u, ustage, nullptr, nullptr, norm, inv, flags, found_inf, partials, s);
+    staged_step(nullptr, nullptr, p, pstage, norm, inv, flags, found_inf, partials, s);
+    return;
+  }
+  const int dtype = u ? u->dtype : p->dtype;
+  const int f = dtype == ETH_F32 ? flags : flags & ~ETH_UNPACK_UNSCALE;
+  if (dtype == ETH_F32)
+    staged_launch<float>(u, ustage, p, pstage, norm, inv, f, found_inf, partials, s);
+  else
+    staged_launch<uint16_t>(u, ustage, p, pstage, norm, inv, f, found_inf, partials, s);
+}
+
 }  // namespace eth
 
 using namespace eth;
@@ -460,7 +539,9 @@ int eth_bucket_unpack(const eth_chunk_t* chunks, int64_t n_chunks, void* payload
 
 int eth_bucket_sync_local(const eth_bucket_t* buckets, int64_t n_buckets, float normalization_scale,
                           float inv_loss_scale, int flags, float* found_inf, double* partials,
-                          void* stream) {
+                          void* staging, int64_t staging_half_bytes, void* stream) {
+  ETH_CHECK_ARG(!staging || (staging_half_bytes > 0 && staging_half_bytes % 16 == 0 && ((uintptr_t)staging & 15) == 0),
+                "eth_bucket_sync_local: staging must be 16-byte aligned halves");
   ETH_CHECK_ARG(n_buckets >= 0 && (n_buckets == 0 || buckets), "eth_bucket_sync_local: bad bucket array");
   ETH_CHECK_ARG(!(flags & ETH_UNPACK_STATS) || (found_inf && partials),
                 "eth_bucket_sync_local: statistics requested without buffers");
@@ -474,6 +555,20 @@ int eth_bucket_sync_local(const eth_bucket_t* buckets, int64_t n_buckets, float 
                   "eth_bucket_sync_local: bucket %lld has a bad chunk table or payload", (long long)i);
     ETH_CHECK_ARG(b.partial_base >= 0, "eth_bucket_sync_local: bucket %lld has a negative partial base",
                   (long long)i);
+  }
+  if (staging) {
+    // bucket i packs into staging half (i & 1) and unpacks from it; step k
+    // unpacks bucket k-1 and packs bucket k in one launch
+    char* half[2] = {(char*)staging, (char*)staging + staging_half_bytes};
+    hipStream_t s = (hipStream_t)stream;
+    for (int64_t k = 0; k <= n_buckets; ++k) {
+      const eth_bucket_t* u = k > 0 ? &buckets[k - 1] : nullptr;
+      const eth_bucket_t* p = k < n_buckets ? &buckets[k] : nullptr;
+      staged_step(u, half[(k - 1) & 1], p, half[k & 1], normalization_scale, inv_loss_scale, flags, found_inf,
+                  partials, s);
+      ETH_CHECK_LAUNCH("eth_bucket_sync_local");
+    }
+    return ETH_OK;
   }
   for (int64_t i = 0; i < n_buckets; ++i) {
     const eth_bucket_t& b = buckets[i];

@@ -322,6 +322,16 @@ class GradientBucketExecutor:
             local[i] = (dev.data_ptr() if dev is not None else 0, n_chunks, payload.data_ptr(), base,
                         nat.dtype_code(payload.dtype), 0)
         self._local_pass = local
+        # staging for the single-rank pass: two halves, each the largest
+        # payload of the pass, so one launch unpacks a bucket while it packs
+        # the next (the identity seam only; a real collective reads the
+        # scratch buffer itself)
+        self._staging, self._staging_half = None, 0
+        if self._all_reduce_sum is local_all_reduce_sum and tables and self._device is not None:
+            half = max(b.exact_numel * self._scratch[b.grad_dtype].element_size() for b, *_ in tables)
+            half = (half + 255) // 256 * 256
+            self._staging = torch.empty(2 * half, dtype=torch.uint8, device=self._device)
+            self._staging_half = half
         return tables
 
     # ----------------------------------------------------------- statistics --
@@ -451,6 +461,8 @@ class GradientBucketExecutor:
                 flags,
                 nat.ptr(stats.found_inf) if stats is not None else None,
                 nat.ptr(stats.partials) if stats is not None else None,
+                nat.ptr(self._staging) if self._staging is not None else None,
+                self._staging_half,
                 nat.stream_ptr(self._device),
             )
         else:

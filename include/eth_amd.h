@@ -100,18 +100,28 @@ typedef struct eth_bucket {
 
 /* A whole sync pass over `n_buckets` buckets (host array, in order) whose
  * all-reduce is the identity -- every process group of the pass holds this
- * rank alone: for each bucket, eth_bucket_pack then eth_bucket_unpack with
- * the pass's scale, flags and statistics buffers (ETH_UNPACK_UNSCALE applies
- * to fp32 payloads only), the same launches in the same order, so the
- * results are bit-identical to the per-bucket calls.  Every entry is checked
- * before the first launch.  One host call instead of two per bucket, so the
- * host stays ahead of the GPU through the pass.
+ * rank alone -- with the pass's scale, flags and statistics buffers
+ * (ETH_UNPACK_UNSCALE applies to fp32 payloads only).  Every entry is
+ * checked before the first launch.  One host call instead of two per
+ * bucket, so the host stays ahead of the GPU through the pass.
+ * Without `staging` (NULL): for each bucket, eth_bucket_pack then
+ * eth_bucket_unpack, the launches of the per-bucket calls in their order.
+ * With `staging` (16-byte aligned, two halves of `staging_half_bytes`, each
+ * at least the largest payload of the pass): bucket i is packed into half
+ * (i & 1) and unpacked from it, and one launch unpacks bucket i-1 while it
+ * packs bucket i (n_buckets + 1 launches instead of 2 * n_buckets).  The
+ * gradients, statistics and the payload buffers' final contents are
+ * bit-identical to the per-bucket calls: a chunk that no later bucket packs
+ * over (not ETH_CHUNK_SHADOWED) stores its payload values -- normalized,
+ * when normalization_scale != 1 -- into the bucket's payload buffer, which
+ * is what the per-bucket sequence leaves there.
  * Replaces the bucket loop of GradientBucketExecutor.execute
  * (eth/runtime/megatron/grad_sync/executor.py:248-260) for a single-rank
  * data-parallel group. */
 int eth_bucket_sync_local(const eth_bucket_t* buckets, int64_t n_buckets,
                           float normalization_scale, float inv_loss_scale, int flags,
-                          float* found_inf, double* partials, void* stream);
+                          float* found_inf, double* partials, void* staging,
+                          int64_t staging_half_bytes, void* stream);
 
 /* Standalone unscale + inf/nan check + sum of squares over chunk-described
  * fp32 gradients, in place (g *= inv_scale when ETH_UNPACK_UNSCALE).  Used

@@ -282,14 +282,17 @@ def test_strided_tp_segments_vs_oracle(cuda):
     np.testing.assert_array_equal(g.cpu().numpy(), host["w"])
 
 
+@pytest.mark.parametrize("scale", [0.3701, 1.0])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
-def test_local_pass_matches_the_per_bucket_calls(cuda, dtype):
+def test_local_pass_matches_the_per_bucket_calls(cuda, dtype, scale):
     """eth_bucket_sync_local (the identity seam, one native call for the
-    pass) against run_bucket's two launches per bucket through a seam that
-    is not the identity object: main grads, the last payload, found_inf and
-    every L2 partial bit for bit, with a normalization scale, an unscale (fp32
-    only) and an inf planted on the second call."""
-    announce(f"grad_sync local pass vs per-bucket calls, {dtype}")
+    pass; each bucket staged in one of two halves, one launch unpacking a
+    bucket while it packs the next) against run_bucket's two launches per
+    bucket through a seam that is not the identity object: main grads, the
+    whole scratch buffer, found_inf and every L2 partial bit for bit, with
+    and without a normalization scale, an unscale (fp32 only) and an inf
+    planted on the second call."""
+    announce(f"grad_sync local pass vs per-bucket calls, {dtype}, scale {scale}")
     setups = [_gpt_setup(cuda, 64, 256, 3, 1 << 13, "block", seed=21, dtype=dtype) for _ in range(2)]
     exs, sts = [], []
     for seam, (plan, descs, grads, bindings) in zip((local_all_reduce_sum, lambda p, h: None), setups):
@@ -308,7 +311,7 @@ def test_local_pass_matches_the_per_bucket_calls(cuda, dtype):
             for _, _, grads, _ in setups:
                 next(iter(grads.values())).view(-1)[17] = float("inf")
         for ex in exs:
-            ex.execute(0.3701)
+            ex.execute(scale)
         torch.cuda.synchronize()
         for a, b in zip(setups[0][2].values(), setups[1][2].values()):
             assert torch.equal(a.view(torch.int16 if dtype != torch.float32 else torch.int32),
@@ -335,7 +338,7 @@ def test_local_pass_rejects_a_bad_entry_before_launching(cuda):
     entries[-1]["dtype"] = 9
     with pytest.raises(ValueError, match="unsupported dtype"):
         nat.call("eth_bucket_sync_local", ctypes.c_void_p(entries.ctypes.data), len(entries), 1.0, 1.0, 0,
-                 None, None, nat.stream_ptr(cuda))
+                 None, None, nat.ptr(ex._staging), ex._staging_half, nat.stream_ptr(cuda))
     torch.cuda.synchronize()
     assert bool((ex.scratch(name) == -7.0).all())
 
