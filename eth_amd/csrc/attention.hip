@@ -377,21 +377,71 @@ __global__ void __launch_bounds__(kAttnThreads, 2) attn_fwd_kernel(AttnArgs a) {
 // Eight waves: wave w < 4 (the dV wave) and wave w + 4 (the dK wave) own the
 // same 32 keys and share a SIMD.  Per step of 64 queries the dV wave computes
 // S = Q K^T and P and hands P (fp32) to its partner through LDS; the dK wave
-// meanwhile computes dP = dO V^T.  After the hand-over the dV wave adds
-// P^T dO into dV while the dK wave forms dS = P (dP - delta) and adds
-// dS^T Q into dK.  S and P are computed once per step (the split dV and dK
-// kernels each recompute them), and on every SIMD one wave's exponentials or
-// dS arithmetic overlap the other wave's MFMAs.  S = Q K^T is computed with
-// lane = key (the mirror image of the forward's layout, query rows swizzled),
-// so P and dS are already the A operands of dV += P^T dO and dK += dS^T Q.
+// meanwhile computes dP = dO V^T and subtracts delta.  After the hand-over
+// the dV wave adds P^T dO into dV while the dK wave forms dS = P (dP - delta)
+// and adds dS^T Q into dK.  S and P are computed once per step (the split dV
+// and dK kernels each recompute them), and on every SIMD one wave's
+// exponentials or dS arithmetic overlap the other wave's MFMAs.  S = Q K^T
+// is computed with lane = key (the mirror image of the forward's layout,
+// query rows swizzled), so P and dS are already the A operands of
+// dV += P^T dO and dK += dS^T Q.
+//
+// The Q and dO rows of a step are kept twice in LDS: a row-swizzled copy
+// (rows of D + 8) read as A operands in the first half of the step, and a
+// natural copy (rows padded for the transposing reads) read as B operands
+// in the second half.  Both are filled by direct global->LDS loads, each in
+// the half-step before it is read: the next step's row-swizzled copy during
+// this step's second half, the next step's natural copy during its first
+// half.  A step therefore has two barriers (P handed over; step done) and
+// no copy phase of its own.
+template <int ROWS, int D, int UPR, bool SWZ>
+struct DmaCopy {
+  // one LDS copy of a ROWS x D tile, rows of UPR 16-byte units (the first
+  // D / 8 hold data, the rest padding), moved by the four waves of a role:
+  // lane l of piece j fills unit (piece * 64 + l) of the image
+  static constexpr int PIECES = ROWS * UPR / 64;
+  static constexpr int PW = (PIECES + 3) / 4;  // pieces per wave (the last wave may have fewer)
+  static_assert(ROWS * UPR % 64 == 0, "whole pieces");
+  int32_t off[PW];
+  int32_t row_in_tile[PW];  // image row of the unit (tile row via the swizzle), -1 for padding units
+  int w;                    // wave within the role (wave-uniform)
+  __device__ __forceinline__ void init(const AttnTensor& t, int b, int h, int hd, int wave, int lane) {
+    w = wave;
+#pragma unroll
+    for (int j = 0; j < PW; ++j) {
+      const int u = (w * PW + j) * 64 + lane;
+      const int p = u / UPR, c = u % UPR;
+      const int q = SWZ ? swz(p) : p;  // image row p holds tile row q
+      const bool data = c < D / 8 && c * 8 < hd && p < ROWS;
+      row_in_tile[j] = data ? q : -1;
+      off[j] = data ? (int32_t)(((int64_t)b * t.sb + (int64_t)h * t.sh + (int64_t)q * t.ss + c * 8) * 2) : kAttnOob;
+    }
+  }
+  // rows [r0, r0 + ROWS) of the tensor into the image at S; with PAD, rows
+  // at or past `seq` read zeros
+  template <bool PAD>
+  __device__ __forceinline__ void issue(uint16_t* S, a_rsrc_t rs, int32_t row_bytes, int r0, int seq) const {
+#pragma unroll
+    for (int j = 0; j < PW; ++j) {
+      if (w * PW + j >= PIECES) break;  // wave-uniform
+      const int32_t o = !PAD || (row_in_tile[j] >= 0 && r0 + row_in_tile[j] < seq) ? off[j] : kAttnOob;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(S + (w * PW + j) * 512),
+                                               16, o, r0 * row_bytes, 0, 0);
+    }
+  }
+};
+
 template <int D, bool FP16, bool PAD>
 __global__ void __launch_bounds__(2 * kAttnThreads, 1) attn_bwd_dkdv_pair_kernel(AttnArgs a) {
   constexpr int KS = D / 16, DT = D / 32;
   constexpr int QN = tr_row(D);
-  __shared__ __attribute__((aligned(16))) uint16_t Qs[kBQ2 * (D + 8)];
-  __shared__ __attribute__((aligned(16))) uint16_t dOs[kBQ2 * (D + 8)];
-  __shared__ __attribute__((aligned(16))) uint16_t Qn[kBQ2 * QN];
-  __shared__ __attribute__((aligned(16))) uint16_t dOn[kBQ2 * QN];
+  constexpr int AL = D + 8;  // row length of the row-swizzled copy
+  typedef DmaCopy<kBQ2, D, AL / 8, true> RowCopy;
+  typedef DmaCopy<kBQ2, D, QN / 8, false> TrCopy;
+  __shared__ __attribute__((aligned(16))) uint16_t Qs[RowCopy::PIECES * 512];
+  __shared__ __attribute__((aligned(16))) uint16_t dOs[RowCopy::PIECES * 512];
+  __shared__ __attribute__((aligned(16))) uint16_t Qn[TrCopy::PIECES * 512];
+  __shared__ __attribute__((aligned(16))) uint16_t dOn[TrCopy::PIECES * 512];
   // P of a step's two 32-query tiles per key group: registers 4g..4g+3 of a
   // lane as 16 contiguous bytes, the 64 lanes side by side
   __shared__ a_u32x4 Ps[4][2][4][64];
@@ -422,50 +472,49 @@ __global__ void __launch_bounds__(2 * kAttnThreads, 1) attn_bwd_dkdv_pair_kernel
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[t][r] = 0.f;
 
-  // the dV waves move the Q rows, the dK waves the dO rows; the next step's
-  // rows, and its queries' lse (dV) or delta (dK), load during this step
-  BufTile<kBQ2, D, D + 8, true, PAD> tile;
-  tile.init(dkw ? a.dout : a.q, b, h, a.S, a.hd, rt);
+  // the dV waves move the Q rows, the dK waves the dO rows
+  const AttnTensor& src = dkw ? a.dout : a.q;
+  const a_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(src.p), (short)0, (int)src.bytes,
+                                                        0x00020000);
+  const int32_t row_bytes = (int32_t)(src.ss * 2);
+  RowCopy rowc;
+  TrCopy trc;
+  rowc.init(src, b, h, a.hd, w, lane);
+  trc.init(src, b, h, a.hd, w, lane);
+  uint16_t* const rowimg = dkw ? dOs : Qs;
+  uint16_t* const trimg = dkw ? dOn : Qn;
   const int qtr = tr_lane(lane, QN);
   const int first = (kb * kBKV2) / kBQ2, nq = (a.S + kBQ2 - 1) / kBQ2;
-  float stat_n = 0.f;
-  auto load_stats = [&](int qs) __attribute__((always_inline)) {
-    if (rt < kBQ2) {
-      const bool real = !PAD || qs + rt < a.S;  // a padding query gets lse = 1e30, so P = 0
-      const int64_t i = (int64_t)bh * a.S + qs + rt;
-      stat_n = dkw ? (real ? a.delta[i] : 0.f) : (real ? a.lse[i] : 1e30f);
-    }
+  // per-query statistics of a step: lse for the dV waves' P, delta for the
+  // dK waves' dS (a padding query gets lse = 1e30, so P = 0)
+  auto stat = [&](int qs) __attribute__((always_inline)) {
+    const bool real = !PAD || qs + rt < a.S;
+    const int64_t i = (int64_t)bh * a.S + qs + rt;
+    return dkw ? (real ? a.delta[i] : 0.f) : (real ? a.lse[i] : 1e30f);
   };
-  tile.load(first * kBQ2);
-  load_stats(first * kBQ2);
+  float stat_n = 0.f;
+  rowc.template issue<PAD>(rowimg, rs, row_bytes, first * kBQ2, a.S);
+  trc.template issue<PAD>(trimg, rs, row_bytes, first * kBQ2, a.S);
+  if (rt < kBQ2) stat_n = stat(first * kBQ2);
+  vm_wait_all();
+  if (rt < kBQ2) (dkw ? del_s : lse_s)[rt] = stat_n;
+  __syncthreads();
   for (int qb = first; qb < nq; ++qb) {
     const int qs0 = qb * kBQ2;
-    __syncthreads();  // previous step's LDS readers are done
-    if (dkw) {
-      tile.store(dOs);
-      tile.template store_natural<QN>(dOn);
-      if (rt < kBQ2) del_s[rt] = stat_n;
-    } else {
-      tile.store(Qs);
-      tile.template store_natural<QN>(Qn);
-      if (rt < kBQ2) lse_s[rt] = stat_n;
-    }
-    __syncthreads();
-    if (qb + 1 < nq) {
-      tile.load(qs0 + kBQ2);
-      load_stats(qs0 + kBQ2);
-    }
+    const bool more = qb + 1 < nq;
+    // the natural copy of this step (read after the hand-over barrier)
+    if (qb != first) trc.template issue<PAD>(trimg, rs, row_bytes, qs0, a.S);
     // a pair whose keys all follow every query of the step skips the work
     // but not the barriers
     const bool active = qs0 + kBQ2 - 1 >= k0;
     const bool diag = qs0 < k0 + 31;
-    a_f32x16 x[2];  // S, then P (dV wave); dP, then dS (dK wave)
+    a_f32x16 x[2];  // S, then P (dV wave); dP - delta, then dS (dK wave)
     if (active) {
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) x[t][r] = 0.f;
-        const uint16_t* ap = (dkw ? dOs : Qs) + (t * 32 + (lane & 31)) * (D + 8) + hl * 8;
+        const uint16_t* ap = rowimg + (t * 32 + (lane & 31)) * AL + hl * 8;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) x[t] = mma<FP16>(*reinterpret_cast<const uint4*>(ap + ks * 16), kf[ks], x[t]);
         if (!dkw) {
@@ -488,10 +537,20 @@ __global__ void __launch_bounds__(2 * kAttnThreads, 1) attn_bwd_dkdv_pair_kernel
           for (int g = 0; g < 4; ++g)
             Ps[w][t][g][lane] = a_u32x4{__float_as_uint(x[t][4 * g]), __float_as_uint(x[t][4 * g + 1]),
                                         __float_as_uint(x[t][4 * g + 2]), __float_as_uint(x[t][4 * g + 3])};
+        } else {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) x[t][r] = x[t][r] - del_s[t * 32 + swz_row(r, hl)];
         }
       }
     }
-    __syncthreads();  // P handed over
+    vm_wait_all();  // this step's natural copy has landed
+    __syncthreads();  // P handed over; every row-swizzled read of the step done
+    // the next step's row-swizzled copy and statistics, read after the
+    // step's closing barrier
+    if (more) {
+      rowc.template issue<PAD>(rowimg, rs, row_bytes, qs0 + kBQ2, a.S);
+      if (rt < kBQ2) stat_n = stat(qs0 + kBQ2);
+    }
     if (active) {
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
@@ -500,11 +559,7 @@ __global__ void __launch_bounds__(2 * kAttnThreads, 1) attn_bwd_dkdv_pair_kernel
           for (int g = 0; g < 4; ++g) {
             const a_u32x4 pv = Ps[w][t][g][lane];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const int r = 4 * g + e;
-              const float p = __uint_as_float(pv[e]);
-              x[t][r] = p * (x[t][r] - del_s[t * 32 + swz_row(r, hl)]);
-            }
+            for (int e = 0; e < 4; ++e) x[t][4 * g + e] = __uint_as_float(pv[e]) * x[t][4 * g + e];
           }
         }
         // dV += P^T dO (dV wave) or dK += dS^T Q (dK wave) over the tile's
@@ -520,6 +575,9 @@ __global__ void __launch_bounds__(2 * kAttnThreads, 1) attn_bwd_dkdv_pair_kernel
         }
       }
     }
+    vm_wait_all();  // the next step's row-swizzled copy and statistics have landed
+    if (more && rt < kBQ2) (dkw ? del_s : lse_s)[rt] = stat_n;
+    __syncthreads();  // step done: both copies and P free for the next step
   }
   // lane holds d = t*32 + lane%32 for keys k0 + acc_row(r, hl)
 #pragma unroll
@@ -534,6 +592,321 @@ __global__ void __launch_bounds__(2 * kAttnThreads, 1) attn_bwd_dkdv_pair_kernel
       else
         row_ptr(a.dv, kr, b, h)[d] = from_f<FP16>(acc[t][r]);
     }
+}
+
+// ------------------------------ backward: dK, dV paired, head_dim 128 --
+// The pairing above for D = 128, skewed by half a step so that each step
+// has one barrier and both waves of a SIMD mix MFMAs and VALU work: in step
+// m the dV wave computes S(m) and P(m) (handing P to LDS) and then adds
+// P(m)^T dO(m) into dV, while the dK wave first finishes step m-1 -- reads
+// P(m-1), forms dS = P (dP - delta) and adds dS^T Q(m-1) into dK -- and then
+// computes dP(m) - delta.  One wave's exponentials or dS arithmetic then
+// fall between the other wave's MFMAs instead of after them.
+//
+// LDS holds one image per tile of 64 query rows: the 16 chunks of 8 columns
+// of a row, chunk c of row r at position c ^ xsw(r); xsw swaps the two
+// 2-bit fields of r mod 16, so the row reads of the A operands (16 lanes on
+// 16 rows, one chunk) and the transposing reads of the B operands (4 rows x
+// 64 bytes per 32 lanes) both hit distinct banks, and one image serves
+// both.  Step m reads Q(m-1), Q(m) and dO(m), and the rows of step m+1 load
+// directly into idle images a whole step ahead: three Q images, two dO
+// images and two P buffers (145 KB in all).  The arithmetic per element is
+// that of the kernel above, in the same order, so the results are
+// bit-identical.
+__device__ __forceinline__ int xsw(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
+
+template <bool FP16, bool PAD>
+__global__ void __launch_bounds__(2 * kAttnThreads, 1) attn_bwd_dkdv_x128_kernel(AttnArgs a) {
+  constexpr int D = 128, KS = D / 16, DT = D / 32;
+  constexpr int IMG = kBQ2 * D;  // elements of one image
+  __shared__ __attribute__((aligned(16))) uint16_t Qx[3 * IMG];
+  __shared__ __attribute__((aligned(16))) uint16_t dOx[2 * IMG];
+  __shared__ a_u32x4 Ps[2][4][2][4][64];
+  __shared__ __attribute__((aligned(16))) float lse_s[2][kBQ2];
+  __shared__ __attribute__((aligned(16))) float del_s[2][kBQ2];
+
+  const int BH = a.B * a.H;
+  const int bh = blockIdx.x % BH, kb = blockIdx.x / BH;
+  const int b = bh / a.H, h = bh % a.H;
+  const int lane = threadIdx.x & 63, hl = lane >> 5;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+  const int w = wv & 3;
+  const bool dkw = wv >= 4;  // the dK wave of its pair
+  const int rt = threadIdx.x & (kAttnThreads - 1);
+  const int k0 = kb * kBKV2 + w * 32;
+  const int key = k0 + (lane & 31);
+
+  // B operands of the first product: K rows (S = Q K^T) in the dV wave, V
+  // rows (dP = dO V^T) in the dK wave
+  uint4 kf[KS];
+  {
+    const uint16_t* kp = row_ptr(dkw ? a.v : a.k, key, b, h);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) kf[ks] = load_row16<PAD>(kp, key < a.S, ks * 16 + hl * 8, a.hd);
+  }
+  a_f32x16 acc[DT];  // dV in the dV wave, dK in the dK wave
+#pragma unroll
+  for (int t = 0; t < DT; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[t][r] = 0.f;
+
+  // direct loads (the dV waves move Q, the dK waves dO): lane l of piece j
+  // (4 per wave, 16 per image) fills unit (w*4 + j)*64 + l, i.e. image row
+  // u / 16, position u % 16
+  const AttnTensor& src = dkw ? a.dout : a.q;
+  const a_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(src.p), (short)0, (int)src.bytes,
+                                                        0x00020000);
+  const int32_t row_bytes = (int32_t)(src.ss * 2);
+  int32_t doff[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int u = (w * 4 + j) * 64 + lane;
+    const int r = u >> 4, c = (u & 15) ^ xsw(r);
+    doff[j] = c * 8 < a.hd ? (int32_t)(((int64_t)b * src.sb + (int64_t)h * src.sh + (int64_t)r * src.ss + c * 8) * 2)
+                           : kAttnOob;
+  }
+  uint16_t* const ldsimg = dkw ? dOx : Qx;
+  auto issue = [&](int slot, int r0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int32_t o = !PAD || r0 + (w * 4 + j) * 4 + (lane >> 4) < a.S ? doff[j] : kAttnOob;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rs, (__attribute__((address_space(3))) void*)(ldsimg + slot * IMG + (w * 4 + j) * 512), 16, o,
+          r0 * row_bytes, 0, 0);
+    }
+  };
+  // A-operand rows: tile row t*32 + swz(lane%32), chunk 2*ks + hl at
+  // position (2*ks + hl) ^ xsw(row) = 2*(ks ^ (xa >> 1)) + (hl ^ (xa & 1))
+  int aoff[KS];
+  {
+    const int arow = swz(lane & 31), xa = xsw(arow);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) aoff[ks] = arow * D + (((2 * ks + hl) ^ xa) << 3);
+  }
+  // B-operand transposing reads: k-rows kk*16 + 8*(l/32) + (l%16)/4 (+4 for
+  // the second read), columns d2*32 + 16*((l/16)%2) + 4*(l%4)
+  int toff[DT][2];
+  {
+    const int R = (lane & 15) >> 2, L5 = lane >> 5, L4 = (lane >> 4) & 1, L1 = (lane >> 1) & 1;
+#pragma unroll
+    for (int d2 = 0; d2 < DT; ++d2)
+#pragma unroll
+      for (int hi = 0; hi < 2; ++hi) {
+        const int row = 8 * L5 + R + 4 * hi;
+        const int pc = 4 * (d2 ^ R) + ((2 * L4 + L1) ^ (2 * L5 + hi));
+        toff[d2][hi] = row * D + pc * 8 + (lane & 1) * 4;
+      }
+  }
+  auto bfrag = [&](const uint16_t* img, int kk, int d2) __attribute__((always_inline)) {
+    const uint16_t* bp = img + kk * 16 * D;
+    const a_u32x2 lo =
+        __builtin_bit_cast(a_u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((a_lds_s16x4*)(bp + toff[d2][0])));
+    const a_u32x2 hi =
+        __builtin_bit_cast(a_u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((a_lds_s16x4*)(bp + toff[d2][1])));
+    return make_uint4(lo.x, lo.y, hi.x, hi.y);
+  };
+  // acc += X^T B over a step's 64 queries: X (P or dS, one 32-query tile
+  // per t) as the A operand, B from the transposing reads of `img`.  Four
+  // B fragments in flight, each refilled with the next k-step's fragment of
+  // its head-dim tile right after its MFMA issues (order pinned: the
+  // scheduler otherwise hoists every read and runs out of registers)
+  // With `pbuf` (the dK wave), tile t's X is first formed as dS = P (dP -
+  // delta) from P in `pbuf`, one tile at a time.
+  auto second = [&](a_f32x16 (&x)[2], const uint16_t* img, const a_u32x4 (*pbuf)[2][4][64])
+                    __attribute__((always_inline)) {
+    uint4 fb[DT];
+#pragma unroll
+    for (int d2 = 0; d2 < DT; ++d2) fb[d2] = bfrag(img, 0, d2);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      if (pbuf) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const a_u32x4 pv = pbuf[w][t][g][lane];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) x[t][4 * g + e] = __uint_as_float(pv[e]) * x[t][4 * g + e];
+        }
+      }
+#pragma unroll
+      for (int k2 = 0; k2 < 2; ++k2) {
+        const int kk = t * 2 + k2, e0 = k2 * 8;
+        const uint4 pa = make_uint4(pack2<FP16>(x[t][e0 + 0], x[t][e0 + 1]), pack2<FP16>(x[t][e0 + 2], x[t][e0 + 3]),
+                                    pack2<FP16>(x[t][e0 + 4], x[t][e0 + 5]), pack2<FP16>(x[t][e0 + 6], x[t][e0 + 7]));
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int d2 = 0; d2 < DT; ++d2) {
+          acc[d2] = mma<FP16>(pa, fb[d2], acc[d2]);
+          __builtin_amdgcn_sched_barrier(0);
+          if (kk < 3) fb[d2] = bfrag(img, kk + 1, d2);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    }
+  };
+  // x = (rows of img) kf^T over the 64 queries of a step: S (dV wave) or
+  // dP (dK wave), query index of register r of tile t = t*32 + swz_row(r, hl).
+  // A rolling window of four A fragments, pinned like the B fragments
+  // x starts at `x0(t)` (zero, or the per-query -delta of the dK wave)
+  auto first_product = [&](a_f32x16 (&x)[2], const uint16_t* img, auto x0) __attribute__((always_inline)) {
+    auto afrag = [&](int i) __attribute__((always_inline)) {  // fragment i = t*KS + ks
+      return *reinterpret_cast<const uint4*>(img + (i / KS) * 32 * D + aoff[i % KS]);
+    };
+    uint4 fa[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) fa[i] = afrag(i);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const int i = t * KS + ks;
+        x[t] = mma<FP16>(fa[i & 3], kf[ks], ks == 0 ? x0(t) : x[t]);
+        __builtin_amdgcn_sched_barrier(0);
+        if (i + 4 < 2 * KS) fa[i & 3] = afrag(i + 4);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+  };
+
+  const int first = (kb * kBKV2) / kBQ2, nq = (a.S + kBQ2 - 1) / kBQ2, n = nq - first;
+  auto stat = [&](int qs) __attribute__((always_inline)) {
+    const bool real = !PAD || qs + rt < a.S;
+    const int64_t i = (int64_t)bh * a.S + qs + rt;
+    return dkw ? (real ? -a.delta[i] : 0.f) : (real ? a.lse[i] : 1e30f);
+  };
+  float stat_n = 0.f;
+  issue(0, first * kBQ2);
+  if (rt < kBQ2) stat_n = stat(first * kBQ2);
+  vm_wait_all();
+  if (rt < kBQ2) (dkw ? del_s : lse_s)[0][rt] = stat_n;
+  __syncthreads();
+
+  a_f32x16 x[2];  // S then P (dV wave); dP - delta, then dS (dK wave)
+  // step j = m - first (Q image j % 3; dO image, P buffer and statistics
+  // j % 2 = P, a template constant)
+  auto step = [&](int j, int qslot, auto par_c, auto role_c) __attribute__((always_inline)) {
+    constexpr int P = decltype(par_c)::value;
+    constexpr bool DKW = decltype(role_c)::value;  // the role, a constant here
+    const int m = first + j, qs0 = m * kBQ2;
+    const int qnext = qslot == 2 ? 0 : qslot + 1, qprev = qslot == 0 ? 2 : qslot - 1;
+    if (j + 1 < n) {  // the next step's rows into idle images, a step ahead
+      issue(dkw ? P ^ 1 : qnext, qs0 + kBQ2);
+      if (rt < kBQ2) stat_n = stat(qs0 + kBQ2);
+    }
+    // a pair whose keys all follow every query of a step skips its work
+    const bool active = qs0 + kBQ2 - 1 >= k0;
+    const bool active_prev = j > 0 && qs0 - 1 >= k0;
+    // the sub-products are fenced from each other: the scheduler otherwise
+    // hoists every fragment read of the next product above the current
+    // one and runs out of registers
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (!DKW) {
+      if (active) {
+        first_product(x, Qx + qslot * IMG, [](int) { return a_f32x16{}; });
+        __builtin_amdgcn_sched_barrier(0);
+        const bool diag = qs0 < k0 + 31;
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          auto probs = [&](auto masked) __attribute__((always_inline)) {
+            // the causal mask: query qs0 + t*32 + swz_row(r, hl) precedes the
+            // key when kq > t*32 + swz_row(r, 0) (a constant per register)
+            const int kq = key - qs0 - 8 * hl;
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+              // lse of the 4 queries of registers 4g..4g+3 (consecutive)
+              const float4 l4 = *reinterpret_cast<const float4*>(&lse_s[P][t * 32 + swz_row(4 * g, hl)]);
+              const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const int r = 4 * g + e;
+                float p = fast_exp2(__builtin_fmaf(x[t][r], a.scale_log2, -lv[e]));
+                if (decltype(masked)::value && kq > t * 32 + swz_row(r, 0)) p = 0.f;
+                x[t][r] = p;
+              }
+            }
+          };
+          if (diag)
+            probs(std::true_type{});
+          else
+            probs(std::false_type{});
+#pragma unroll
+          for (int g = 0; g < 4; ++g)
+            Ps[P][w][t][g][lane] = a_u32x4{__float_as_uint(x[t][4 * g]), __float_as_uint(x[t][4 * g + 1]),
+                                           __float_as_uint(x[t][4 * g + 2]), __float_as_uint(x[t][4 * g + 3])};
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        second(x, dOx + P * IMG, nullptr);
+      }
+    } else {
+      if (active_prev)  // finish step m-1: dS = P (dP - delta), dK += dS^T Q
+        second(x, Qx + qprev * IMG, Ps[P ^ 1]);
+      __builtin_amdgcn_sched_barrier(0);
+      if (active) {
+        // dP - delta: the accumulator starts at -delta (stored negated)
+        first_product(x, dOx + P * IMG, [&](int t) __attribute__((always_inline)) {
+          a_f32x16 d;
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const float4 d4 = *reinterpret_cast<const float4*>(&del_s[P][t * 32 + swz_row(4 * g, hl)]);
+            d[4 * g + 0] = d4.x;
+            d[4 * g + 1] = d4.y;
+            d[4 * g + 2] = d4.z;
+            d[4 * g + 3] = d4.w;
+          }
+          return d;
+        });
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    vm_wait_all();  // the next step's rows and statistics have landed
+    if (j + 1 < n && rt < kBQ2) (dkw ? del_s : lse_s)[P ^ 1][rt] = stat_n;
+    __syncthreads();  // P(m) handed over; images of step m-1 free
+  };
+  // each role runs its own copy of the step loop (the same barriers in the
+  // same order), so neither keeps the other's values alive
+  auto run = [&](auto role_c) __attribute__((always_inline)) {
+    int j = 0, qslot = 0;
+    for (; j + 1 < n; j += 2) {
+      step(j, qslot, std::integral_constant<int, 0>{}, role_c);
+      qslot = qslot == 2 ? 0 : qslot + 1;
+      step(j + 1, qslot, std::integral_constant<int, 1>{}, role_c);
+      qslot = qslot == 2 ? 0 : qslot + 1;
+    }
+    if (j < n) {
+      step(j, qslot, std::integral_constant<int, 0>{}, role_c);
+      qslot = qslot == 2 ? 0 : qslot + 1;
+    }
+    // the dK waves finish the last step (its P is in buffer (n - 1) % 2)
+    if (decltype(role_c)::value && (nq - 1) * kBQ2 + kBQ2 - 1 >= k0) {
+      const int pb = (n - 1) & 1, qlast = qslot == 0 ? 2 : qslot - 1;
+      second(x, Qx + qlast * IMG, Ps[pb]);
+    }
+  };
+  if (dkw)
+    run(std::true_type{});
+  else
+    run(std::false_type{});
+  // the 32 x 128 tile of each wave (dV or dK, rounded to 16 bits) through
+  // LDS, then out in 16-byte row chunks: lane holds d = t*32 + lane%32 for
+  // keys acc_row(r, hl); the staging rows are padded by 8 elements
+  constexpr int SL = D + 8;
+  __syncthreads();  // every image and P buffer read
+  // 8.5 KB per wave: the dV waves' in the Q images, the dK waves' in the P buffers
+  uint16_t* stage = (dkw ? reinterpret_cast<uint16_t*>(&Ps[0][0][0][0][0]) : Qx) + w * 32 * SL;
+  static_assert(4 * 32 * SL <= 3 * IMG && 4 * 32 * SL * 2 <= (int)sizeof(Ps), "staging fits");
+#pragma unroll
+  for (int t = 0; t < DT; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+      stage[acc_row(r, hl) * SL + t * 32 + (lane & 31)] = from_f<FP16>(dkw ? acc[t][r] * a.scale : acc[t][r]);
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's staging writes are done (the wave reads only its own)
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int c = i * 64 + lane, kr = c >> 4, col = (c & 15) * 8;  // key row, first column of the chunk
+    const int key_g = k0 + kr;
+    if (PAD && (key_g >= a.S || col >= a.hd)) continue;
+    *reinterpret_cast<uint4*>(row_ptr(dkw ? a.dk : a.dv, key_g, b, h) + col) =
+        *reinterpret_cast<const uint4*>(stage + kr * SL + col);
+  }
 }
 
 // ------------------------------------------------------------ backward: dQ --
@@ -787,9 +1160,12 @@ extern "C" int eth_attn_bwd(const eth_attn_desc_t* d, const void* q, const void*
   const int width = a.hd > 96 ? 128 : a.hd > 64 ? 96 : 64;
   static_assert(kBKV2 == kBQ, "one padding rule for the three backward kernels");
   const bool pad = a.S % kBKV2 != 0 || a.hd != width;
-#define ETH_ATTN_BWD_P(D, F, P)                                                  \
-  attn_bwd_dq_kernel<D, F, P><<<g_q, kAttnThreads, 0, s>>>(a);                 \
-  attn_bwd_dkdv_pair_kernel<D, F, P><<<g_kv, 2 * kAttnThreads, 0, s>>>(a);
+#define ETH_ATTN_BWD_P(D, F, P)                                                    \
+  attn_bwd_dq_kernel<D, F, P><<<g_q, kAttnThreads, 0, s>>>(a);                   \
+  if constexpr (D == 128)                                                         \
+    attn_bwd_dkdv_x128_kernel<F, P><<<g_kv, 2 * kAttnThreads, 0, s>>>(a);         \
+  else                                                                            \
+    attn_bwd_dkdv_pair_kernel<D, F, P><<<g_kv, 2 * kAttnThreads, 0, s>>>(a);
 #define ETH_ATTN_BWD(D, F)        \
   if (pad) {                      \
     ETH_ATTN_BWD_P(D, F, true)    \
