@@ -373,6 +373,203 @@ __global__ void __launch_bounds__(kAttnThreads, 2) attn_fwd_kernel(AttnArgs a) {
   if (hl == 0) a.lse[(int64_t)bh * a.S + q] = m + log2f(l);
 }
 
+// -------------------------------------------------- forward, head_dim 128 --
+// attn_fwd_kernel for D = 128 with each 64-key block of K and V in an
+// XOR-swizzled LDS image (chunk c of row r at c ^ xsw(r), see
+// attn_bwd_dkdv_x128_kernel), double buffered and filled by direct
+// global->LDS loads a whole block ahead: no register staging, no copy
+// phase, one barrier per block.  K rows are read as A operands (S^T = K Q^T)
+// and V through transposing reads (O^T = V^T P^T); same arithmetic in the
+// same order as attn_fwd_kernel, so the results are bit-identical.
+__device__ __forceinline__ int xsw(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
+template <bool FP16, bool PAD>
+__global__ void __launch_bounds__(kAttnThreads, 2) attn_fwd_x128_kernel(AttnArgs a) {
+  constexpr int D = 128, KS = D / 16, DT = D / 32;
+  constexpr int IMG = kBKV * D;
+  __shared__ __attribute__((aligned(16))) uint16_t Kx[2 * IMG];
+  __shared__ __attribute__((aligned(16))) uint16_t Vx[2 * IMG];
+
+  const int BH = a.B * a.H, nqb = (a.S + kBQ - 1) / kBQ;
+  const int bh = blockIdx.x % BH, qb = nqb - 1 - blockIdx.x / BH;
+  const int b = bh / a.H, h = bh % a.H;
+  const int lane = threadIdx.x & 63, hl = lane >> 5;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+  const int q0 = qb * kBQ + w * 32;
+  const int q = q0 + (lane & 31);
+  const float sl2 = a.scale_log2;
+
+  // direct loads: each wave fills 4 pieces of the K image and 4 of the V image
+  const a_rsrc_t rsk = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.k.p), (short)0, (int)a.k.bytes,
+                                                         0x00020000);
+  const a_rsrc_t rsv = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.v.p), (short)0, (int)a.v.bytes,
+                                                         0x00020000);
+  int32_t koff[4], voff[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int u = (w * 4 + j) * 64 + lane;
+    const int r = u >> 4, c = (u & 15) ^ xsw(r);
+    koff[j] = c * 8 < a.hd ? (int32_t)(((int64_t)b * a.k.sb + (int64_t)h * a.k.sh + (int64_t)r * a.k.ss + c * 8) * 2)
+                           : kAttnOob;
+    voff[j] = c * 8 < a.hd ? (int32_t)(((int64_t)b * a.v.sb + (int64_t)h * a.v.sh + (int64_t)r * a.v.ss + c * 8) * 2)
+                           : kAttnOob;
+  }
+  const int32_t krow = (int32_t)(a.k.ss * 2), vrow = (int32_t)(a.v.ss * 2);
+  auto issue = [&](int slot, int r0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bool in = !PAD || r0 + (w * 4 + j) * 4 + (lane >> 4) < a.S;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rsk, (__attribute__((address_space(3))) void*)(Kx + slot * IMG + (w * 4 + j) * 512), 16,
+          in ? koff[j] : kAttnOob, r0 * krow, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rsv, (__attribute__((address_space(3))) void*)(Vx + slot * IMG + (w * 4 + j) * 512), 16,
+          in ? voff[j] : kAttnOob, r0 * vrow, 0, 0);
+    }
+  };
+  const int nkv = (qb * kBQ + kBQ) / kBKV;  // blocks up to the diagonal
+  issue(0, 0);
+
+  uint4 qf[KS];
+  {
+    const uint16_t* qp = row_ptr(a.q, q, b, h);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) qf[ks] = load_row16<PAD>(qp, q < a.S, ks * 16 + hl * 8, a.hd);
+  }
+  a_f32x16 o[DT];
+#pragma unroll
+  for (int t = 0; t < DT; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[t][r] = 0.f;
+  float m = -1e30f, l = 0.f;  // running max (log2 units) and sum for query q
+
+  // K rows as A operands: row t*32 + swz(lane%32) (the swizzled key order
+  // that makes S^T's result layout the B operand layout of P^T), chunk
+  // 2*ks + hl
+  int aoff[KS];
+  {
+    const int arow = swz(lane & 31), xa = xsw(arow);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) aoff[ks] = arow * D + (((2 * ks + hl) ^ xa) << 3);
+  }
+  // V^T through transposing reads: k-rows (keys) kk*16 + 8*(l/32) +
+  // (l%16)/4 (+4 for the second read), columns dt*32 + 16*((l/16)%2) + 4*(l%4)
+  int toff[DT][2];
+  {
+    const int R = (lane & 15) >> 2, L5 = lane >> 5, L4 = (lane >> 4) & 1, L1 = (lane >> 1) & 1;
+#pragma unroll
+    for (int d2 = 0; d2 < DT; ++d2)
+#pragma unroll
+      for (int hi = 0; hi < 2; ++hi) {
+        const int row = 8 * L5 + R + 4 * hi;
+        const int pc = 4 * (d2 ^ R) + ((2 * L4 + L1) ^ (2 * L5 + hi));
+        toff[d2][hi] = row * D + pc * 8 + (lane & 1) * 4;
+      }
+  }
+  vm_wait_all();
+  __syncthreads();
+
+  auto block = [&](int j, auto cur_c) __attribute__((always_inline)) {
+    constexpr int cur = decltype(cur_c)::value;
+    const int kv0 = j * kBKV;
+    if (j + 1 < nkv) issue(cur ^ 1, kv0 + kBKV);  // the next block, a block ahead
+    if (kv0 <= q0 + 31) {  // wave has at least one unmasked key in the block
+      const uint16_t* ki = Kx + cur * IMG;
+      const uint16_t* vi = Vx + cur * IMG;
+      a_f32x16 sc[2];
+      // all K fragments of the first 32-key tile are read before its MFMAs,
+      // each register refilled with the second tile's fragment right after
+      // its MFMA issues (order pinned)
+      {
+        uint4 kr[KS];
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) kr[ks] = *reinterpret_cast<const uint4*>(ki + aoff[ks]);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          sc[0] = mma<FP16>(kr[ks], qf[ks], ks == 0 ? a_f32x16{} : sc[0]);
+          __builtin_amdgcn_sched_barrier(0);
+          kr[ks] = *reinterpret_cast<const uint4*>(ki + 32 * D + aoff[ks]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) sc[1] = mma<FP16>(kr[ks], qf[ks], ks == 0 ? a_f32x16{} : sc[1]);
+      }
+      if (kv0 + kBKV - 1 > q0) {  // diagonal block: mask keys after the query
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            if (kv0 + t * 32 + swz_row(r, hl) > q) sc[t][r] = -1e30f;
+      }
+      float mx = sc[0][0];
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[t][r]);
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float mnew = fmaxf(m, mx * sl2);
+      if (__any(mnew > m + kRescaleLog2)) {
+        const float alpha = fast_exp2(m - mnew);
+        l *= alpha;
+#pragma unroll
+        for (int t = 0; t < DT; ++t)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o[t][r] *= alpha;
+        m = mnew;
+      }
+      float rs = 0.f;
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float p = fast_exp2(__builtin_fmaf(sc[t][r], sl2, -m));
+          sc[t][r] = p;
+          rs += p;
+        }
+      l += rs;
+      // O^T += V^T P^T over the 64 keys (4 k-steps of 16)
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const int t = kk >> 1, e0 = (kk & 1) * 8;
+        const uint4 pb = make_uint4(pack2<FP16>(sc[t][e0 + 0], sc[t][e0 + 1]), pack2<FP16>(sc[t][e0 + 2], sc[t][e0 + 3]),
+                                    pack2<FP16>(sc[t][e0 + 4], sc[t][e0 + 5]), pack2<FP16>(sc[t][e0 + 6], sc[t][e0 + 7]));
+        const uint16_t* vp = vi + kk * 16 * D;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          const a_u32x2 lo =
+              __builtin_bit_cast(a_u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((a_lds_s16x4*)(vp + toff[dt][0])));
+          const a_u32x2 hi =
+              __builtin_bit_cast(a_u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((a_lds_s16x4*)(vp + toff[dt][1])));
+          o[dt] = mma<FP16>(make_uint4(lo.x, lo.y, hi.x, hi.y), pb, o[dt]);
+        }
+      }
+    }
+    vm_wait_all();  // the next block's rows have landed
+    __syncthreads();  // this block's images free, the next block's visible
+  };
+  int j = 0;
+  for (; j + 1 < nkv; j += 2) {
+    block(j, std::integral_constant<int, 0>{});
+    block(j + 1, std::integral_constant<int, 1>{});
+  }
+  if (j < nkv) block(j, std::integral_constant<int, 0>{});
+  l += __shfl_xor(l, 32, 64);
+  if (PAD && q >= a.S) return;  // a padding row of the last query block
+  const float inv = 1.0f / l;
+  uint16_t* op = row_ptr(a.out, q, b, h);
+#pragma unroll
+  for (int t = 0; t < DT; ++t)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      if (PAD && t * 32 + g * 8 >= a.hd) continue;
+      uint2 v;
+      v.x = pack2<FP16>(o[t][g * 4 + 0] * inv, o[t][g * 4 + 1] * inv);
+      v.y = pack2<FP16>(o[t][g * 4 + 2] * inv, o[t][g * 4 + 3] * inv);
+      *reinterpret_cast<uint2*>(op + t * 32 + g * 8 + hl * 4) = v;
+    }
+  if (hl == 0) a.lse[(int64_t)bh * a.S + q] = m + log2f(l);
+}
+
 // ------------------------------------------------ backward: dK, dV paired --
 // Eight waves: wave w < 4 (the dV wave) and wave w + 4 (the dK wave) own the
 // same 32 keys and share a SIMD.  Per step of 64 queries the dV wave computes
@@ -613,7 +810,6 @@ __global__ void __launch_bounds__(2 * kAttnThreads, 1) attn_bwd_dkdv_pair_kernel
 // images and two P buffers (145 KB in all).  The arithmetic per element is
 // that of the kernel above, in the same order, so the results are
 // bit-identical.
-__device__ __forceinline__ int xsw(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
 
 template <bool FP16, bool PAD>
 __global__ void __launch_bounds__(2 * kAttnThreads, 1) attn_bwd_dkdv_x128_kernel(AttnArgs a) {
@@ -1112,7 +1308,13 @@ extern "C" int eth_attn_fwd(const eth_attn_desc_t* d, const void* q, const void*
     else attn_fwd_kernel<D, false, false><<<grid, kAttnThreads, 0, s>>>(a);            \
   }
   if (a.hd > 96) {
-    ETH_ATTN_FWD(128)
+    if (pad) {
+      if (fp16) attn_fwd_x128_kernel<true, true><<<grid, kAttnThreads, 0, s>>>(a);
+      else attn_fwd_x128_kernel<false, true><<<grid, kAttnThreads, 0, s>>>(a);
+    } else {
+      if (fp16) attn_fwd_x128_kernel<true, false><<<grid, kAttnThreads, 0, s>>>(a);
+      else attn_fwd_x128_kernel<false, false><<<grid, kAttnThreads, 0, s>>>(a);
+    }
   } else if (a.hd > 64) {
     ETH_ATTN_FWD(96)
   } else {
