@@ -808,8 +808,12 @@ __global__ void __launch_bounds__(2 * kAttnThreads, 1) attn_bwd_dkdv_pair_kernel
 // both.  Step m reads Q(m-1), Q(m) and dO(m), and the rows of step m+1 load
 // directly into idle images a whole step ahead: three Q images, two dO
 // images and two P buffers (145 KB in all).  The arithmetic per element is
-// that of the kernel above, in the same order, so the results are
-// bit-identical.
+// that of the kernel above, in the same order, with one exception: dP's
+// accumulator starts at -delta instead of having delta subtracted after
+// the product.  dV is therefore bit-identical to the kernel above, and dK
+// may differ from it in the last bit of the 16-bit result (about 0.02 % of
+// the elements at the benchmarked shape), the fp32 sum being rounded in
+// another order.
 
 template <bool FP16, bool PAD>
 __global__ void __launch_bounds__(2 * kAttnThreads, 1) attn_bwd_dkdv_x128_kernel(AttnArgs a) {
