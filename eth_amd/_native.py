@@ -90,6 +90,7 @@ SIGNATURES["eth_xent_fwd"] = [_P, _I64, _P, _P, _P, _I64, _I64, _P, _I32, _P]
 SIGNATURES["eth_xent_bwd"] = [_P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _I32, _P]
 SIGNATURES["eth_tied_grad_sum"] = [_P, _P, _I64, _P]
 SIGNATURES["eth_tied_grad_sum_half"] = [_P, _P, _I64, _I32, _P]
+SIGNATURES["eth_synthetic_batch"] = [_P, _I64, _I64, _I64, _P, _P, _P, _P]
 SIGNATURES["eth_attn_fwd"] = [_P, _P, _P, _P, _P, _P, _P]
 SIGNATURES["eth_attn_bwd"] = [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]
 

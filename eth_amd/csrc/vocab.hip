@@ -308,9 +308,54 @@ __global__ void tied_sum_half_kernel(uint16_t* __restrict__ a, uint16_t* __restr
   }
 }
 
+// The deterministic synthetic batch of a step, one thread per (sample,
+// position): tokens = (id * 1103515245 + p * 12345) mod V, loss mask
+// ((id + p) mod 4 != 0), position ids p; int64 products wrap in two's
+// complement and the residues are taken non-negative, as torch.remainder
+// gives them (grad_sync/loss.py:100-119).  The sample ids travel by value.
+constexpr int kBatchIds = 64;
+struct SampleIds {
+  int64_t id[kBatchIds];
+};
+__global__ void __launch_bounds__(256) synthetic_batch_kernel(SampleIds ids, int64_t n, int64_t seq, int64_t vocab,
+                                                              int64_t* __restrict__ tokens,
+                                                              float* __restrict__ loss_mask,
+                                                              int64_t* __restrict__ position_ids) {
+  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (i >= n * seq) return;
+  const int64_t row = i / seq, p = i - row * seq;
+  const int64_t id = ids.id[row];
+  const int64_t t = (int64_t)((uint64_t)id * 1103515245ull + (uint64_t)p * 12345ull);
+  int64_t r = t % vocab;
+  if (r < 0) r += vocab;
+  int64_t m = (int64_t)((uint64_t)id + (uint64_t)p) % 4;
+  if (m < 0) m += 4;
+  tokens[i] = r;
+  loss_mask[i] = m != 0 ? 1.0f : 0.0f;
+  position_ids[i] = p;
+}
+
 }  // namespace eth
 
 using namespace eth;
+
+extern "C" int eth_synthetic_batch(const int64_t* sample_ids, int64_t n_samples, int64_t seq, int64_t vocab,
+                                   int64_t* tokens, float* loss_mask, int64_t* position_ids, void* stream) {
+  ETH_CHECK_ARG(n_samples >= 0 && seq > 0 && vocab > 0, "eth_synthetic_batch: bad sizes");
+  ETH_CHECK_ARG(n_samples == 0 || (sample_ids && tokens && loss_mask && position_ids),
+                "eth_synthetic_batch: null pointer");
+  ETH_CHECK_ARG(seq <= (1LL << 31) / kBatchIds, "eth_synthetic_batch: sequence too long (%lld)", (long long)seq);
+  for (int64_t r0 = 0; r0 < n_samples; r0 += kBatchIds) {
+    const int64_t n = n_samples - r0 < kBatchIds ? n_samples - r0 : kBatchIds;
+    SampleIds ids{};
+    for (int64_t r = 0; r < n; ++r) ids.id[r] = sample_ids[r0 + r];
+    const int64_t elems = n * seq;
+    synthetic_batch_kernel<<<(int)((elems + 255) / 256), 256, 0, (hipStream_t)stream>>>(
+        ids, n, seq, vocab, tokens + r0 * seq, loss_mask + r0 * seq, position_ids + r0 * seq);
+    ETH_CHECK_LAUNCH("eth_synthetic_batch");
+  }
+  return ETH_OK;
+}
 
 extern "C" int eth_tied_grad_sum(float* root, float* copy, int64_t n, void* stream) {
   ETH_CHECK_ARG(n >= 0 && (n == 0 || (root && copy)), "eth_tied_grad_sum: bad arguments");

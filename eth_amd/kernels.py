@@ -7,6 +7,8 @@ the current stream.  There is no CPU fallback: CPU tensors raise.
 
 import ctypes
 
+import numpy as np
+
 import torch
 
 from . import _native as nat
@@ -445,6 +447,23 @@ def xent_bwd(logits2d, labels, lse, dloss):
     nat.call("eth_xent_bwd", nat.ptr(logits2d), logits2d.stride(0), nat.ptr(labels), nat.ptr(lse), nat.ptr(dloss),
              nat.ptr(dz), V, rows, V, code, nat.stream_ptr(logits2d.device))
     return dz
+
+
+def synthetic_batch(sample_ids, seq, vocab, device):
+    """tokens [b, s] int64, loss_mask [b, s] fp32, position_ids [b, s] int64
+    of the deterministic synthetic batch, computed on the device in one
+    launch per 64 samples (the ids cross as a host array)."""
+    ids = np.ascontiguousarray(np.asarray(sample_ids, dtype=np.int64).reshape(-1))
+    b = ids.size
+    if seq <= 0 or vocab <= 0:
+        raise ValueError("sequence length and vocabulary size must be positive")
+    tokens = torch.empty(b, seq, dtype=torch.int64, device=device)
+    mask = torch.empty(b, seq, dtype=torch.float32, device=device)
+    positions = torch.empty(b, seq, dtype=torch.int64, device=device)
+    nat.require_cuda(tokens)
+    nat.call("eth_synthetic_batch", ids.ctypes.data_as(ctypes.c_void_p), b, seq, vocab, nat.ptr(tokens),
+             nat.ptr(mask), nat.ptr(positions), nat.stream_ptr(tokens.device))
+    return tokens, mask, positions
 
 
 def tied_grad_sum(root, copy):

@@ -14,9 +14,11 @@ is formed once, by the gradient sync (eth/runtime/megatron/grad_sync/loss.py):
   microbatch, DP rank) consumes;
 * `synthetic_gpt_batch` (:100-119): the reference's deterministic batch,
   token = (id * 1103515245 + pos * 12345) mod vocab and mask
-  (id + pos) % 4 != 0.
+  (id + pos) % 4 != 0; on the GPU its tokens, mask and position ids come
+  from one kernel (`eth_synthetic_batch`), and the stages skip the boolean
+  attention mask, which the causal attention kernels imply.
 
-All of it is [b, s]-sized or scalar host orchestration; none of it is on the
+All of it is [b, s]-sized or scalar orchestration; none of it is on the
 HBM- or MFMA-bound part of the step.
 """
 
@@ -98,17 +100,29 @@ def local_sample_slots(pipeline_id, microbatch_index, dp_degree, dp_rank, mbs_se
     return tuple(range(start, start + share))
 
 
-def synthetic_gpt_batch(sample_ids, sequence_length, vocab_size, device):
+def synthetic_gpt_batch(sample_ids, sequence_length, vocab_size, device, attention_mask=True):
     """(tokens [b, s] int64, loss_mask [b, s] fp32, position_ids [b, s],
-    attention_mask [b, 1, s, s] bool, True above the diagonal)."""
-    ids = torch.as_tensor(sample_ids, dtype=torch.long, device=device).reshape(-1, 1)
+    attention_mask [b, 1, s, s] bool, True above the diagonal -- or None
+    when `attention_mask` is False).  On a GPU the first three come from the
+    eth_synthetic_batch kernel; on the CPU from torch."""
+    device = torch.device(device)
     pos = torch.arange(sequence_length, dtype=torch.long, device=device).reshape(1, -1)
-    tokens = torch.remainder(ids * _LCG_SAMPLE + pos * _LCG_POSITION, vocab_size)
-    loss_mask = torch.remainder(ids + pos, 4).ne(0).to(torch.float32)
-    position_ids = pos.repeat(ids.shape[0], 1)
+    if device.type == "cuda":
+        from . import kernels
+
+        tokens, loss_mask, position_ids = kernels.synthetic_batch(sample_ids, sequence_length, vocab_size, device)
+        n = tokens.shape[0]
+    else:
+        ids = torch.as_tensor(sample_ids, dtype=torch.long, device=device).reshape(-1, 1)
+        tokens = torch.remainder(ids * _LCG_SAMPLE + pos * _LCG_POSITION, vocab_size)
+        loss_mask = torch.remainder(ids + pos, 4).ne(0).to(torch.float32)
+        position_ids = pos.repeat(ids.shape[0], 1)
+        n = ids.shape[0]
+    if not attention_mask:
+        return tokens, loss_mask, position_ids, None
     future = pos.reshape(-1, 1) < pos  # key position after the query position
-    attention_mask = future.expand(ids.shape[0], 1, sequence_length, sequence_length).clone()
-    return tokens, loss_mask, position_ids, attention_mask
+    mask = future.expand(n, 1, sequence_length, sequence_length).clone()
+    return tokens, loss_mask, position_ids, mask
 
 
 def restore_training_clock(checkpoint_args, iteration):

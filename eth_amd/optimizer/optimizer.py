@@ -364,13 +364,16 @@ class MegatronOptimizer:
                 )
             self._unlaunched_parts = set(range(len(model_parts)))
             self._join_pending = True
+            # the eager parts go out before the per-parameter bookkeeping,
+            # which the GPU would otherwise wait for at the step boundary
+            eager = min(self.eager_update_parts, len(model_parts))
+            for k in range(eager):
+                self.launch_update_part(k)
             for k, (part, ev) in enumerate(zip(model_parts, self.optimizer.part_events)):
-                launch = functools.partial(self.launch_update_part, k)
+                launch = functools.partial(self.launch_update_part, k) if k >= eager else None
                 for p in part:
                     p._eth_ready_event = ev
                     p._eth_update_launch = launch
-            for k in range(min(self.eager_update_parts, len(model_parts))):
-                self.launch_update_part(k)
         if host is not None:
             host[1].synchronize()
         if scaler is not None:

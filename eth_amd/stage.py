@@ -373,8 +373,10 @@ class FirstLastStageTrainer:
         """One microbatch: forward, loss contract, backward of
         numerator / nominal times the loss scale (schedules.py:97-104,214-217).
         Returns (per-token loss [b, s], LossOutput)."""
+        # the causal attention kernels imply the boolean attention mask
         tokens, mask, positions, _ = synthetic_gpt_batch(sample_ids, self.cfg.seq_length, self.unpadded_vocab,
-                                                         self.embedding.word_embeddings.weight.device)
+                                                         self.embedding.word_embeddings.weight.device,
+                                                         attention_mask=False)
         extra = {} if labels is None else {"labels": labels}
         out = self.model({"enc_input_ids": tokens, "enc_position_ids": positions}, extra)
         losses = out["output"]

@@ -402,6 +402,18 @@ int eth_tied_grad_sum(float* root, float* copy, int64_t n, void* stream);
  * fp32 and rounded once, as an all-reduce sum in that dtype rounds it. */
 int eth_tied_grad_sum_half(void* root, void* copy, int64_t n, int dtype, void* stream);
 
+/* The deterministic synthetic batch of `n_samples` samples (`sample_ids`: a
+ * HOST array) of `seq` positions, row-major [n_samples, seq] on the device:
+ * tokens = (id * 1103515245 + p * 12345) mod vocab (int64, wrapping products,
+ * non-negative residues), loss_mask = ((id + p) mod 4 != 0) as fp32 1 / 0,
+ * position_ids = p.  One launch per 64 samples, the ids passed by value.
+ * Replaces the token / loss-mask / position-id tensors of
+ * synthetic_gpt_batch (eth/runtime/megatron/grad_sync/loss.py:100-119); the
+ * boolean attention mask it also returns is not built here (the causal
+ * attention kernels imply it). */
+int eth_synthetic_batch(const int64_t* sample_ids, int64_t n_samples, int64_t seq, int64_t vocab,
+                        int64_t* tokens, float* loss_mask, int64_t* position_ids, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

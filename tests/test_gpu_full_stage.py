@@ -119,6 +119,45 @@ def test_embedding_backward_beyond_one_sort_chunk(cuda, b, s):
     assert torch.equal(dp.cpu(), torch.from_numpy(ref_p))
 
 
+def _lcg_batch_exact(ids, seq, vocab):
+    """The synthetic batch by Python integers: the int64 products wrap in
+    two's complement, the residues are floor-mod (non-negative)."""
+    def wrap(x):
+        x &= (1 << 64) - 1
+        return x - (1 << 64) if x >= 1 << 63 else x
+
+    tokens = [[wrap(i * 1103515245 + p * 12345) % vocab for p in range(seq)] for i in ids]
+    mask = [[1.0 if wrap(i + p) % 4 else 0.0 for p in range(seq)] for i in ids]
+    return tokens, mask
+
+
+def test_synthetic_batch_kernel_matches_the_host_batch(cuda):
+    """eth_synthetic_batch: the reference's known answers, the torch path on
+    the CPU (ragged sequence, more than one 64-sample launch), and products
+    past 2^63 against exact integer arithmetic."""
+    from tests.helpers import known_answers
+
+    announce("synthetic batch kernel")
+    for case in known_answers()["synthetic_gpt_batch"]["cases"]:
+        tokens, mask, positions, attn = synthetic_gpt_batch(case["ids"], case["seq"], case["vocab"], "cuda")
+        assert tokens.tolist() == case["tokens"]
+        assert mask.tolist() == case["mask"]
+        assert positions.tolist() == [list(range(case["seq"]))] * len(case["ids"])
+        assert attn.shape == (len(case["ids"]), 1, case["seq"], case["seq"]) and attn.is_cuda
+    ids = list(range(5, 5 + 3 * 67, 3))  # 67 samples: two launches
+    for seq, vocab in ((7, 50257), (2048, 50304), (33, 4)):
+        g = synthetic_gpt_batch(ids, seq, vocab, "cuda", attention_mask=False)
+        c = synthetic_gpt_batch(ids, seq, vocab, "cpu", attention_mask=False)
+        assert g[3] is None and c[3] is None
+        for a, b in zip(g[:3], c[:3]):
+            assert a.dtype == b.dtype and torch.equal(a.cpu(), b)
+    big = [0, 1, 2**40 + 7, 2**62 - 1, 9_000_000_000_000_000_000]
+    tokens, mask, _, _ = synthetic_gpt_batch(big, 19, 50257, "cuda", attention_mask=False)
+    ref_t, ref_m = _lcg_batch_exact(big, 19, 50257)
+    assert tokens.tolist() == ref_t
+    assert mask.tolist() == ref_m
+
+
 def test_cross_entropy_backward_beyond_one_launch(cuda):
     """70,000 rows (past the 65,535 rows of one launch's grid) against the
     fp64 oracle's gradient, every row including the last launch's."""

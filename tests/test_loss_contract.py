@@ -105,3 +105,6 @@ def test_synthetic_batch_hand_computed_values():
         assert attn.shape == (b, 1, s, s) and attn.dtype == torch.bool
         for i in range(s):
             assert attn[0, 0, i].tolist() == [j > i for j in range(s)]
+        # the stages ask for no attention mask (the causal kernels imply it)
+        t2, m2, p2, none = L.synthetic_gpt_batch(case["ids"], case["seq"], case["vocab"], "cpu", attention_mask=False)
+        assert none is None and torch.equal(t2, tokens) and torch.equal(m2, mask) and torch.equal(p2, positions)
