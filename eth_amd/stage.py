@@ -15,6 +15,7 @@ unpack bound to the optimizer.
 """
 
 import dataclasses
+import functools
 import math
 
 import torch
@@ -72,6 +73,16 @@ def save_stage_snapshot(trainer, output_dir, phase, iteration, metrics=None, clo
         metrics=metrics,
         run_metadata=run_metadata,
     )
+
+
+def _weight_to_host(weight):
+    """Queue a copy of a loss weight (device scalar) into pinned host memory
+    on the current stream; returns (host tensor [1], event after the copy)."""
+    host = torch.empty(1, dtype=weight.dtype, pin_memory=True)
+    host.copy_(weight.detach().reshape(1), non_blocking=True)
+    ev = torch.cuda.Event()
+    ev.record(torch.cuda.current_stream(weight.device))
+    return host, ev
 
 
 def _fp32_main_grads(cfg, requested):
@@ -368,6 +379,7 @@ class FirstLastStageTrainer:
             # under the whole forward
             self.optimizer.overlap_with_next_forward(update_parts(ops))
         self.nominal = float(cfg.micro_batch_size * cfg.seq_length)
+        self._host_weights = []
 
     def forward_backward(self, sample_ids, labels=None, nominal=None):
         """One microbatch: forward, loss contract, backward of
@@ -381,20 +393,32 @@ class FirstLastStageTrainer:
         out = self.model({"enc_input_ids": tokens, "enc_position_ids": positions}, extra)
         losses = out["output"]
         lo = gpt_loss_output(losses, mask, self.nominal if nominal is None else nominal)
+        self._host_weights.append(_weight_to_host(lo.local_loss_weight))
         output_tensor = lo.local_loss_sum / lo.nominal_global_loss_scale
         with overlapped_wgrad():
             torch.autograd.backward(self.optimizer.scale_loss(output_tensor))
         return losses.detach(), lo
+
+    def _host_weight(self):
+        """The step's summed loss weight as a host tensor, from the pinned
+        copies queued right after each forward's loss: reading it waits for
+        those forwards only, not for the backward queued behind them, so the
+        sync's launches follow the backward without the GPU idling."""
+        weights, self._host_weights = self._host_weights, []
+        for _, ev in weights:
+            ev.synchronize()
+        return functools.reduce(lambda a, b: a + b, [w[0] for w, _ in weights])
 
     def tie_gradients(self):
         K.tied_grad_sum(self.embedding.word_embeddings.weight.main_grad, self.post.word_embeddings.weight.main_grad)
 
     def train_step(self, sample_ids, labels=None):
         self.ddp.zero_grad_buffer(defer=True)
+        self._host_weights = []
         losses, lo = self.forward_backward(sample_ids, labels)
         self.optimizer.join_overlapped_update()
         self.ddp.settle_grad_buffer()
-        self.grad_sync.execute(global_normalization_scale(self.nominal, lo.local_loss_weight))
+        self.grad_sync.execute(global_normalization_scale(self.nominal, self._host_weight()))
         self.tie_gradients()
         ok, norm, zeros = self.optimizer.step()
         return losses, lo, ok, norm
@@ -409,6 +433,7 @@ class FirstLastStageTrainer:
         summed LossOutput pair, update_successful, grad_norm)."""
         nominal = float(len(sample_id_batches) * self.cfg.micro_batch_size * self.cfg.seq_length)
         self.ddp.zero_grad_buffer(defer=True)
+        self._host_weights = []
         losses, outs = [], []
         for i, ids in enumerate(sample_id_batches):
             lab = None if labels is None else labels[i]
@@ -418,7 +443,7 @@ class FirstLastStageTrainer:
         self.optimizer.join_overlapped_update()
         self.ddp.settle_grad_buffer()
         numerator, weight = sum_loss_outputs(outs)
-        self.grad_sync.execute(global_normalization_scale(nominal, weight))
+        self.grad_sync.execute(global_normalization_scale(nominal, self._host_weight()))
         self.tie_gradients()
         ok, norm, _zeros = self.optimizer.step()
         return losses, (numerator, weight), ok, norm
