@@ -61,6 +61,17 @@ class FusedAdamW(torch.optim.Optimizer):
             st["exp_avg_sq"] = self._exp_avg_sq_flat[off : off + p.numel()].view_as(p)
             off += n
 
+    def remove_param(self, param):
+        """Stop updating `param`: it leaves its group, its state, its model
+        copy and the partition (its moment views stay allocated, unused)."""
+        for g in self.param_groups:
+            g["params"] = [q for q in g["params"] if q is not param]
+        self.state.pop(param, None)
+        self._model_copies.pop(param, None)
+        if self._partition:
+            self._partition = [[q for q in part if q is not param] for part in self._partition]
+        self._table_key = None
+
     def set_partition(self, parts):
         """Split every step into one launch per part (a list of parameter
         lists, in launch order; parameters in no part form a last part),

@@ -64,6 +64,7 @@ class MegatronOptimizer:
         # and starts the next forward
         self.eager_update_parts = 3
         self._post_sync = (None, 0)  # chunk table of norm-owned gradients summed after the sync
+        self._shared_copies = []  # model parameters updated through another's optimizer parameter
 
     # ----------------------------------------------------------- plumbing --
     @property
@@ -116,8 +117,16 @@ class MegatronOptimizer:
         by op, so the update of later layers overlaps the forward of earlier
         ones; every result is the same as with the update in line."""
         dev = self._device()
-        parts = [[self.optimizer_parameter_for_model_parameter(p) for p in part] for part in model_param_parts]
-        placed = {id(p) for part in parts for p in part}
+        # an optimizer parameter that serves several model parameters (a
+        # shared tied copy) updates in the first part that holds one of them
+        parts, placed = [], set()
+        for part in model_param_parts:
+            parts.append([])
+            for p in part:
+                o = self.optimizer_parameter_for_model_parameter(p)
+                if id(o) not in placed:
+                    placed.add(id(o))
+                    parts[-1].append(o)
         missing = [p for g in self.optimizer.param_groups for p in g["params"] if id(p) not in placed]
         if missing:
             # the deferred launches only cover the given parts: a parameter in
@@ -155,6 +164,42 @@ class MegatronOptimizer:
                 if ev is not None:
                     stream.wait_event(ev)
                     p._eth_ready_event = None
+
+    def share_tied_copy(self, root, copy):
+        """Make the tied copy `copy` of model parameter `root` (the LM head's
+        word embedding beside the embedding's, on one GPU) share the root's
+        storage: its weight becomes a view of the root's, and the root's fp32
+        master and AdamW moments serve both, so one update writes both.  The
+        reference keeps two parameters whose gradients it sums and updates
+        alike (training.py:489-531); from equal starting values, equal
+        gradients and equal hyper-parameters the two updates are identical,
+        so the shared one gives the same bits.  The copy keeps its own main
+        grad, which the sync and the tied gradient sum treat as before."""
+        if self._overlap is not None or self._executor is not None:
+            raise ValueError("share the tied copy before binding the sync or overlapping the update")
+        r = self.optimizer_parameter_for_model_parameter(root)
+        c = self.optimizer_parameter_for_model_parameter(copy)
+        if r is c:
+            return
+        if root.shape != copy.shape or root.dtype != copy.dtype:
+            raise ValueError("tied copies must have one shape and dtype")
+        hyper = [{k: v for k, v in g.items() if k != "params"} for q in (r, c)
+                 for g in self.optimizer.param_groups if any(x is q for x in g["params"])]
+        if len(hyper) != 2 or hyper[0] != hyper[1]:
+            raise ValueError("tied copies must be in parameter groups with equal hyper-parameters")
+        st_r, st_c = self.optimizer.state.get(r, {}), self.optimizer.state.get(c, {})
+        if float(st_r.get("step", 0)) != float(st_c.get("step", 0)) or not torch.equal(root, copy):
+            raise ValueError("tied copies must have equal values and step counts to share storage")
+        with torch.no_grad():
+            copy.data = root.data
+        self.optimizer.remove_param(c)
+        self._drop_model_parameter(copy)
+        self._model_to_optimizer_param[id(copy)] = r
+        self._shared_copies.append(copy)
+
+    def _drop_model_parameter(self, param):
+        """Forget the bookkeeping that pairs `param` with an optimizer
+        parameter of its own (subclasses that keep masters)."""
 
     def bind_gradient_sync(self, executor, resynced=()):
         """Fuse unscale / inf-nan flag / L2 partials into `executor`'s unpack.
@@ -232,8 +277,14 @@ class MegatronOptimizer:
         without `stats`."""
         widen = self._widen_sources()
         params = [p for p in self.get_parameters() if p.grad is not None]
+        # the fp32 main grads of shared tied copies are nobody's optimizer
+        # gradient, but the reference unscales them in place like every main
+        # grad (and checks them): they join the pass outside the norm
+        extra = [c.main_grad for c in self._shared_copies
+                 if self.params_have_main_grad and getattr(c, "main_grad", None) is not None
+                 and c.main_grad.dtype == torch.float32]
         key = tuple((p.grad.data_ptr(), p.grad.numel(), widen[id(p)].data_ptr() if id(p) in widen else 0)
-                    for p in params)
+                    for p in params) + tuple((g.data_ptr(), g.numel(), -1) for g in extra)
         if key != self._stats_key:
             wide, plain, code = [], [], None
             base = self._widen_target().data_ptr() if widen else 0
@@ -253,6 +304,10 @@ class MegatronOptimizer:
                 code = nat.dtype_code(src.dtype)
                 dst = (g.data_ptr() - base) // 4
                 split_block(src.data_ptr(), 2, 1, src.numel(), src.numel(), dst, 1.0, flags, wide)
+            for g in extra:
+                if not g.is_contiguous():
+                    raise ValueError("main grads must be contiguous")
+                split_block(g.data_ptr(), 4, 1, g.numel(), g.numel(), 0, 1.0, 0, plain)
             self._stats_tables = tuple(
                 (nat.table_to_device(chunk_table(e), self._device()) if e else None, len(e)) for e in (wide, plain))
             self._widen_code = code
@@ -533,6 +588,13 @@ class Float16OptimizerWithFloat16Params(MegatronOptimizer):
 
     def _norm_owned(self, param):
         return super()._norm_owned(param)
+
+    def _drop_model_parameter(self, param):
+        for mg, fg in zip(self.float16_groups, self.fp32_from_float16_groups):
+            for k, p in enumerate(mg):
+                if p is param:
+                    del mg[k], fg[k]
+                    return
 
     def reload_model_params(self):
         for mg, fg in zip(self.float16_groups, self.fp32_from_float16_groups):

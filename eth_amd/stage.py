@@ -343,7 +343,7 @@ class FirstLastStageTrainer:
     def __init__(self, cfg: GPTConfig, lr=1e-4, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01, clip_grad=1.0,
                  sync_mode="block", bucket_cap_bytes=1024 * 1024, initial_loss_scale=2.0**16, unpadded_vocab=50257,
                  recompute_ops=None, runtime_evidence_dir=None, accumulate_allreduce_grads_in_fp32=True,
-                 overlap_optimizer=False):
+                 overlap_optimizer=False, share_tied_storage=True):
         self.cfg = cfg
         self.unpadded_vocab = unpadded_vocab
         n_ops = 10 * cfg.num_layers + 3
@@ -364,6 +364,11 @@ class FirstLastStageTrainer:
             bf16=cfg.params_dtype == torch.bfloat16, fp16=cfg.params_dtype == torch.float16,
             initial_loss_scale=initial_loss_scale,
         )
+        if share_tied_storage:
+            # both tied copies live on this GPU: one weight, one master, one
+            # set of moments, updated once for both (bit-identical to two
+            # updates of equal inputs); the main grads stay separate
+            self.optimizer.share_tied_copy(self.embedding.word_embeddings.weight, self.post.word_embeddings.weight)
         if self.ddp.accumulate_allreduce_grads_in_fp32 and math.frexp(initial_loss_scale)[0] == 0.5:
             # unscale and inf/nan flag fused into the sync's unpack; the tied
             # word embedding, summed after the sync, gets its norm share and

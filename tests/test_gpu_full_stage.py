@@ -387,6 +387,52 @@ def test_first_last_update_overlapped_with_the_next_forward_is_bit_identical(cud
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("mode", ["fused", "standalone", "overlapped"])
+def test_shared_tied_storage_is_bit_identical_to_two_copies(cuda, dtype, mode):
+    """The tied head copy sharing the root's weight, master and moments (one
+    update for both) against two separately updated copies, as the
+    reference keeps them: three steps give the same losses and norms, and
+    every parameter, main grad, master and moment is bit-identical -- with
+    the statistics fused into the sync, in one standalone pass (which also
+    unscales the copy's main grad in place), and with the update overlapped
+    with the next forward."""
+    announce(f"shared tied storage {dtype} {mode}")
+    cfg = GPTConfig(hidden_size=256, num_attention_heads=4, ffn_hidden_size=1024, num_layers=2, seq_length=128,
+                    micro_batch_size=2, padded_vocab_size=50304, params_dtype=dtype, device="cuda", seed=17)
+    kw = dict(lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01, clip_grad=0.05, initial_loss_scale=1024.0,
+              overlap_optimizer=mode == "overlapped")
+    two = FirstLastStageTrainer(cfg, share_tied_storage=False, **kw)
+    one = FirstLastStageTrainer(cfg, **kw)
+    root, copy = one.embedding.word_embeddings.weight, one.post.word_embeddings.weight
+    assert copy.data_ptr() == root.data_ptr() and copy.main_grad.data_ptr() != root.main_grad.data_ptr()
+    assert one.optimizer.optimizer_parameter_for_model_parameter(copy) is \
+        one.optimizer.optimizer_parameter_for_model_parameter(root)
+    if mode == "standalone":
+        one.optimizer.unbind_gradient_sync()
+        two.optimizer.unbind_gradient_sync()
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    for step in range(3):
+        labels = torch.randint(0, 50257, (2, 128), generator=gen, device="cuda")
+        l2, _, ok2, n2 = two.train_step([3 + step, 8 + step], labels)
+        l1, _, ok1, n1 = one.train_step([3 + step, 8 + step], labels)
+        assert ok1 and ok2 and n1 == n2, (step, n1, n2)
+        assert torch.equal(l1, l2), step
+    one.optimizer.join_overlapped_update()
+    two.optimizer.join_overlapped_update()
+    torch.cuda.synchronize()
+    for (name, p1), (_, p2) in zip(one.model.named_parameters(), two.model.named_parameters()):
+        assert torch.equal(p1, p2), name
+        assert torch.equal(p1.main_grad, p2.main_grad), name
+        m1 = one.optimizer.optimizer_parameter_for_model_parameter(p1)
+        m2 = two.optimizer.optimizer_parameter_for_model_parameter(p2)
+        assert torch.equal(m1, m2), name
+        s1, s2 = one.optimizer.state_for_model_parameter(p1), two.optimizer.state_for_model_parameter(p2)
+        for k in ("exp_avg", "exp_avg_sq"):
+            assert torch.equal(s1[k], s2[k]), (name, k)
+        assert float(s1["step"]) == float(s2["step"]) == 3.0, name
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_first_last_fused_statistics_match_the_standalone_pass(cuda, dtype):
     """The first+last stage unscales in the sync's unpack and takes the tied
     root's norm share after the tied sum: the step's norm, outcome and
