@@ -66,6 +66,7 @@ SIGNATURES = {
     "eth_bucket_unpack": [_P, _I64, _P, _I32, _F32, _F32, _I32, _P, _P, _I64, _P],
     "eth_bucket_sync_local": [_P, _I64, _F32, _F32, _I32, _P, _P, _P, _I64, _P],
     "eth_grad_stats": [_P, _I64, _F32, _I32, _P, _P, _I64, _P],
+    "eth_tied_grad_sum_stats": [_P, _I64, _P, _P, _F32, _P, _P, _I64, _P],
     "eth_widen_grad_stats": [_P, _I64, _P, _I32, _F32, _I32, _P, _P, _I64, _P],
     "eth_grad_norm_finalize": [_P, _I64, _F64, _P, _P],
     "eth_adam_step": [_P, _P, _I64, _F64, _F64, _F64, _I64, _I32, _P, _P, _P],

@@ -239,26 +239,48 @@ __global__ void __launch_bounds__(kThreads) staged_step_kernel(const eth_chunk_t
 }
 
 // ------------------------------------------------- standalone statistics ---
+// TIED: the chunk's gradient g is first replaced by g + g[copy_off] -- the
+// tied word-embedding sum, stored into both the root (g) and the copy --
+// and the statistics are taken of that sum, element for element as the
+// plain form takes them of a gradient holding it.
+template <bool TIED>
 __global__ void __launch_bounds__(kThreads) stats_kernel(const eth_chunk_t* __restrict__ chunks,
                                                          float inv, int flags,
                                                          float* __restrict__ found_inf,
                                                          double* __restrict__ partials,
-                                                         int64_t partial_base) {
+                                                         int64_t partial_base, int64_t copy_off) {
+  // every product and sum rounded on its own, so both forms of the kernel
+  // form the same partials from the same values
+#pragma clang fp contract(off)
   __shared__ float red[kThreads / 64];
   const eth_chunk_t c = chunks[blockIdx.x];
   float* g = reinterpret_cast<float*>(c.src);
   const int64_t n = (int64_t)c.rows * c.row_len;
-  const bool unscale = flags & ETH_UNPACK_UNSCALE;
+  const bool unscale = !TIED && (flags & ETH_UNPACK_UNSCALE);
   // the scaled-overflow check multiplies by the loss scale (passed in `inv`)
   // without storing; with unscaling it is meaningless and ignored
   const float chk = (!unscale && (flags & ETH_STATS_SCALED_OVERFLOW)) ? inv : 1.0f;
   float sq = 0.f;
   bool bad = false;
   if (c.rows == 1 && aligned16(g)) {
+    // the walk over the gradient is the same in both forms; a copy that is
+    // not 16-byte aligned is read and written element by element
+    const bool cvec = !TIED || aligned16(g + copy_off);
     const int64_t nv = n / 4;
     float4* gv = reinterpret_cast<float4*>(g);
     for (int64_t i = threadIdx.x; i < nv; i += kThreads) {
       float4 x = gv[i];
+      if (TIED) {
+        float* cp = g + copy_off + 4 * i;
+        const float4 y = cvec ? *reinterpret_cast<const float4*>(cp) : make_float4(cp[0], cp[1], cp[2], cp[3]);
+        x.x = x.x + y.x; x.y = x.y + y.y; x.z = x.z + y.z; x.w = x.w + y.w;
+        gv[i] = x;
+        if (cvec) {
+          *reinterpret_cast<float4*>(cp) = x;
+        } else {
+          cp[0] = x.x; cp[1] = x.y; cp[2] = x.z; cp[3] = x.w;
+        }
+      }
       bad |= !isfinite(x.x * chk) | !isfinite(x.y * chk) | !isfinite(x.z * chk) | !isfinite(x.w * chk);
       if (unscale) {
         x.x *= inv; x.y *= inv; x.z *= inv; x.w *= inv;
@@ -268,6 +290,7 @@ __global__ void __launch_bounds__(kThreads) stats_kernel(const eth_chunk_t* __re
     }
     for (int64_t i = nv * 4 + threadIdx.x; i < n; i += kThreads) {
       float x = g[i];
+      if (TIED) g[i] = g[i + copy_off] = x = x + g[i + copy_off];
       bad |= !isfinite(x * chk);
       if (unscale) g[i] = x = x * inv;
       sq += x * x;
@@ -277,6 +300,7 @@ __global__ void __launch_bounds__(kThreads) stats_kernel(const eth_chunk_t* __re
       const int64_t r = i / c.row_len, col = i - r * c.row_len;
       float* e = g + r * c.src_stride + col;
       float x = *e;
+      if (TIED) *e = e[copy_off] = x = x + e[copy_off];
       bad |= !isfinite(x * chk);
       if (unscale) *e = x = x * inv;
       sq += x * x;
@@ -588,9 +612,25 @@ int eth_grad_stats(const eth_chunk_t* chunks, int64_t n_chunks, float inv_loss_s
   ETH_CHECK_ARG(found_inf && partials && partial_base >= 0, "eth_grad_stats: null buffers");
   if (n_chunks == 0) return ETH_OK;
   ETH_CHECK_ARG(chunks, "eth_grad_stats: null chunk table");
-  stats_kernel<<<(int)n_chunks, kThreads, 0, (hipStream_t)stream>>>(
-      chunks, inv_loss_scale, flags, found_inf, partials, partial_base);
+  stats_kernel<false><<<(int)n_chunks, kThreads, 0, (hipStream_t)stream>>>(
+      chunks, inv_loss_scale, flags, found_inf, partials, partial_base, 0);
   ETH_CHECK_LAUNCH("eth_grad_stats");
+  return ETH_OK;
+}
+
+int eth_tied_grad_sum_stats(const eth_chunk_t* chunks, int64_t n_chunks, float* root, float* copy,
+                            float loss_scale, float* found_inf, double* partials, int64_t partial_base,
+                            void* stream) {
+  ETH_CHECK_ARG(n_chunks >= 0 && n_chunks < (1LL << 31), "eth_tied_grad_sum_stats: bad chunk count");
+  ETH_CHECK_ARG(found_inf && partials && partial_base >= 0, "eth_tied_grad_sum_stats: null buffers");
+  if (n_chunks == 0) return ETH_OK;
+  ETH_CHECK_ARG(chunks && root && copy, "eth_tied_grad_sum_stats: null pointer");
+  ETH_CHECK_ARG(((uintptr_t)copy - (uintptr_t)root) % sizeof(float) == 0,
+                "eth_tied_grad_sum_stats: root and copy must be fp32-aligned alike");
+  const int64_t off = ((intptr_t)copy - (intptr_t)root) / (int64_t)sizeof(float);
+  stats_kernel<true><<<(int)n_chunks, kThreads, 0, (hipStream_t)stream>>>(
+      chunks, loss_scale, ETH_STATS_SCALED_OVERFLOW, found_inf, partials, partial_base, off);
+  ETH_CHECK_LAUNCH("eth_tied_grad_sum_stats");
   return ETH_OK;
 }
 

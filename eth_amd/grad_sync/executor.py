@@ -120,10 +120,12 @@ class GradientStatistics:
         # called before the buffers are rewritten: an update still reading
         # the previous step's values is issued and waited for first
         self.before_reuse = None
+        self.generation = 0  # counts resets: statistics taken after one belong to that pass
 
     def reset(self):
         if self.before_reuse is not None:
             self.before_reuse()
+        self.generation += 1
         nat.call("eth_fill_f32", nat.ptr(self.found_inf), 1, 0.0, nat.stream_ptr(self.device))
 
     def finalize(self, max_norm):

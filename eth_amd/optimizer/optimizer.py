@@ -65,6 +65,8 @@ class MegatronOptimizer:
         self.eager_update_parts = 3
         self._post_sync = (None, 0)  # chunk table of norm-owned gradients summed after the sync
         self._shared_copies = []  # model parameters updated through another's optimizer parameter
+        self._post_sync_params = []  # model parameters whose gradients the post-sync table covers
+        self._post_sync_done = None  # statistics generation whose post-sync pass the tied sum already made
 
     # ----------------------------------------------------------- plumbing --
     @property
@@ -197,6 +199,30 @@ class MegatronOptimizer:
         self._model_to_optimizer_param[id(copy)] = r
         self._shared_copies.append(copy)
 
+    def sum_tied_gradients(self, root, copy):
+        """root.main_grad = copy.main_grad = their sum: the same-rank branch of
+        synchronize_shared_weights_grads (training.py:489-531).  When the
+        sync's statistics are bound and the post-sync table covers the root
+        alone, the sum and the root's post-sync statistics (its norm share
+        and the check of its loss-scaled values) are one pass
+        (eth_tied_grad_sum_stats) and the step skips its own pass; the bits
+        are those of the sum followed by that pass."""
+        from .. import kernels as K
+
+        rg, cg = root.main_grad, copy.main_grad
+        table, n = self._post_sync
+        st = self._statistics
+        if (n and st is not None and st.fresh and len(self._post_sync_params) == 1
+                and self._post_sync_params[0] is root and rg.dtype == cg.dtype == torch.float32
+                and rg.shape == cg.shape and rg.is_contiguous() and cg.is_contiguous()):
+            scale = self.grad_scaler.host_scale if self.grad_scaler is not None else 1.0
+            nat.call("eth_tied_grad_sum_stats", nat.ptr(table), n, nat.ptr(rg), nat.ptr(cg), float(scale),
+                     nat.ptr(st.found_inf), nat.ptr(st.partials), self._executor.n_partials,
+                     nat.stream_ptr(self._device()))
+            self._post_sync_done = st.generation
+            return
+        K.tied_grad_sum(rg, cg)
+
     def _drop_model_parameter(self, param):
         """Forget the bookkeeping that pairs `param` with an optimizer
         parameter of its own (subclasses that keep masters)."""
@@ -227,6 +253,7 @@ class MegatronOptimizer:
             split_block(g.data_ptr(), 4, 1, g.numel(), g.numel(), 0, 1.0, nat.CHUNK_NORM, entries)
         table = chunk_table(entries)
         self._post_sync = (nat.table_to_device(table, self._device()) if len(table) else None, len(table))
+        self._post_sync_params = list(post)
         self._executor = executor
         self._statistics = GradientStatistics(executor.n_partials + len(table), self._device())
         self._statistics.before_reuse = self.join_overlapped_update
@@ -242,6 +269,8 @@ class MegatronOptimizer:
         self._executor = None
         self._statistics = None
         self._post_sync = (None, 0)
+        self._post_sync_params = []
+        self._post_sync_done = None
 
     @property
     def grads_unscaled_by_sync(self):
@@ -363,7 +392,8 @@ class MegatronOptimizer:
         if fused:
             st.n_partials_used = self._executor.n_partials
             table, n = self._post_sync
-            if n:
+            done, self._post_sync_done = self._post_sync_done == st.generation, None
+            if n and not done:
                 # statistics of the gradients changed after the sync (already
                 # unscaled by the unpack): sum of squares into the slots after
                 # the executor's; found_inf where a sum, loss-scaled again,
@@ -373,7 +403,7 @@ class MegatronOptimizer:
                 nat.call("eth_grad_stats", nat.ptr(table), n, float(scale), nat.STATS_SCALED_OVERFLOW,
                          nat.ptr(st.found_inf), nat.ptr(st.partials), st.n_partials_used,
                          nat.stream_ptr(self._device()))
-                st.n_partials_used += n
+            st.n_partials_used += n  # slots the pass above, or the fused tied sum, wrote
         elif scaler is not None or need_norm:
             st = self._standalone_statistics(unscale=scaler is not None)
         elif self._widen_sources():

@@ -20,7 +20,6 @@ import math
 
 import torch
 
-from . import kernels as K
 from .grad_sync.gpt_adapter import collect_stage_metadata
 from .loss import global_normalization_scale, gpt_loss_output, sum_loss_outputs, synthetic_gpt_batch
 from .grad_sync.executor import local_all_reduce_sum
@@ -415,7 +414,9 @@ class FirstLastStageTrainer:
         return functools.reduce(lambda a, b: a + b, [w[0] for w, _ in weights])
 
     def tie_gradients(self):
-        K.tied_grad_sum(self.embedding.word_embeddings.weight.main_grad, self.post.word_embeddings.weight.main_grad)
+        # the sum, with the root's post-sync statistics in the same pass when
+        # the sync's statistics are bound
+        self.optimizer.sum_tied_gradients(self.embedding.word_embeddings.weight, self.post.word_embeddings.weight)
 
     def train_step(self, sample_ids, labels=None):
         self.ddp.zero_grad_buffer(defer=True)

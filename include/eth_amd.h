@@ -139,6 +139,23 @@ int eth_grad_stats(const eth_chunk_t* chunks, int64_t n_chunks, float inv_loss_s
                    int flags, float* found_inf, double* partials, int64_t partial_base,
                    void* stream);
 
+/* The tied word-embedding sum fused with those post-sync statistics: for
+ * every element of the chunks (the root's fp32 main grad), s = root + copy
+ * (the copy's element at the same offset from `copy` as the root's from
+ * `root`) is stored into both, and the chunk's statistics are taken of s as
+ * eth_grad_stats(..., inv_loss_scale = loss_scale,
+ * flags = ETH_STATS_SCALED_OVERFLOW) takes them: found_inf where
+ * s * loss_scale is not finite, partials[partial_base + chunk] = sum of s^2
+ * for ETH_CHUNK_NORM chunks.  The bits equal eth_tied_grad_sum followed by
+ * that eth_grad_stats call, in one pass instead of two.  Replaces the
+ * same-rank branch of synchronize_shared_weights_grads
+ * (eth/runtime/megatron/training.py:489-531) together with the root's share
+ * of the unscale check and L2 statistic (optimizer/optimizer.py:452-453,
+ * grad_sync/optimizer_semantics.py:584-587). */
+int eth_tied_grad_sum_stats(const eth_chunk_t* chunks, int64_t n_chunks, float* root,
+                            float* copy, float loss_scale, float* found_inf,
+                            double* partials, int64_t partial_base, void* stream);
+
 /* The fp16-contract widening copy fused with the statistics: 16-bit main
  * grads (`dtype` bf16 / fp16; chunk.src, strided rows as in a bucket table)
  * into contiguous fp32 gradients out[chunk.dst ...], g = float(x) (exact),

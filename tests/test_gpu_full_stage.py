@@ -386,6 +386,59 @@ def test_first_last_update_overlapped_with_the_next_forward_is_bit_identical(cud
     assert torch.equal(over.embedding.word_embeddings.weight, over.post.word_embeddings.weight)
 
 
+@pytest.mark.parametrize("misalign", [0, 1])
+def test_tied_sum_with_statistics_equals_the_sum_then_the_statistics(cuda, misalign):
+    """eth_tied_grad_sum_stats against eth_tied_grad_sum followed by
+    eth_grad_stats(ETH_STATS_SCALED_OVERFLOW) on the same chunk table: equal
+    sums in both copies, equal per-chunk partials and flags, with a ragged
+    length, a copy 16-byte aligned or not, and an element whose loss-scaled
+    sum overflows fp32."""
+    from eth_amd import _native as nat
+    from eth_amd.grad_sync.executor import chunk_table, split_block
+
+    announce(f"tied sum + statistics, copy misaligned by {misalign}")
+    n, scale = 100_003, 1024.0
+    gen = torch.Generator(device="cuda").manual_seed(21)
+    c0 = (n + 3) // 4 * 4 + 4 + misalign  # the copy's first element (16-byte aligned when misalign is 0)
+    base = torch.randn(c0 + n, generator=gen, device="cuda")
+    for overflow in (False, True):
+        a, b = base.clone(), base.clone()
+        if overflow:
+            for buf in (a, b):
+                buf[12_345] = 2e35
+                buf[c0 + 12_345] = 2e35  # sum 4e35, x 1024 > fp32 max
+        results = []
+        for buf, fused in ((a, False), (b, True)):
+            root, copy = buf[:n], buf[c0 : c0 + n]
+            entries = []
+            split_block(root.data_ptr(), 4, 1, n, n, 0, 1.0, nat.CHUNK_NORM, entries)
+            table = nat.table_to_device(chunk_table(entries), cuda)
+            flag = torch.zeros(1, device="cuda")
+            part = torch.full((len(entries) + 2,), -1.0, dtype=torch.float64, device="cuda")
+            stream = nat.stream_ptr(cuda)
+            if fused:
+                nat.call("eth_tied_grad_sum_stats", nat.ptr(table), len(entries), nat.ptr(root), nat.ptr(copy),
+                         scale, nat.ptr(flag), nat.ptr(part), 2, stream)
+            else:
+                K.tied_grad_sum(root, copy) if misalign == 0 else _tied_sum_unaligned(root, copy)
+                nat.call("eth_grad_stats", nat.ptr(table), len(entries), scale, nat.STATS_SCALED_OVERFLOW,
+                         nat.ptr(flag), nat.ptr(part), 2, stream)
+            torch.cuda.synchronize()
+            results.append((root.clone(), copy.clone(), part.clone(), flag.item()))
+        (ra, ca, pa, fa), (rb, cb, pb, fb) = results
+        assert torch.equal(ra, rb) and torch.equal(ca, cb) and torch.equal(ra, ca)
+        assert torch.equal(pa, pb) and pa[0].item() == pa[1].item() == -1.0
+        assert fa == fb == (1.0 if overflow else 0.0)
+
+
+def _tied_sum_unaligned(root, copy):
+    """The tied sum of fp32 tensors that eth_tied_grad_sum (16-byte aligned
+    only) does not take, in torch: the same one fp32 add per element."""
+    s = root + copy
+    root.copy_(s)
+    copy.copy_(s)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("mode", ["fused", "standalone", "overlapped"])
 def test_shared_tied_storage_is_bit_identical_to_two_copies(cuda, dtype, mode):
@@ -471,8 +524,9 @@ def test_first_last_fused_statistics_match_the_standalone_pass(cuda, dtype):
     from eth_amd.loss import global_normalization_scale
 
     tr.grad_sync.execute(global_normalization_scale(tr.nominal, lo.local_loss_weight))
-    tr.tie_gradients()
+    # (the tied sum takes the root's post-sync statistics in the same pass)
     tr.embedding.word_embeddings.weight.main_grad[7, 3] = float("inf")
+    tr.tie_gradients()
     before = tr.embedding.word_embeddings.weight.detach().clone()
     ok, norm, _ = tr.optimizer.step()
     torch.cuda.synchronize()
@@ -485,8 +539,9 @@ def test_first_last_fused_statistics_match_the_standalone_pass(cuda, dtype):
     tr.ddp.zero_grad_buffer()
     _, lo = tr.forward_backward([5, 9])
     tr.grad_sync.execute(global_normalization_scale(tr.nominal, lo.local_loss_weight))
+    tr.embedding.word_embeddings.weight.main_grad[7, 3] = 1e36  # the sum x 1024 > fp32 max
+    tr.post.word_embeddings.weight.main_grad[7, 3] = 0.0
     tr.tie_gradients()
-    tr.embedding.word_embeddings.weight.main_grad[7, 3] = 1e36  # x 1024 > fp32 max
     ok, norm, _ = tr.optimizer.step()
     torch.cuda.synchronize()
     assert not ok and norm is None
