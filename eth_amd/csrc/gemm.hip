@@ -88,7 +88,7 @@ __device__ __forceinline__ void dma_barrier_but() {
 // Map a linear workgroup id to (tile_m, tile_n): XCD-contiguous, then
 // GROUP_M-row grouped.
 __device__ __forceinline__ void tile_coords(int pid, int tiles_m, int tiles_n, int& tm, int& tn) {
-  constexpr int kXcds = 8, kGroupM = 8;
+  constexpr int kXcds = 8, kGroupM = 4;
   const int total = tiles_m * tiles_n;
   const int per = (total + kXcds - 1) / kXcds;
   const int tall = total % kXcds == 0 ? kXcds : total % kXcds;
