@@ -453,6 +453,8 @@ def synthetic_batch(sample_ids, seq, vocab, device):
     """tokens [b, s] int64, loss_mask [b, s] fp32, position_ids [b, s] int64
     of the deterministic synthetic batch, computed on the device in one
     launch per 64 samples (the ids cross as a host array)."""
+    if isinstance(sample_ids, torch.Tensor):
+        sample_ids = sample_ids.detach().cpu()  # the ids travel to the kernel by value
     ids = np.ascontiguousarray(np.asarray(sample_ids, dtype=np.int64).reshape(-1))
     b = ids.size
     if seq <= 0 or vocab <= 0:

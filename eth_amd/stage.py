@@ -379,8 +379,9 @@ class FirstLastStageTrainer:
                 resynced=[self.embedding.word_embeddings.weight, self.post.word_embeddings.weight])
         if overlap_optimizer:
             # the update of each part overlaps the next step's forward up to
-            # that part's first op; the tied head copy, read last, updates
-            # under the whole forward
+            # that part's first op; a tied head copy of its own (without
+            # shared storage), read last, updates under the whole forward,
+            # a shared one with the embedding's part
             self.optimizer.overlap_with_next_forward(update_parts(ops))
         self.nominal = float(cfg.micro_batch_size * cfg.seq_length)
         self._host_weights = []
