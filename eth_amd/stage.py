@@ -371,9 +371,10 @@ class FirstLastStageTrainer:
         if self.ddp.accumulate_allreduce_grads_in_fp32 and math.frexp(initial_loss_scale)[0] == 0.5:
             # unscale and inf/nan flag fused into the sync's unpack; the tied
             # word embedding, summed after the sync, gets its norm share and
-            # overflow check in one pass over the root at the step (exact
-            # because a power-of-two loss scale -- which the dynamic scaler
-            # keeps -- unscales each addend without rounding)
+            # overflow check in the pass of the tied sum (exact because a
+            # power-of-two loss scale -- which the dynamic scaler keeps --
+            # unscales each addend without rounding, short of subnormal
+            # results)
             self.optimizer.bind_gradient_sync(
                 self.grad_sync.executor,
                 resynced=[self.embedding.word_embeddings.weight, self.post.word_embeddings.weight])
