@@ -74,6 +74,8 @@ SIGNATURES = {
     "eth_gemm_splitk": [_P, _I64, _I32, _P, _I64, _I32, _P, _I64, _I64, _I64, _I64, _I32, _I32, _I32, _P, _P],
     "eth_ln_fwd": [_P, _P, _P, _P, _P, _P, _I64, _I64, _F32, _I32, _P],
     "eth_ln_bwd": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I32, _I32, _P],
+    "eth_ln_fwd_sb": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _F32, _I32, _P],
+    "eth_ln_bwd_sb": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I32, _I32, _P],
     "eth_bias_gelu_fwd": [_P, _P, _P, _I64, _I64, _I32, _P],
     "eth_bias_gelu_bwd": [_P, _P, _P, _P, _I64, _I64, _I32, _P],
     "eth_bias_dropout_add_fwd": [_P, _P, _P, _P, _I64, _I64, _F32, ctypes.c_uint64, _I32, _P],

@@ -38,6 +38,15 @@ __device__ __forceinline__ uint16_t cvt_out(float v) {
   return FP16 ? f2h_bits(v) : f2bf(v);
 }
 
+// Row r of a [batch, seq] view of an x stored [seq, batch] (trb = batch;
+// 0 leaves rows as they are): the transposed LayerNorm reads and writes x
+// there while y, mean, rstd and dy stay in [batch, seq] row order.
+__device__ __forceinline__ int sb_row(int r, int rows, int trb) {
+  if (!trb) return r;
+  const int seq = rows / trb;
+  return (r % seq) * trb + r / seq;
+}
+
 // Each lane handles VPL vectors of 8 elements: cols == VPL * 8 * 64 * ... we
 // loop in strides of 512 elements (64 lanes x 8).
 template <int NV, bool FP16>
@@ -47,11 +56,11 @@ __global__ void __launch_bounds__(64 * kLnWaves) ln_fwd_kernel(const uint16_t* _
                                                                uint16_t* __restrict__ y,
                                                                float* __restrict__ mean,
                                                                float* __restrict__ rstd, int rows,
-                                                               int cols, float eps) {
+                                                               int cols, float eps, int trb) {
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * kLnWaves + (threadIdx.x >> 6);
   if (row >= rows) return;
-  const uint16_t* xr = x + (int64_t)row * cols;
+  const uint16_t* xr = x + (int64_t)sb_row(row, rows, trb) * cols;
   float v[NV][8];
   float s = 0.f;
 #pragma unroll
@@ -230,7 +239,8 @@ template <int T, int NVW, bool FP16, bool RESID, bool CSUM>
 __global__ void __launch_bounds__(64 * kLnBwdWaves) ln_bwd_kernel(
     const uint16_t* __restrict__ dy, const uint16_t* __restrict__ x, const float* __restrict__ mean,
     const float* __restrict__ rstd, const uint16_t* __restrict__ gamma, const uint16_t* __restrict__ dres,
-    uint16_t* __restrict__ dx, float* __restrict__ part, float* __restrict__ cpart, int rows, int cols) {
+    uint16_t* __restrict__ dx, float* __restrict__ part, float* __restrict__ cpart, int rows, int cols,
+    int trb) {
   constexpr int TEAMS = kLnBwdWaves / T;
   constexpr int NQ = CSUM ? 3 : 2;
   const int lane = threadIdx.x & 63;
@@ -264,7 +274,8 @@ __global__ void __launch_bounds__(64 * kLnBwdWaves) ln_bwd_kernel(
   auto load_row = [&](int k) __attribute__((always_inline)) {
     const bool live = k < nrows;
     const int r = g + k * G;
-    const __amdgpu_buffer_rsrc_t xr = row_rsrc(x, r, cols, live), dr = row_rsrc(dy, r, cols, live);
+    const __amdgpu_buffer_rsrc_t xr = row_rsrc(x, live ? sb_row(r, rows, trb) : r, cols, live);
+    const __amdgpu_buffer_rsrc_t dr = row_rsrc(dy, r, cols, live);
 #pragma unroll
     for (int i = 0; i < NVW; ++i) {
       nx[i] = __builtin_amdgcn_raw_buffer_load_b128(xr, voff + i * 1024, 0, 0);
@@ -327,7 +338,7 @@ __global__ void __launch_bounds__(64 * kLnBwdWaves) ln_bwd_kernel(
       asm volatile("" : "+v"(g16[i]));
     }
     if (valid) {
-      const __amdgpu_buffer_rsrc_t orow = row_rsrc(dx, r, cols);
+      const __amdgpu_buffer_rsrc_t orow = row_rsrc(dx, sb_row(r, rows, trb), cols);
 #pragma unroll
       for (int i = 0; i < NVW; ++i) {
         ln_u32x4 o;
@@ -394,12 +405,12 @@ inline int ln_bwd_groups(int64_t rows, int64_t cols) {
 
 template <bool FP16>
 static void launch_fwd(const uint16_t* x, const uint16_t* g, const uint16_t* b, uint16_t* y, float* mean,
-                       float* rstd, int rows, int cols, float eps, hipStream_t s) {
+                       float* rstd, int rows, int cols, float eps, hipStream_t s, int trb = 0) {
   const int grid = (rows + kLnWaves - 1) / kLnWaves;
   const int nv = (cols + 511) / 512;
   switch (nv) {
 #define ETH_LN_CASE(N) \
-  case N: ln_fwd_kernel<N, FP16><<<grid, 64 * kLnWaves, 0, s>>>(x, g, b, y, mean, rstd, rows, cols, eps); break;
+  case N: ln_fwd_kernel<N, FP16><<<grid, 64 * kLnWaves, 0, s>>>(x, g, b, y, mean, rstd, rows, cols, eps, trb); break;
     ETH_LN_CASE(1) ETH_LN_CASE(2) ETH_LN_CASE(3) ETH_LN_CASE(4) ETH_LN_CASE(5) ETH_LN_CASE(6)
     ETH_LN_CASE(7) ETH_LN_CASE(8) ETH_LN_CASE(9) ETH_LN_CASE(10) ETH_LN_CASE(11) ETH_LN_CASE(12)
     ETH_LN_CASE(13) ETH_LN_CASE(14) ETH_LN_CASE(15) ETH_LN_CASE(16)
@@ -430,12 +441,12 @@ static void launch_bda_ln(const uint16_t* x, const uint16_t* bias, const uint16_
 template <bool FP16, bool RESID, bool CSUM>
 static void launch_bwd(const uint16_t* dy, const uint16_t* x, const float* mean, const float* rstd,
                        const uint16_t* g, const uint16_t* dres, uint16_t* dx, float* part, float* cpart,
-                       int groups, int rows, int cols, hipStream_t s) {
+                       int groups, int rows, int cols, hipStream_t s, int trb) {
   const int nv = (cols + 511) / 512;
   const dim3 block(64 * kLnBwdWaves);
 #define ETH_LN_BWD(T, N)                                                                              \
   ln_bwd_kernel<T, N, FP16, RESID, CSUM><<<groups, block, 0, s>>>(dy, x, mean, rstd, g, dres, dx, part, \
-                                                                  cpart, rows, cols)
+                                                                  cpart, rows, cols, trb)
   if (nv == 1) ETH_LN_BWD(1, 1);
   else if (nv == 2) ETH_LN_BWD(1, 2);
   else if (nv <= 4) ETH_LN_BWD(2, 2);
@@ -507,13 +518,13 @@ extern "C" int64_t eth_ln_bwd_workspace(int64_t rows, int64_t cols) {
 template <bool RESID, bool CSUM>
 static void ln_bwd_dispatch(const void* dy, const void* x, const float* mean, const float* rstd,
                             const void* gamma, const void* dresid, void* dx, float* part, float* cpart,
-                            int groups, int rows, int cols, int dtype, hipStream_t s) {
+                            int groups, int rows, int cols, int dtype, hipStream_t s, int trb = 0) {
   if (dtype == ETH_BF16)
     launch_bwd<false, RESID, CSUM>((const uint16_t*)dy, (const uint16_t*)x, mean, rstd, (const uint16_t*)gamma,
-                                   (const uint16_t*)dresid, (uint16_t*)dx, part, cpart, groups, rows, cols, s);
+                                   (const uint16_t*)dresid, (uint16_t*)dx, part, cpart, groups, rows, cols, s, trb);
   else
     launch_bwd<true, RESID, CSUM>((const uint16_t*)dy, (const uint16_t*)x, mean, rstd, (const uint16_t*)gamma,
-                                  (const uint16_t*)dresid, (uint16_t*)dx, part, cpart, groups, rows, cols, s);
+                                  (const uint16_t*)dresid, (uint16_t*)dx, part, cpart, groups, rows, cols, s, trb);
 }
 
 extern "C" int eth_ln_bwd_residual(const void* dy, const void* x, const float* mean, const float* rstd,
@@ -557,4 +568,57 @@ extern "C" int eth_ln_bwd(const void* dy, const void* x, const float* mean, cons
                           void* stream) {
   return eth_ln_bwd_residual(dy, x, mean, rstd, gamma, nullptr, dx, dgamma, dbeta, nullptr, workspace, rows, cols,
                              accumulate, dtype, stream);
+}
+
+// The LayerNorm of a [seq, batch, cols] input written as [batch, seq, cols]
+// (and its backward, taking dy in [batch, seq] order and writing dx as
+// [seq, batch]): the same kernels, reading and writing x through the row
+// permutation, so the results are those of the transposed copy followed by
+// eth_ln_fwd / eth_ln_bwd bit for bit.
+extern "C" int eth_ln_fwd_sb(const void* x, const void* gamma, const void* beta, void* y, float* mean,
+                             float* rstd, int64_t seq, int64_t batch, int64_t cols, float eps, int dtype,
+                             void* stream) {
+  ETH_CHECK_ARG(dtype == ETH_BF16 || dtype == ETH_F16, "eth_ln_fwd_sb: dtype must be bf16/fp16");
+  ETH_CHECK_ARG(seq >= 0 && batch >= 0 && seq * batch < (1LL << 31) && cols > 0 && cols <= kMaxCols &&
+                    cols % 8 == 0,
+                "eth_ln_fwd_sb: bad sizes (seq %lld, batch %lld, cols %lld)", (long long)seq, (long long)batch,
+                (long long)cols);
+  if (seq * batch == 0) return ETH_OK;
+  ETH_CHECK_ARG(x && gamma && beta && y && mean && rstd, "eth_ln_fwd_sb: null pointer");
+  hipStream_t s = (hipStream_t)stream;
+  const int rows = (int)(seq * batch);
+  if (dtype == ETH_BF16)
+    launch_fwd<false>((const uint16_t*)x, (const uint16_t*)gamma, (const uint16_t*)beta, (uint16_t*)y,
+                      mean, rstd, rows, (int)cols, eps, s, (int)batch);
+  else
+    launch_fwd<true>((const uint16_t*)x, (const uint16_t*)gamma, (const uint16_t*)beta, (uint16_t*)y,
+                     mean, rstd, rows, (int)cols, eps, s, (int)batch);
+  ETH_CHECK_LAUNCH("eth_ln_fwd_sb");
+  return ETH_OK;
+}
+
+extern "C" int eth_ln_bwd_sb(const void* dy, const void* x, const float* mean, const float* rstd,
+                             const void* gamma, void* dx, float* dgamma, float* dbeta, float* workspace,
+                             int64_t seq, int64_t batch, int64_t cols, int accumulate, int dtype,
+                             void* stream) {
+  ETH_CHECK_ARG(dtype == ETH_BF16 || dtype == ETH_F16, "eth_ln_bwd_sb: dtype must be bf16/fp16");
+  ETH_CHECK_ARG(seq >= 0 && batch >= 0 && seq * batch < (1LL << 31) && cols > 0 && cols <= kMaxCols &&
+                    cols % 8 == 0,
+                "eth_ln_bwd_sb: bad sizes (seq %lld, batch %lld, cols %lld)", (long long)seq, (long long)batch,
+                (long long)cols);
+  const int64_t rows = seq * batch;
+  if (rows == 0) return ETH_OK;
+  ETH_CHECK_ARG(dy && x && mean && rstd && gamma && dx && dgamma && dbeta && workspace,
+                "eth_ln_bwd_sb: null pointer");
+  ETH_CHECK_ARG((((uintptr_t)workspace | (uintptr_t)dy | (uintptr_t)x | (uintptr_t)dx | (uintptr_t)gamma) & 15u) == 0,
+                "eth_ln_bwd_sb: operands must be 16-byte aligned");
+  const int groups = (int)eth_ln_bwd_groups(rows, cols);
+  hipStream_t s = (hipStream_t)stream;
+  ln_bwd_dispatch<false, false>(dy, x, mean, rstd, gamma, nullptr, dx, workspace, nullptr, groups, (int)rows,
+                                (int)cols, dtype, s, (int)batch);
+  ETH_CHECK_LAUNCH("eth_ln_bwd_sb");
+  reduce_partials_kernel<<<reduce_partials_grid((int)cols, 2), kReducePartialsThreads, 0, s>>>(
+      workspace, groups, (int)cols, 2 * cols, dgamma, dbeta, accumulate);
+  ETH_CHECK_LAUNCH("eth_ln_bwd_sb reduce");
+  return ETH_OK;
 }

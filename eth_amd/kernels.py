@@ -188,6 +188,44 @@ def layer_norm_fwd(x, gamma, beta, eps=1e-5):
     return y, mean, rstd
 
 
+def layer_norm_fwd_sb(x, gamma, beta, eps=1e-5):
+    """LayerNorm of a contiguous [s, b, h] x returned as [b, s, h] (the
+    final LayerNorm after .transpose(0, 1).contiguous(), without the copy);
+    mean / rstd in the output's row order."""
+    code = _check_half(x, gamma, beta)
+    if x.dim() != 3 or not x.is_contiguous():
+        raise ValueError("x must be a contiguous [s, b, h] tensor")
+    s, b, h = x.shape
+    if gamma.numel() != h or beta.numel() != h:
+        raise ValueError("gamma/beta must match the normalized size")
+    y = torch.empty(b, s, h, dtype=x.dtype, device=x.device)
+    mean = torch.empty(b * s, dtype=torch.float32, device=x.device)
+    rstd = torch.empty(b * s, dtype=torch.float32, device=x.device)
+    nat.call("eth_ln_fwd_sb", nat.ptr(x), nat.ptr(gamma), nat.ptr(beta), nat.ptr(y), nat.ptr(mean), nat.ptr(rstd),
+             s, b, h, float(eps), code, nat.stream_ptr(x.device))
+    return y, mean, rstd
+
+
+def layer_norm_bwd_sb(dy, x, mean, rstd, gamma, dgamma, dbeta, accumulate):
+    """Backward of layer_norm_fwd_sb: dy [b, s, h], x [s, b, h] -> dx [s, b, h];
+    dgamma/dbeta fp32 stored or accumulated in place."""
+    code = _check_half(dy, x, gamma)
+    if x.dim() != 3 or not x.is_contiguous():
+        raise ValueError("x must be a contiguous [s, b, h] tensor")
+    s, b, h = x.shape
+    if tuple(dy.shape) != (b, s, h) or not dy.is_contiguous():
+        raise ValueError("dy must be a contiguous [b, s, h] tensor")
+    for t in (dgamma, dbeta):
+        if t.dtype != torch.float32 or t.numel() != h or not t.is_contiguous():
+            raise ValueError("dgamma/dbeta must be contiguous fp32 [cols]")
+    ws = torch.empty(nat.value("eth_ln_bwd_workspace", s * b, h), dtype=torch.float32, device=x.device)
+    dx = torch.empty_like(x)
+    nat.call("eth_ln_bwd_sb", nat.ptr(dy), nat.ptr(x), nat.ptr(mean), nat.ptr(rstd), nat.ptr(gamma), nat.ptr(dx),
+             nat.ptr(dgamma), nat.ptr(dbeta), nat.ptr(ws), s, b, h, 1 if accumulate else 0, code,
+             nat.stream_ptr(x.device))
+    return dx
+
+
 def layer_norm_bwd(dy, x, mean, rstd, gamma, dgamma, dbeta, accumulate, dresid=None, colsum=False):
     """dx (returned); dgamma/dbeta fp32 stored or accumulated in place.
 

@@ -16,7 +16,8 @@ from dataclasses import dataclass
 import torch
 from torch import nn
 
-from .functional import BiasDropoutAddFn, BiasDropoutAddLayerNormFn, BiasGeluFn, CausalAttentionFn, SplitQKVFn
+from .functional import (BiasDropoutAddFn, BiasDropoutAddLayerNormFn, BiasGeluFn, CausalAttentionFn, SplitQKVFn,
+                         TransposedLayerNormFn)
 from .layers import ColumnParallelLinear, LayerNorm, RowParallelLinear, init_method_normal
 
 
@@ -91,6 +92,11 @@ class ParallelLayerNormOp(RopalaModule):
 
     def forward(self, input_tensors, input_extra_tensors, output_extra_tensors, profiling=False):
         hidden = input_tensors["hidden_states"]
+        if self.name == "final-layernorm" and not self.output_extra_tensors_info:
+            # hidden.transpose(0, 1).contiguous() and the LayerNorm, the
+            # [s, b, h] -> [b, s, h] permutation inside the LayerNorm kernels
+            ln = self.input_layernorm
+            return {"hidden_states": TransposedLayerNormFn.apply(hidden, ln.weight, ln.bias, ln.eps)}
         if self.name == "final-layernorm":
             hidden = hidden.transpose(0, 1).contiguous()
         if not self.output_extra_tensors_info:

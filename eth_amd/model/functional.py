@@ -147,6 +147,35 @@ class LayerNormFn(torch.autograd.Function):
         return dx.view(x.shape), dg.to(gamma.dtype), db.to(beta.dtype), None
 
 
+class TransposedLayerNormFn(torch.autograd.Function):
+    """The final LayerNorm of the GPT stage, x.transpose(0, 1).contiguous()
+    then MixedFusedLayerNorm (flex_ops.py final-layernorm, :552-553): [s, b, h]
+    in, [b, s, h] out, with the row permutation done by the LayerNorm
+    kernels' own reads and writes instead of two transposing copies."""
+
+    @staticmethod
+    def forward(ctx, x, gamma, beta, eps):
+        xc = x.contiguous()
+        y, mean, rstd = K.layer_norm_fwd_sb(xc, gamma, beta, eps)
+        ctx.save_for_backward(xc, gamma, beta, mean, rstd)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, gamma, beta, mean, rstd = ctx.saved_tensors
+        dg, db, acc = _pair_target(gamma, beta)
+        own = dg is None
+        if own:
+            dg = torch.empty(gamma.shape, dtype=torch.float32, device=x.device)
+            db = torch.empty(beta.shape, dtype=torch.float32, device=x.device)
+        dx = K.layer_norm_bwd_sb(dy.contiguous(), x, mean, rstd, gamma, dg, db, accumulate=acc)
+        if not own:
+            grad_written(gamma)
+            grad_written(beta)
+            return dx, None, None, None
+        return dx, dg.to(gamma.dtype), db.to(beta.dtype), None
+
+
 class LayerNormResidualFn(torch.autograd.Function):
     """MixedFusedLayerNorm whose input also feeds a later residual add:
     returns (LayerNorm(x), x).  The second output is what the op publishes

@@ -267,6 +267,23 @@ int64_t eth_ln_bwd_workspace(int64_t rows, int64_t cols);
 int eth_ln_bwd(const void* dy, const void* x, const float* mean, const float* rstd,
                const void* gamma, void* dx, float* dgamma, float* dbeta, float* workspace,
                int64_t rows, int64_t cols, int accumulate, int dtype, void* stream);
+
+/* The final LayerNorm of a GPT stage with its transpose folded in: x is a
+ * [seq, batch, cols] tensor, y is written [batch, seq, cols], mean / rstd in
+ * y's row order (eth_ln_fwd_sb); the backward takes dy [batch, seq, cols]
+ * and writes dx [seq, batch, cols] (eth_ln_bwd_sb, workspace as for
+ * eth_ln_bwd with rows = seq * batch).  The kernels of eth_ln_fwd /
+ * eth_ln_bwd read and write x through the row permutation, so the results
+ * equal a transposed copy followed by those calls bit for bit.
+ * Replaces hidden_states.transpose(0, 1).contiguous() + FusedLayerNorm of
+ * the final-layernorm op (eth/runtime/megatron/model/flex_ops.py:552-553)
+ * and the copy its backward makes. */
+int eth_ln_fwd_sb(const void* x, const void* gamma, const void* beta, void* y, float* mean,
+                  float* rstd, int64_t seq, int64_t batch, int64_t cols, float eps, int dtype,
+                  void* stream);
+int eth_ln_bwd_sb(const void* dy, const void* x, const float* mean, const float* rstd,
+                  const void* gamma, void* dx, float* dgamma, float* dbeta, float* workspace,
+                  int64_t seq, int64_t batch, int64_t cols, int accumulate, int dtype, void* stream);
 /* LayerNorm backward fused with the residual branch that read the same
  * input: dx = bf16(bf16(dx_ln) + dresid), the sum autograd forms when a
  * tensor feeds both the LayerNorm and the later residual add

@@ -159,6 +159,44 @@ def test_layer_norm_fwd_bwd(cuda, dtype, rows, cols):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("seq,batch,cols", [(2048, 2, 4096), (37, 3, 1032), (64, 4, 2048), (5, 1, 8), (1, 7, 256)])
+def test_transposed_layer_norm_equals_the_copy_then_layer_norm(cuda, dtype, seq, batch, cols):
+    """The final LayerNorm with its [s, b, h] -> [b, s, h] transpose folded
+    into the kernels (eth_ln_fwd_sb / eth_ln_bwd_sb) against
+    .transpose(0, 1).contiguous() + eth_ln_fwd / eth_ln_bwd: y, mean, rstd,
+    dx (transposed back) and the accumulated dgamma / dbeta bit for bit, and
+    y against the fp32 oracle."""
+    announce(f"transposed layernorm {dtype} s{seq} b{batch} h{cols}")
+    gen = torch.Generator().manual_seed(seq * 7 + batch * 3 + cols)
+    x = (_rand((seq, batch, cols), dtype, gen, 2.0) + 0.5).to(cuda)
+    g = (1 + _rand((cols,), torch.float32, gen, 0.1)).to(dtype).to(cuda)
+    b = _rand((cols,), dtype, gen, 0.1).to(cuda)
+    dy = _rand((batch, seq, cols), dtype, gen).to(cuda)
+    y1, m1, r1 = K.layer_norm_fwd_sb(x, g, b)
+    xt = x.transpose(0, 1).contiguous()
+    y2, m2, r2 = K.layer_norm_fwd(xt.view(-1, cols), g, b)
+    assert torch.equal(y1.view(-1, cols), y2) and torch.equal(m1, m2) and torch.equal(r1, r2)
+    _close(y1.cpu().view(-1, cols), ol.layer_norm(xt.float().cpu().view(-1, cols), g.float().cpu(), b.float().cpu()),
+           dtype, "transposed ln fwd")
+    outs = []
+    for sb in (True, False):
+        dg = torch.full((cols,), 0.5, device=cuda)
+        db = torch.full((cols,), -0.25, device=cuda)
+        if sb:
+            dx = K.layer_norm_bwd_sb(dy, x, m1, r1, g, dg, db, accumulate=True)
+        else:
+            dx = K.layer_norm_bwd(dy.view(-1, cols), xt.view(-1, cols), m2, r2, g, dg, db, accumulate=True)
+            dx = dx.view(batch, seq, cols).transpose(0, 1).contiguous()
+        outs.append((dx, dg, db))
+    for a, c in zip(*outs):
+        assert torch.equal(a, c)
+    with pytest.raises(ValueError):  # dy in the input's [s, b] order
+        K.layer_norm_bwd_sb(dy.transpose(0, 1).contiguous(), x, m1, r1, g, dg, db, accumulate=False)
+    with pytest.raises(ValueError):  # not a 3-D [s, b, h] input
+        K.layer_norm_fwd_sb(x.view(-1, cols), g, b)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("rows,cols", [(300, 256), (1000, 2048), (2100, 1032), (33, 4096), (5, 8), (40, 1536), (17, 8192)])
 def test_layer_norm_bwd_residual_colsum(cuda, dtype, rows, cols):
     """LayerNorm backward fused with the residual gradient: dx equals the
