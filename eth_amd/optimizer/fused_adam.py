@@ -183,12 +183,18 @@ class FusedAdamW(torch.optim.Optimizer):
             for ttab, ctab, n_chunks in self._tables
         ]
         self._launched = [False] * len(self._launches)
-        self.part_events = [torch.cuda.Event() for _ in self._launches] if self._partition else []
+        if not self._partition:
+            self.part_events = []
+        elif len(self.part_events) != len(self._launches):
+            # one event per part, re-recorded every step (a wait already
+            # queued on it keeps the recording it was queued behind)
+            self.part_events = [torch.cuda.Event() for _ in self._launches]
         if not deferred:
             for k in range(len(self._launches)):
                 self.launch_part(k)
         self._pending_step = step
-        if found_inf is None:
+        if found_inf is None and not deferred:
+            # (a deferred step's caller commits once its first parts are out)
             self.commit_step(True)
         return loss
 

@@ -85,7 +85,10 @@ class MegatronOptimizer:
         return self.get_loss_scale() * loss
 
     def _device(self):
-        return self.get_parameters()[0].device
+        dev = getattr(self, "_dev", None)
+        if dev is None:
+            dev = self._dev = self.get_parameters()[0].device
+        return dev
 
     def state_for_model_parameter(self, model_parameter):
         p = self._model_to_optimizer_param.get(id(model_parameter))
@@ -144,8 +147,7 @@ class MegatronOptimizer:
         if k not in self._unlaunched_parts:
             return
         self._unlaunched_parts.discard(k)
-        for p in model_parts[k]:
-            p._eth_update_launch = None
+        # (the parameters keep their launch hook: a second call returns above)
         side.wait_stream(torch.cuda.current_stream(self._device()))
         with torch.cuda.stream(side):
             self.optimizer.launch_part(k)
@@ -459,6 +461,9 @@ class MegatronOptimizer:
                 for p in part:
                     p._eth_ready_event = ev
                     p._eth_update_launch = launch
+            if scaler is None:
+                # no overflow to wait for: the step counters advance now
+                self.optimizer.commit_step(True)
         if host is not None:
             host[1].synchronize()
         if scaler is not None:
