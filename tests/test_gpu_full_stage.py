@@ -485,6 +485,54 @@ def test_shared_tied_storage_is_bit_identical_to_two_copies(cuda, dtype, mode):
         assert float(s1["step"]) == float(s2["step"]) == 3.0, name
 
 
+@pytest.mark.parametrize("case", ["microbatches", "fp16_main_grads"])
+def test_shared_tied_storage_in_microbatches_and_fp16_main_grads(cuda, tmp_path, case):
+    """The shared tied storage against two updated copies where the step
+    takes other paths: two microbatches per step (the loss weights of both
+    forwards read from their pinned copies and summed on the host), and fp16
+    main grads (the reference's fp16 contract: 16-bit tied sum, the widening
+    statistics pass).  Losses, norms, parameters, masters and moments are
+    bit-identical over two steps, and so are the post_step evidence
+    snapshots of every parameter."""
+    from eth_amd.grad_sync.evidence import load_rank_snapshot
+
+    announce(f"shared tied storage: {case}")
+    cfg = GPTConfig(hidden_size=256, num_attention_heads=4, ffn_hidden_size=1024, num_layers=2, seq_length=128,
+                    micro_batch_size=2, padded_vocab_size=50304, params_dtype=torch.float16, device="cuda", seed=23)
+    kw = dict(lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01, clip_grad=0.05, initial_loss_scale=1024.0,
+              accumulate_allreduce_grads_in_fp32=case != "fp16_main_grads")
+    two = FirstLastStageTrainer(cfg, share_tied_storage=False, **kw)
+    one = FirstLastStageTrainer(cfg, **kw)
+    assert one.post.word_embeddings.weight.data_ptr() == one.embedding.word_embeddings.weight.data_ptr()
+    gen = torch.Generator(device="cuda").manual_seed(29)
+    for step in range(2):
+        if case == "microbatches":
+            ids = [[3 + step, 8 + step], [11 + step, 2 + step]]
+            labels = [torch.randint(0, 50257, (2, 128), generator=gen, device="cuda") for _ in ids]
+            l2, (n2_, w2), ok2, norm2 = two.train_step_microbatches(ids, labels)
+            l1, (n1_, w1), ok1, norm1 = one.train_step_microbatches(ids, labels)
+            assert torch.equal(n1_, n2_) and torch.equal(w1, w2)
+            assert all(torch.equal(a, b) for a, b in zip(l1, l2))
+        else:
+            labels = torch.randint(0, 50257, (2, 128), generator=gen, device="cuda")
+            l2, _, ok2, norm2 = two.train_step([3 + step, 8 + step], labels)
+            l1, _, ok1, norm1 = one.train_step([3 + step, 8 + step], labels)
+            assert torch.equal(l1, l2)
+        assert ok1 and ok2 and norm1 == norm2, (step, norm1, norm2)
+    paths = [tr.record_evidence(tmp_path / name, "post_step", 2) for tr, name in ((one, "one"), (two, "two"))]
+    torch.cuda.synchronize()
+    snaps = [load_rank_snapshot(p_) for p_ in paths]
+    assert len(snaps[0]["records"]) == len(snaps[1]["records"]) == len(one.bindings)
+    for r1, r2 in zip(*(s_["records"] for s_ in snaps)):
+        name = r1["descriptor"]["logical_param_id"]
+        assert name == r2["descriptor"]["logical_param_id"]
+        for key in ("parameter", "main_grad", "optimizer_parameter"):
+            assert torch.equal(r1[key], r2[key]), (name, key)
+        for key in ("exp_avg", "exp_avg_sq", "step"):
+            assert torch.equal(r1["optimizer_state"][key], r2["optimizer_state"][key]), (name, key)
+        assert r1["optimizer_hyperparameters"] == r2["optimizer_hyperparameters"], name
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_first_last_fused_statistics_match_the_standalone_pass(cuda, dtype):
     """The first+last stage unscales in the sync's unpack and takes the tied
