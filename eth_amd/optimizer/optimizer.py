@@ -383,6 +383,18 @@ class MegatronOptimizer:
 
     @torch.no_grad()
     def step(self):
+        st = self.gather_statistics()
+        return self.apply_statistics(st)
+
+    @torch.no_grad()
+    def gather_statistics(self):
+        """The first half of step(): the pending update joined, the model
+        grads copied to the main grads, and the statistics passes queued
+        (found_inf and the per-chunk partial sums of squares, before the norm
+        is finalized).  Returns the statistics (None when the step needs
+        neither a norm nor an overflow check).  Stages that clip by one norm
+        combine their statistics between the two halves
+        (step_model_parallel_group)."""
         self.join_overlapped_update()
         self._copy_model_grads_to_main_grads()
         scaler = self.grad_scaler
@@ -413,11 +425,22 @@ class MegatronOptimizer:
             self._standalone_statistics(unscale=False, stats=False)
         if st is not None:
             st.fresh = False
+        return st if (scaler is not None or need_norm) else None
+
+    @torch.no_grad()
+    def apply_statistics(self, st, partials=None, n_partials=None):
+        """The second half of step(): finalize the norm from `partials`
+        (default: the statistics' own), read the norm and the overflow flag
+        back, and update.  Returns (update_successful, grad_norm, num_zeros)."""
+        scaler = self.grad_scaler
+        need_norm = self.clip_grad > 0.0
         if need_norm:
+            if partials is None:
+                partials, n_partials = st.partials, st.n_partials_used
             nat.call(
                 "eth_grad_norm_finalize",
-                nat.ptr(st.partials),
-                st.n_partials_used,
+                nat.ptr(partials),
+                n_partials,
                 self.clip_grad,
                 nat.ptr(st.stats),
                 nat.stream_ptr(self._device()),
@@ -653,6 +676,50 @@ class FP32Optimizer(MegatronOptimizer):
         if self.params_have_main_grad:
             for p in self.get_parameters():
                 p.grad = p.main_grad
+
+
+@torch.no_grad()
+def step_model_parallel_group(optimizers):
+    """One optimizer step of several pipeline stages that share one GPU, as
+    the ranks of one model-parallel group step together: the clip norm is
+    the L2 norm over every stage's gradients (clip_grads.py:100-113 sums the
+    ranks' squared norms over the model-parallel group), the overflow flag
+    is the maximum of the stages' flags (optimizer.py:449-461 takes it over
+    every rank), so every stage skips or applies the step alike, and the
+    zero count is the sum (clip_grads.py:150-155).  The stages' partial sums of squares are joined
+    into one vector that every stage finalizes its norm from, in fp64.
+    Returns [(update_successful, grad_norm, num_zeros)] per stage."""
+    if not optimizers:
+        return []
+    clip = {o.clip_grad for o in optimizers}
+    scaled = {o.grad_scaler is not None for o in optimizers}
+    if len(clip) != 1 or len(scaled) != 1:
+        raise ValueError("the stages of one group must clip alike and all (or none) scale the loss")
+    if scaled == {True} and len({o.grad_scaler.host_scale for o in optimizers}) != 1:
+        raise ValueError("the stages of one group must hold one loss scale")
+    devices = {o._device() for o in optimizers}
+    if len(devices) != 1:
+        raise ValueError("the in-process group steps stages of one GPU")
+    sts = [o.gather_statistics() for o in optimizers]
+    if sts[0] is None:
+        return [o.apply_statistics(None) for o in optimizers]
+    if scaled == {True}:
+        flag = sts[0].found_inf.clone()
+        for st in sts[1:]:
+            torch.maximum(flag, st.found_inf, out=flag)
+        for st in sts:
+            st.found_inf.copy_(flag)
+    partials, n = None, None
+    if clip.pop() > 0.0:
+        parts = [st.partials[: st.n_partials_used] for st in sts if st.n_partials_used]
+        partials = torch.cat(parts) if parts else sts[0].partials
+        n = sum(st.n_partials_used for st in sts)
+    out = [o.apply_statistics(st, partials, n) for o, st in zip(optimizers, sts)]
+    zeros = [z for _, _, z in out]
+    if all(z is not None for z in zeros):
+        total = float(sum(zeros))
+        out = [(ok, norm, total) for ok, norm, _ in out]
+    return out
 
 
 def get_params_for_weight_decay_optimization(modules, layernorm_types=()):
