@@ -90,9 +90,11 @@ def _resolve(root, path):
     return functools.reduce(lambda obj, attr: getattr(obj, attr, None) if obj is not None else None, path.split("."), root)
 
 
-def collect_stage_metadata(ops, stage_op_begin, stage_op_end, model_impl="gpt", manifest_hash="manifest"):
+def collect_stage_metadata(ops, stage_op_begin, stage_op_end, model_impl="gpt", manifest_hash="manifest",
+                           global_rank=0):
     """Descriptors and main_grad bindings of every trainable parameter of the
-    stage's ops (single rank)."""
+    stage's ops, held by `global_rank` alone (no tensor or data
+    parallelism; pipeline stages of one process take ranks 0, 1, ...)."""
     descriptors, bindings = [], []
     for op in ops:
         layer = (op.op_index - 1) // 10 if op.name.startswith("enc-") else None
@@ -101,23 +103,23 @@ def collect_stage_metadata(ops, stage_op_begin, stage_op_end, model_impl="gpt", 
             p = _resolve(op, path)
             if p is None:
                 if required:
-                    raise ValueError(f"logical_param_id {lid} rank 0 is missing {path}")
+                    raise ValueError(f"logical_param_id {lid} rank {global_rank} is missing {path}")
                 continue
             if id(p) in seen:
-                raise ValueError(f"duplicate parameter for logical_param_id {lid} rank 0")
+                raise ValueError(f"duplicate parameter for logical_param_id {lid} rank {global_rank}")
             seen.add(id(p))
             if not p.requires_grad:
                 continue
             mg = getattr(p, "main_grad", None)
             if mg is None:
-                raise ValueError(f"logical_param_id {lid} rank 0 is missing main_grad")
+                raise ValueError(f"logical_param_id {lid} rank {global_rank} is missing main_grad")
             tp = bool(p.tensor_model_parallel)
             pdim = int(p.partition_dim)
             if tp and pdim < 0:
                 pdim += p.dim()
             actual = f"sharded_dim{pdim}" if tp else "replicated"
             if actual != semantics:
-                raise ValueError(f"logical_param_id {lid} rank 0 expected {semantics}, got {actual}")
+                raise ValueError(f"logical_param_id {lid} rank {global_rank} expected {semantics}, got {actual}")
             shape = tuple(int(s) for s in p.shape)
             descriptors.append(
                 SerializableGradientDescriptor(
@@ -126,11 +128,11 @@ def collect_stage_metadata(ops, stage_op_begin, stage_op_end, model_impl="gpt", 
                     shared_weight_root=shared_root,
                     logical_region_key=lid,
                     semantic_order_key=(op.op_index, order, lid),
-                    global_rank=0,
+                    global_rank=global_rank,
                     model_impl=model_impl,
                     op_manifest_hash=manifest_hash,
                     pipeline_id=0,
-                    stage_id=0,
+                    stage_id=global_rank,
                     model_chunk_id=0,
                     global_op_index=op.op_index,
                     manifest_op_name=op.name,
@@ -144,9 +146,9 @@ def collect_stage_metadata(ops, stage_op_begin, stage_op_end, model_impl="gpt", 
                     local_dp_rank=0,
                     local_cp_degree=1,
                     local_cp_rank=0,
-                    stage_ranks=(0,),
-                    local_tp_group_ranks=(0,),
-                    local_dp_group_ranks=(0,),
+                    stage_ranks=(global_rank,),
+                    local_tp_group_ranks=(global_rank,),
+                    local_dp_group_ranks=(global_rank,),
                     full_shape=shape,
                     local_shape=shape,
                     tensor_parallel=tp,
@@ -161,5 +163,5 @@ def collect_stage_metadata(ops, stage_op_begin, stage_op_end, model_impl="gpt", 
             bindings.append(LocalGradientBinding(logical_param_id=lid, parameter=p, main_grad=mg, device=p.device))
         unlisted = {id(p) for p in op.parameters() if p.requires_grad} - seen
         if unlisted:
-            raise ValueError(f"unlisted trainable parameter on rank 0 op {op.op_index} ({op.name})")
+            raise ValueError(f"unlisted trainable parameter on rank {global_rank} op {op.op_index} ({op.name})")
     return tuple(descriptors), tuple(bindings)

@@ -27,6 +27,7 @@ import collections
 
 import torch
 
+from .loss import global_normalization_scale, sum_loss_outputs
 from .optimizer.optimizer import step_model_parallel_group
 
 
@@ -107,7 +108,10 @@ def forward_backward_pipelining_without_interleaving(stages, microbatches, forwa
     a time).  Each microbatch is a dict with `input_tensors` (and optionally
     `input_extra_tensors`) for the first stage and `output_grads` (and
     optionally `output_extra_grads`) for the last one -- the upstream
-    gradient of the last stage's outputs, standing in for its loss.
+    gradient of the last stage's outputs, standing in for its loss.  A GPT
+    pipeline's first and last stages (PipelineStageTrainer) read
+    `sample_ids` (and optionally `labels`) instead: the first builds its
+    tokens from them and the last ends in the loss.
 
     Returns (results, timeline): per microbatch (outputs of the last stage,
     its output extra tensors, input gradients of the first stage, its input
@@ -136,15 +140,18 @@ def forward_backward_pipelining_without_interleaving(stages, microbatches, forwa
                 if r > 0 and not StageLink._ready(links[r - 1].forward, tick, mb):
                     continue
                 if r == 0:
-                    ins = microbatches[mb]["input_tensors"]
+                    ins = microbatches[mb].get("input_tensors")
                     extras = microbatches[mb].get("input_extra_tensors")
                 else:
                     ins, extras = links[r - 1].recv_forward(mb)
+                # stages that read the batch (a first stage's tokens, a last
+                # stage's loss mask and labels) get the microbatch too
+                kw = {"microbatch": microbatches[mb]} if getattr(stages[r], "takes_microbatch", False) else {}
                 if forward_only:
                     with torch.no_grad():
-                        out, out_extra, leaves = stages[r].forward_step(ins, extras)
+                        out, out_extra, leaves = stages[r].forward_step(ins, extras, **kw)
                 else:
-                    out, out_extra, leaves = stages[r].forward_step(ins, extras)
+                    out, out_extra, leaves = stages[r].forward_step(ins, extras, **kw)
                     saved[r].append((mb, out, out_extra, leaves))
                     peak[r] = max(peak[r], len(saved[r]))
                 if r < p - 1:
@@ -156,7 +163,8 @@ def forward_backward_pipelining_without_interleaving(stages, microbatches, forwa
                 if r < p - 1 and not StageLink._ready(links[r].backward, tick, mb):
                     continue
                 if r == p - 1:
-                    grads = microbatches[mb]["output_grads"]
+                    # (none for a stage that ends in the loss)
+                    grads = microbatches[mb].get("output_grads")
                     extra_grads = microbatches[mb].get("output_extra_grads")
                 else:
                     grads, extra_grads = links[r].recv_backward(mb)
@@ -186,10 +194,12 @@ def forward_backward_pipelining_without_interleaving(stages, microbatches, forwa
 class PipelineTrainer:
     """A training step of several pipeline stages on one GPU: the
     microbatches through the stages in the 1F1B order, then each stage's
-    gradient sync and one optimizer step for the group, with one clip norm
-    and one overflow decision over all stages (the train_step of
-    pipeline-parallel ranks, training.py:904-1020).  `stages` are MiddleStageTrainer objects in
-    pipeline order."""
+    gradient sync, the tied word-embedding gradients summed across the
+    first and last stages, and one optimizer step for the group, with one
+    clip norm and one overflow decision over all stages (the train_step of
+    pipeline-parallel ranks, training.py:904-1020).  `stages` are
+    MiddleStageTrainer objects in pipeline order, or PipelineStageTrainer
+    objects from the embedding to the loss."""
 
     def __init__(self, stages, schedule="1f1b"):
         if schedule not in SCHEDULES:
@@ -197,12 +207,45 @@ class PipelineTrainer:
         self.stages = list(stages)
         self.schedule = schedule
         self.last_timeline = None
+        self.loss_stage = getattr(self.stages[-1], "is_last", False)
+        self.last_loss = None
+        if self.loss_stage and not getattr(self.stages[0], "is_first", False):
+            raise ValueError("a pipeline that ends in the loss starts at the embedding")
+
+    def tie_embeddings(self):
+        """Give the LM head's copy of the word embedding the root's values
+        and reload the last stage's fp32 masters from them (the copy starts
+        from the root, training.py:349-470)."""
+        first, last = self.stages[0], self.stages[-1]
+        if not self.loss_stage or first is last:
+            return
+        with torch.no_grad():
+            last.tied_copy.copy_(first.tied_root)
+        last.optimizer.reload_model_params()
+
+    def _tie_gradients(self):
+        """synchronize_shared_weights_grads (training.py:489-531): root and
+        copy main grads both become their sum; the root's optimizer takes
+        the sum's statistics (its norm share and overflow check), which the
+        group's step shares with the copy's stage."""
+        if not self.loss_stage:
+            return
+        first, last = self.stages[0], self.stages[-1]
+        first.optimizer.sum_tied_gradients(first.tied_root, last.tied_copy)
 
     def train_step(self, microbatches, normalization_scale=1.0):
         """Returns (results as forward_backward_pipelining_without_interleaving
-        gives them, [(update_successful, grad_norm, num_zeros)] per stage)."""
+        gives them, [(update_successful, grad_norm, num_zeros)] per stage).
+        A pipeline that ends in the loss normalizes by the step's nominal
+        token count over its summed loss weight (global_normalization_scale)
+        and leaves the summed (numerator, weight) in `last_loss`."""
         if hasattr(normalization_scale, "item"):
             normalization_scale = float(normalization_scale.item())
+        last = self.stages[-1]
+        if self.loss_stage:
+            cfg = last.cfg
+            nominal = float(len(microbatches) * cfg.micro_batch_size * cfg.seq_length)
+            last.begin_step(nominal)
         for s in self.stages:
             s.ddp.zero_grad_buffer(defer=True)
         results, self.last_timeline = forward_backward_pipelining_without_interleaving(
@@ -210,5 +253,42 @@ class PipelineTrainer:
         for s in self.stages:
             s.optimizer.join_overlapped_update()
             s.ddp.settle_grad_buffer()
+        if self.loss_stage:
+            self.last_loss = sum_loss_outputs(last.loss_outputs)
+            normalization_scale = global_normalization_scale(nominal, last.step_loss_weight())
+        for s in self.stages:
             s.grad_sync.execute(normalization_scale)
+        self._tie_gradients()
         return results, step_model_parallel_group([s.optimizer for s in self.stages])
+
+
+def build_gpt_pipeline(cfg, cuts, schedule="1f1b", **stage_kwargs):
+    """A GPT pipeline of PipelineStageTrainer stages over the consecutive
+    op ranges `cuts` (from the embedding, op 0, to the loss, the last op),
+    stage r holding rank r.  As the manager plans it across ranks
+    (manager.py:122-214), every stage's gradient-sync plan comes from the
+    descriptors of all stages -- the word embedding's root on the first
+    stage and its copy on the last form one shared weight -- and each
+    stage runs its own rank's buckets.  The head's copy of the word
+    embedding starts from the root.  Returns the PipelineTrainer."""
+    from .stage import PipelineStageTrainer
+
+    n_ops = 10 * cfg.num_layers + 3
+    cuts = [tuple(c) for c in cuts]
+    if not cuts or cuts[0][0] != 0 or cuts[-1][1] != n_ops or any(
+            a[1] != b[0] or a[0] >= a[1] for a, b in zip(cuts, cuts[1:] + [(n_ops, n_ops + 1)])):
+        raise ValueError(f"cuts {cuts} do not split ops [0, {n_ops}) into consecutive stages")
+    stages = [PipelineStageTrainer(cfg, cut, global_rank=r, defer_grad_sync=True, **stage_kwargs)
+              for r, cut in enumerate(cuts)]
+    parts = [tuple(st.descriptors) for st in stages]
+
+    def gather(obj):  # the descriptor exchange; the plan hash is checked below
+        return list(parts) if isinstance(obj, tuple) else [obj]
+
+    for st in stages:
+        st.finish_setup(gather)
+    if len({st.grad_sync.plan.global_plan_hash for st in stages}) != 1:
+        raise ValueError("gradient sync plan hash mismatch across stages")
+    pipe = PipelineTrainer(stages, schedule=schedule)
+    pipe.tie_embeddings()
+    return pipe

@@ -62,7 +62,7 @@ def save_stage_snapshot(trainer, output_dir, phase, iteration, metrics=None, clo
         output_dir,
         phase=phase,
         iteration=iteration,
-        global_rank=0,
+        global_rank=getattr(trainer, "global_rank", 0),
         descriptors=trainer.descriptors,
         runtime_bindings=bindings,
         optimizer_state_by_logical=state,
@@ -98,7 +98,9 @@ def _fp32_main_grads(cfg, requested):
 class MiddleStageTrainer:
     """A middle pipeline stage (no embedding, no head): whole layers
     `[first_layer, first_layer + num_layers)`, or any manifest op range
-    `op_range = (op_start, op_end)` that may cut a layer."""
+    `op_range = (op_start, op_end)` that may cut a layer.  `model` (a
+    FlexGPTModel) replaces both; `resynced` names parameters whose main
+    grads change after the sync (a tied word embedding)."""
 
     def __init__(
         self,
@@ -118,42 +120,70 @@ class MiddleStageTrainer:
         runtime_evidence_dir=None,
         overlap_optimizer=False,
         accumulate_allreduce_grads_in_fp32=True,
+        model=None,
+        initial_loss_scale=2.0**32,
+        resynced=(),
+        global_rank=0,
+        defer_grad_sync=False,
     ):
         if cfg.params_dtype not in (torch.bfloat16, torch.float16):
             raise ValueError("the stage trains in bf16 or fp16")
         fp32_grads = _fp32_main_grads(cfg, accumulate_allreduce_grads_in_fp32)
         self.cfg = cfg
-        if op_range is not None:
+        self.global_rank = global_rank
+        if model is not None:
+            self.model = model
+        elif op_range is not None:
             self.model = op_range_stage(cfg, *op_range, recompute_ops=recompute_ops)
         else:
             self.model = middle_stage(cfg, first_layer, num_layers, recompute_ops=recompute_ops)
         self.ddp = DistributedDataParallel(self.model, accumulate_allreduce_grads_in_fp32=fp32_grads)
         lm = self.model.language_model
-        self.descriptors, self.bindings = collect_stage_metadata(lm.ops, self.model.op_start, self.model.op_end)
+        self.descriptors, self.bindings = collect_stage_metadata(lm.ops, self.model.op_start, self.model.op_end,
+                                                                 global_rank=global_rank)
+        self._setup = dict(sync_mode=sync_mode, bucket_cap_bytes=bucket_cap_bytes, all_reduce_sum=all_reduce_sum,
+                           runtime_evidence_dir=runtime_evidence_dir, lr=lr, weight_decay=weight_decay, betas=betas,
+                           eps=eps, clip_grad=clip_grad, initial_loss_scale=initial_loss_scale, fp32_grads=fp32_grads,
+                           resynced=list(resynced), overlap_optimizer=overlap_optimizer)
+        if not defer_grad_sync:
+            self.finish_setup()
+
+    def finish_setup(self, all_gather_object=None):
+        """The gradient-sync plan and the optimizer.  The plan covers the
+        descriptors `all_gather_object(own descriptors)` returns -- those of
+        every stage of a pipeline built in one process (a stage built alone
+        plans from its own) -- and this stage runs its rank's share of it."""
+        o = self._setup
+        cfg = self.cfg
+        gather = {} if all_gather_object is None else {"all_gather_object": all_gather_object}
         self.grad_sync = initialize_gradient_sync(
             self.descriptors,
             self.bindings,
-            global_rank=0,
+            global_rank=self.global_rank,
             expected_pipeline_ids=(0,),
-            sync_mode=sync_mode,
-            bucket_cap_bytes=bucket_cap_bytes,
-            all_reduce_sum=all_reduce_sum or local_all_reduce_sum,
-            runtime_evidence_dir=runtime_evidence_dir,
+            sync_mode=o["sync_mode"],
+            bucket_cap_bytes=o["bucket_cap_bytes"],
+            all_reduce_sum=o["all_reduce_sum"] or local_all_reduce_sum,
+            runtime_evidence_dir=o["runtime_evidence_dir"],
+            **gather,
         )
         self.optimizer = get_megatron_optimizer(
             [self.model],
-            lr=lr,
-            weight_decay=weight_decay,
-            betas=betas,
-            eps=eps,
-            clip_grad=clip_grad,
+            lr=o["lr"],
+            weight_decay=o["weight_decay"],
+            betas=o["betas"],
+            eps=o["eps"],
+            clip_grad=o["clip_grad"],
             bf16=cfg.params_dtype == torch.bfloat16,
             fp16=cfg.params_dtype == torch.float16,
+            initial_loss_scale=o["initial_loss_scale"],
         )
-        if fp32_grads:
-            # 16-bit main grads are widened and unscaled by the optimizer
-            self.optimizer.bind_gradient_sync(self.grad_sync.executor)
-        if overlap_optimizer:
+        # (16-bit main grads are widened and unscaled by the optimizer; a
+        # re-synced tied gradient is unscaled addend by addend by the sync,
+        # exact only for a power-of-two loss scale)
+        if o["fp32_grads"] and (not o["resynced"] or math.frexp(o["initial_loss_scale"])[0] == 0.5):
+            self.optimizer.bind_gradient_sync(self.grad_sync.executor, resynced=o["resynced"])
+        if o["overlap_optimizer"]:
             self.optimizer.overlap_with_next_forward(update_parts(self.model.language_model.ops))
         # buckets synced during the backward, as soon as their gradients
         # exist (train_step(streamed_sync=True))
@@ -458,3 +488,109 @@ class FirstLastStageTrainer:
 
     def record_evidence(self, output_dir, phase, iteration, metrics=None, clock=None, run_metadata=None):
         return save_stage_snapshot(self, output_dir, phase, iteration, metrics, clock, run_metadata)
+
+
+class PipelineStageTrainer(MiddleStageTrainer):
+    """One stage of a GPT pipeline: manifest ops [op_start, op_end) of the
+    whole model.  The first stage holds the embedding and builds its input
+    from the microbatch's sample ids; the last one holds the final
+    LayerNorm, the tied LM head and the loss contract, and backpropagates
+    numerator / nominal times the loss scale (forward_step and backward_step,
+    schedules.py:62-111,196-227; grad_sync/loss.py:16-39).  Both read the
+    microbatch, as get_batch does on the first and last stages; the pipeline
+    driver (eth_amd.schedules) hands it to every forward.  The defaults are
+    the first+last stage's (AdamW betas 0.9 / 0.999, weight decay 0.01,
+    loss scale 2^16)."""
+
+    takes_microbatch = True
+
+    def __init__(self, cfg: GPTConfig, op_range, unpadded_vocab=50257, lr=1e-4, betas=(0.9, 0.999), eps=1e-8,
+                 weight_decay=0.01, clip_grad=1.0, initial_loss_scale=2.0**16, sync_mode="block",
+                 bucket_cap_bytes=1024 * 1024, recompute_ops=None, runtime_evidence_dir=None,
+                 overlap_optimizer=False, accumulate_allreduce_grads_in_fp32=True, global_rank=0,
+                 defer_grad_sync=False):
+        lo, hi = op_range
+        n_ops = 10 * cfg.num_layers + 3
+        model = FlexGPTModel(cfg, lo, hi, recompute_ops=recompute_ops)
+        ops = model.language_model.ops
+        self.is_first, self.is_last = lo == 0, hi == n_ops
+        # the tied word embedding: the root in the embedding op, the copy in
+        # the LM head's op
+        self.tied_root = ops[0].word_embeddings.weight if self.is_first else None
+        self.tied_copy = ops[-1].word_embeddings.weight if self.is_last else None
+        if self.is_first and self.is_last:
+            with torch.no_grad():  # the head copy starts from the root (training.py:349-470)
+                self.tied_copy.copy_(self.tied_root)
+        self.unpadded_vocab = unpadded_vocab
+        self.nominal = float(cfg.micro_batch_size * cfg.seq_length)
+        self._host_weights = []
+        self.loss_outputs = []
+        super().__init__(cfg, lr=lr, betas=betas, eps=eps, weight_decay=weight_decay, clip_grad=clip_grad,
+                         sync_mode=sync_mode, bucket_cap_bytes=bucket_cap_bytes, recompute_ops=recompute_ops,
+                         runtime_evidence_dir=runtime_evidence_dir, overlap_optimizer=overlap_optimizer,
+                         accumulate_allreduce_grads_in_fp32=accumulate_allreduce_grads_in_fp32, model=model,
+                         initial_loss_scale=initial_loss_scale,
+                         resynced=[p for p in (self.tied_root, self.tied_copy) if p is not None],
+                         global_rank=global_rank, defer_grad_sync=defer_grad_sync)
+
+    def begin_step(self, nominal):
+        """Start a step whose nominal loss scale (the step's global token
+        count, config_normalization.py:535-541) is `nominal`."""
+        self.nominal = float(nominal)
+        self._host_weights = []
+        self.loss_outputs = []
+
+    def _batch(self, microbatch):
+        if microbatch is None or "sample_ids" not in microbatch:
+            raise ValueError("a first or last stage needs the microbatch's sample ids")
+        dev = next(self.model.parameters()).device
+        tokens, mask, positions, _ = synthetic_gpt_batch(microbatch["sample_ids"], self.cfg.seq_length,
+                                                         self.unpadded_vocab, dev, attention_mask=False)
+        return tokens, mask, positions
+
+    def forward_step(self, input_tensors, input_extra_tensors=None, microbatch=None):
+        """The stage's forward of one microbatch.  A last stage returns
+        ({"loss": numerator / nominal, "losses": per-token loss [b, s]}, {},
+        leaves) and keeps the microbatch's LossOutput."""
+        if not (self.is_first or self.is_last):
+            return super().forward_step(input_tensors, input_extra_tensors)
+        tokens, mask, positions = self._batch(microbatch)
+        extras = {k: v.detach().requires_grad_(v.is_floating_point())
+                  for k, v in (input_extra_tensors or {}).items()}
+        if self.is_first:
+            ins, inputs = {}, {"enc_input_ids": tokens, "enc_position_ids": positions}
+        else:
+            ins = {k: v.detach().requires_grad_(True) for k, v in input_tensors.items()}
+            self.model.set_input_tensor(ins)
+            inputs = None
+        run_extras = dict(extras)
+        if self.is_last and microbatch.get("labels") is not None:
+            run_extras["labels"] = microbatch["labels"]
+        result = self.model(inputs, run_extras)
+        if not self.is_last:
+            out, out_extra = result
+            return out, out_extra, (ins, extras)
+        losses = result["output"]
+        lo = gpt_loss_output(losses, mask, self.nominal)
+        self._host_weights.append(_weight_to_host(lo.local_loss_weight))
+        self.loss_outputs.append(lo)
+        return {"loss": lo.local_loss_sum / lo.nominal_global_loss_scale, "losses": losses}, {}, (ins, extras)
+
+    def backward_step(self, outputs, output_grads, output_extra_tensors=None, output_extra_grads=None, leaves=None):
+        """A last stage backpropagates its loss times the loss scale
+        (schedules.py:214-217); the others take the next stage's gradients."""
+        if not self.is_last:
+            return super().backward_step(outputs, output_grads, output_extra_tensors, output_extra_grads, leaves)
+        with overlapped_wgrad():
+            torch.autograd.backward(self.optimizer.scale_loss(outputs["loss"]))
+        ins, extras = leaves if leaves is not None else ({}, {})
+        zero = lambda t: t.grad if t.grad is not None else torch.zeros_like(t)  # noqa: E731
+        return {k: zero(t) for k, t in ins.items()}, {k: zero(t) for k, t in extras.items() if t.is_floating_point()}
+
+    def step_loss_weight(self):
+        """The step's summed loss weight as a host tensor (the pinned copies
+        queued after each forward's loss; waits for those forwards only)."""
+        weights, self._host_weights = self._host_weights, []
+        for _, ev in weights:
+            ev.synchronize()
+        return functools.reduce(lambda a, b: a + b, [w[0] for w, _ in weights])

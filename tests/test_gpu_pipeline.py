@@ -2,16 +2,20 @@
 (schedules.py:595-713, p2p_communication.py:200-538): the pipelined order
 against one microbatch at a time, bit for bit, with cuts at and inside a
 layer; the step's one clip norm over all stages and its AdamW result
-against the fp32 oracle; and one overflow decision for every stage."""
+against the fp32 oracle; one overflow decision for every stage; and a GPT
+pipeline from the embedding to the loss, with the tied word embedding
+split between its first and last stages, against the first+last stage and
+the fp64 oracle."""
 
 import numpy as np
 import pytest
 import torch
 
+from eth_amd.loss import global_normalization_scale
 from eth_amd.model.flex_ops import GPTConfig
 from eth_amd.optimizer.optimizer import step_model_parallel_group
-from eth_amd.schedules import PipelineTrainer, forward_backward_pipelining_without_interleaving
-from eth_amd.stage import MiddleStageTrainer
+from eth_amd.schedules import PipelineTrainer, build_gpt_pipeline, forward_backward_pipelining_without_interleaving
+from eth_amd.stage import FirstLastStageTrainer, MiddleStageTrainer
 from oracle import adamw as oadam
 from oracle import gradsync as og
 from oracle import layer as ol
@@ -195,3 +199,160 @@ def test_an_overflow_on_one_stage_skips_every_stage(cuda):
     after = _masters(stages)
     for a, b in zip(before, after):
         assert any(not torch.equal(a[n], b[n]) for n in a)
+
+
+# ------------------------------------------------------------ GPT pipeline --
+N_OPS = 23  # embedding, 2 x 10 layer ops, final LayerNorm, LM head + loss
+
+
+def _gpt_cfg(dtype):
+    return GPTConfig(hidden_size=H, num_attention_heads=HEADS, ffn_hidden_size=FFN, num_layers=2, seq_length=SEQ,
+                     micro_batch_size=1, padded_vocab_size=50304, params_dtype=dtype, device="cuda", seed=11)
+
+
+def _gpt_pipeline(cuts, whole, dtype, **kw):
+    """A GPT pipeline over `cuts` holding the weights of the first+last
+    stage `whole`, the tied copy initialised from the root."""
+    pipe = build_gpt_pipeline(_gpt_cfg(dtype), cuts, **kw)
+    assert [st.global_rank for st in pipe.stages] == list(range(len(cuts)))
+    by_index = {op.op_index: op for op in whole.model.language_model.ops}
+    for st in pipe.stages:
+        with torch.no_grad():
+            for op in st.model.language_model.ops:
+                for (n1, p1), (n2, p2) in zip(op.named_parameters(), by_index[op.op_index].named_parameters()):
+                    assert n1 == n2
+                    p1.copy_(p2)
+        st.optimizer.reload_model_params()
+    pipe.tie_embeddings()
+    return pipe
+
+
+def _by_op(trainers):
+    """{(op index, parameter name): parameter} over the trainers' ops."""
+    out = {}
+    for tr in trainers:
+        for op in tr.model.language_model.ops:
+            for n, p in op.named_parameters():
+                out[(op.op_index, n)] = p
+    return out
+
+
+GPT_CUTS = [((0, 11), (11, N_OPS)), ((0, 6), (6, 16), (16, N_OPS)), ((0, N_OPS),)]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("cuts", GPT_CUTS)
+def test_gpt_pipeline_step_equals_the_first_last_stage(cuda, cuts, dtype):
+    """Embedding to loss in 1, 2 or 3 stages (cuts at a layer boundary, and
+    inside both layers), four one-sample microbatches in the 1F1B order,
+    against the same model on one first+last stage running them one at a
+    time: per-token losses, the summed loss, every synced and tied main
+    grad equal bit for bit, one norm, and the fp32 masters after the step
+    within 1e-6.  The one exception: where a cut separates a bias-dropout-add
+    from the LayerNorm after it (which one stage runs as one fused kernel),
+    the bias gradient of the linear before it is summed by the unfused
+    kernel, in another order, and agrees to 1e-6."""
+    announce(f"GPT pipeline {cuts} {dtype} vs first+last")
+    whole = FirstLastStageTrainer(_gpt_cfg(dtype))
+    pipe = _gpt_pipeline(cuts, whole, dtype)
+    ids = [[3], [8], [5], [1]]
+    losses, (num, weight), ok, norm = whole.train_step_microbatches(ids)
+    results, steps = pipe.train_step([{"sample_ids": i} for i in ids])
+    torch.cuda.synchronize()
+    assert ok and all(o for o, _, _ in steps)
+    for (out, _e, in_g, _x), ref in zip(results, losses):
+        assert torch.equal(out["losses"], ref) and in_g == {}
+    p_num, p_weight = pipe.last_loss
+    assert torch.equal(p_num, num) and torch.equal(p_weight, weight)
+    assert len({n for _, n, _ in steps}) == 1
+    assert steps[0][1] == pytest.approx(norm, rel=1e-9)
+    mine, ref = _by_op(pipe.stages), _by_op([whole])
+    assert sorted(mine) == sorted(ref)
+    stage_of = {key: st for st in pipe.stages for key in _by_op([st])}
+    # a stage that ends in a dropout op (index 5 or 0 mod 10) hands the
+    # LayerNorm after it to the next stage
+    split = {(hi - 2, "dense.bias") for _, hi in cuts[:-1] if (hi - 1) % 10 in (5, 0)}
+    for key, p in ref.items():
+        if key in split:
+            assert _rel(mine[key].main_grad, p.main_grad) < 1e-6, key
+        else:
+            assert torch.equal(mine[key].main_grad, p.main_grad), key
+        got = stage_of[key].optimizer.optimizer_parameter_for_model_parameter(mine[key]).detach()
+        want = whole.optimizer.optimizer_parameter_for_model_parameter(p).detach()
+        assert _rel(got, want) < 1e-6, key
+    # the tied copies stay equal
+    assert torch.equal(pipe.stages[0].tied_root, pipe.stages[-1].tied_copy)
+
+
+def test_gpt_pipeline_gradients_match_the_fp64_oracle(cuda):
+    """Two one-sample microbatches through a 2-stage GPT pipeline: the
+    per-token losses and the synced, tied main grads against the fp64
+    oracle of the whole model on the 2-sample batch (the gradient of the
+    masked mean over both samples): losses within 2e-2, each gradient's norm
+    within 2e-2 and its relative error within 5e-2."""
+    announce("GPT pipeline vs fp64 oracle")
+    from eth_amd.loss import synthetic_gpt_batch
+    from tests.test_gpu_full_stage import _oracle_params, tr_layer_params
+
+    whole = FirstLastStageTrainer(_gpt_cfg(torch.bfloat16))
+    params = _oracle_params(whole)
+    pipe = _gpt_pipeline(GPT_CUTS[0], whole, torch.bfloat16)
+    tokens, mask, positions, _ = synthetic_gpt_batch([3, 8], SEQ, 50257, "cpu")
+    ref_losses, ref_mean, grads = ol.full_model_fwd_bwd(tokens, positions, mask, params, HEADS)
+    results, steps = pipe.train_step([{"sample_ids": [3]}, {"sample_ids": [8]}])
+    torch.cuda.synchronize()
+    assert all(o for o, _, _ in steps)
+    assert _rel(torch.cat([r[0]["losses"] for r in results]), ref_losses) < 2e-2
+    num, weight = pipe.last_loss
+    assert abs((num / weight).item() - ref_mean.item()) < 2e-2 * abs(ref_mean.item())
+    first, last = pipe.stages
+    ops0 = first.model.language_model.ops
+    ops1 = last.model.language_model.ops
+    checks = [(first.tied_root, grads["word"]), (last.tied_copy, grads["word"]),
+              (ops0[0].position_embeddings.weight, grads["pos"]),
+              (ops1[-2].input_layernorm.weight, grads["lnf_w"]), (ops1[-2].input_layernorm.bias, grads["lnf_b"])]
+    layer_params = tr_layer_params(first) + tr_layer_params(last)
+    assert len(layer_params) == 2
+    for lp, gl in zip(layer_params, grads["layers"]):
+        checks += [(p, gl[k]) for k, p in lp.items()]
+    for p, r in checks:
+        g = p.main_grad
+        gn, rn = g.double().norm().item(), r.double().norm().item()
+        assert abs(gn - rn) <= 2e-2 * rn + 1e-12
+        assert _rel(g, r) < 5e-2
+
+
+def test_gpt_pipeline_overflow_in_the_tied_sum_skips_every_stage(cuda):
+    """fp16, three stages: an inf in the LM head's copy of the word
+    embedding gradient reaches the root through the cross-stage tied sum;
+    the root's stage flags it and every stage skips the step, with its
+    masters untouched and one loss scale."""
+    announce("GPT pipeline fp16 overflow through the tied sum")
+    whole = FirstLastStageTrainer(_gpt_cfg(torch.float16))
+    pipe = _gpt_pipeline(GPT_CUTS[1], whole, torch.float16)
+    before = _masters(pipe.stages)
+    last = pipe.stages[-1]
+    mbs = [{"sample_ids": [3]}, {"sample_ids": [8]}]
+    last.begin_step(2.0 * SEQ)
+    for s in pipe.stages:
+        s.ddp.zero_grad_buffer(defer=True)
+    forward_backward_pipelining_without_interleaving(pipe.stages, mbs)
+    for s in pipe.stages:
+        s.ddp.settle_grad_buffer()
+    scale = global_normalization_scale(2.0 * SEQ, last.step_loss_weight())
+    for s in pipe.stages:
+        s.grad_sync.execute(scale)
+    with torch.no_grad():
+        last.tied_copy.main_grad.view(-1)[17] = float("inf")
+    pipe._tie_gradients()
+    steps = step_model_parallel_group([s.optimizer for s in pipe.stages])
+    torch.cuda.synchronize()
+    assert [ok for ok, _, _ in steps] == [False] * 3
+    for a, b in zip(before, _masters(pipe.stages)):
+        for name in a:
+            assert torch.equal(a[name], b[name]), name
+    assert len({s.optimizer.grad_scaler.host_scale for s in pipe.stages}) == 1
+    # the next clean step applies on every stage
+    _results, steps = pipe.train_step(mbs)
+    torch.cuda.synchronize()
+    assert [ok for ok, _, _ in steps] == [True] * 3

@@ -184,3 +184,16 @@ def test_a_schedule_that_cannot_progress_is_reported(monkeypatch):
         sch.forward_backward_pipelining_without_interleaving(stages, mbs, schedule="bad")
     with pytest.raises(ValueError, match="unknown schedule"):
         sch.forward_backward_pipelining_without_interleaving(stages, mbs, schedule="interleaved")
+
+
+def test_gpt_pipeline_cuts_must_cover_the_manifest_in_order():
+    """build_gpt_pipeline refuses cuts that leave a gap, overlap, or do not
+    run from the embedding (op 0) to the loss (op 10 L + 2) before it builds
+    any stage."""
+    from eth_amd.model.flex_ops import GPTConfig
+
+    cfg = GPTConfig(hidden_size=64, num_attention_heads=2, ffn_hidden_size=256, num_layers=2, seq_length=16,
+                    micro_batch_size=1, device="cpu")
+    for cuts in ([(1, 23)], [(0, 11), (12, 23)], [(0, 11), (10, 23)], [(0, 11), (11, 22)], [], [(0, 0), (0, 23)]):
+        with pytest.raises(ValueError, match="consecutive stages"):
+            sch.build_gpt_pipeline(cfg, cuts)
