@@ -497,6 +497,68 @@ def first_last_stage(torch, steps=5, warmup=2, overlap_optimizer=True):
     }
 
 
+def pipeline_stage_step(torch, steps=5, warmup=2, microbatches=4, overlap_optimizer=True):
+    """The C2 stage's 6 layers as two 3-layer stages in the 1F1B order
+    (eth_amd.schedules.PipelineTrainer) beside the same 6 layers as one
+    stage running the microbatches one at a time (train_step_microbatches):
+    the step's 8192 tokens as `microbatches` microbatches of one sequence,
+    one clip norm over both stages.  On one GPU the two stages run one
+    after the other, so the figures differ by the driver's host work only."""
+    from eth_amd.model.flex_ops import GPTConfig
+    from eth_amd.schedules import PipelineTrainer
+    from eth_amd.stage import MiddleStageTrainer
+
+    mb = MB * SEQ // (SEQ * microbatches)
+    kw = dict(lr=1e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, clip_grad=1.0,
+              overlap_optimizer=overlap_optimizer)
+
+    def cfg(layers):
+        return GPTConfig(hidden_size=H, num_attention_heads=HEADS, ffn_hidden_size=FFN, num_layers=layers,
+                         seq_length=SEQ, micro_batch_size=mb, params_dtype=torch.bfloat16, device="cuda", seed=1234)
+
+    g = torch.Generator(device="cuda").manual_seed(99)
+    mbs = [{"input_tensors": {"hidden_states": torch.randn(SEQ, mb, H, device="cuda", generator=g).to(torch.bfloat16)},
+            "output_grads": {"hidden_states": (torch.randn(SEQ, mb, H, device="cuda", generator=g) * 1e-3)
+                             .to(torch.bfloat16)}} for _ in range(microbatches)]
+
+    def timed(step):
+        for i in range(warmup):
+            if i == warmup - 1:
+                torch.cuda.synchronize()
+                quiet_gc()
+            step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+        return 1e3 * (time.perf_counter() - t0) / steps
+
+    one = MiddleStageTrainer(cfg(LAYERS), **kw)
+    ms_one = timed(lambda: one.train_step_microbatches(mbs))
+    del one
+    torch.cuda.empty_cache()
+    half = LAYERS // 2
+    stages = [MiddleStageTrainer(cfg(LAYERS), first_layer=0, num_layers=half, **kw),
+              MiddleStageTrainer(cfg(LAYERS), first_layer=half, num_layers=LAYERS - half, **kw)]
+    pipe = PipelineTrainer(stages)
+    ms_pipe = timed(lambda: pipe.train_step(mbs))
+    ticks = pipe.last_timeline["ticks"]
+    del pipe, stages
+    torch.cuda.empty_cache()
+    T = MB * SEQ
+    return {
+        "workload": f"C2 widths, {LAYERS} layers, {microbatches} microbatches of micro-batch {mb} x seq {SEQ} "
+                    f"({T} tokens per step), bf16",
+        "one_stage_ms_per_step": ms_one,
+        "one_stage_tokens_per_s": T / (ms_one * 1e-3),
+        "two_stage_1f1b_ms_per_step": ms_pipe,
+        "two_stage_1f1b_tokens_per_s": T / (ms_pipe * 1e-3),
+        "pipeline_ticks": ticks,
+        "steps": steps,
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -516,6 +578,8 @@ def main():
     ap.add_argument("--hbm-only", action="store_true",
                     help="time only the grad-sync and AdamW legs and their copy ceiling (for their "
                          "FETCH_SIZE / WRITE_SIZE counter runs)")
+    ap.add_argument("--pipeline-only", action="store_true",
+                    help="time only the C2 layers as two 1F1B pipeline stages beside one stage")
     ap.add_argument("--copy-probe", action="store_true",
                     help="after the timed steps, copy 1 GiB once (the calibration kernel of the "
                          "FETCH_SIZE / WRITE_SIZE counter runs behind roofline.traffic)")
@@ -540,6 +604,10 @@ def main():
         return
     if args.gemm_only:
         print(json.dumps({"gemm_layer_products": gemm_layer_products(torch)}), flush=True)
+        return
+    if args.pipeline_only:
+        print(json.dumps({"pipeline": pipeline_stage_step(torch, steps=args.steps, warmup=args.warmup,
+                                                          overlap_optimizer=not args.inline_update)}), flush=True)
         return
 
     cfg = GPTConfig(hidden_size=H, num_attention_heads=HEADS, ffn_hidden_size=FFN, num_layers=LAYERS,
