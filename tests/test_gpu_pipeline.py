@@ -356,3 +356,33 @@ def test_gpt_pipeline_overflow_in_the_tied_sum_skips_every_stage(cuda):
     _results, steps = pipe.train_step(mbs)
     torch.cuda.synchronize()
     assert [ok for ok, _, _ in steps] == [True] * 3
+
+
+def test_gpt_pipeline_overlapped_update_is_bit_identical_over_steps(cuda):
+    """Three steps of a 2-stage GPT pipeline with every stage's AdamW update
+    overlapped with its next forward against the same pipeline updating in
+    line: per-token losses of every step, norms and the fp32 masters after
+    the last step are identical (the second and third steps' forwards wait
+    for the overlapped parts op by op)."""
+    announce("GPT pipeline, overlapped update vs in line, 3 steps")
+    whole = FirstLastStageTrainer(_gpt_cfg(torch.bfloat16))
+    runs = []
+    for overlap in (False, True):
+        pipe = _gpt_pipeline(GPT_CUTS[0], whole, torch.bfloat16, overlap_optimizer=overlap)
+        losses, norms = [], []
+        for step in range(3):
+            results, steps = pipe.train_step([{"sample_ids": [3 + step]}, {"sample_ids": [8 + step]}])
+            assert all(ok for ok, _, _ in steps)
+            losses.append(torch.cat([r[0]["losses"] for r in results]))
+            norms.append(steps[0][1])
+        for st in pipe.stages:
+            st.optimizer.join_overlapped_update()
+        torch.cuda.synchronize()
+        runs.append((losses, norms, _masters(pipe.stages)))
+    (l0, n0, m0), (l1, n1, m1) = runs
+    assert n0 == n1
+    for a, b in zip(l0, l1):
+        assert torch.equal(a, b)
+    for a, b in zip(m0, m1):
+        for name in a:
+            assert torch.equal(a[name], b[name]), name
