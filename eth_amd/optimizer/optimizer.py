@@ -118,9 +118,11 @@ class MegatronOptimizer:
         launch per part of `model_param_parts` (lists of model parameters, in
         the order the next forward reads them), and leave on each model
         parameter the event after which its new value is written
-        (`_eth_ready_event`).  The stage's forward waits for those events op
-        by op, so the update of later layers overlaps the forward of earlier
-        ones; every result is the same as with the update in line."""
+        (`_eth_ready_event`, shared by the parameters of a part listed in
+        `_eth_ready_part`).  The stage's forward waits for a part's event at
+        the first op that reads one of its parameters, so the update of later
+        layers overlaps the forward of earlier ones; every result is the same
+        as with the update in line."""
         dev = self._device()
         # an optimizer parameter that serves several model parameters (a
         # shared tied copy) updates in the first part that holds one of them
@@ -162,11 +164,14 @@ class MegatronOptimizer:
         for k in sorted(self._unlaunched_parts):
             self.launch_update_part(k)
         stream = torch.cuda.current_stream(self._device())
+        waited = set()
         for part in self._overlap[1]:
             for p in part:
                 ev = getattr(p, "_eth_ready_event", None)
                 if ev is not None:
-                    stream.wait_event(ev)
+                    if id(ev) not in waited:
+                        stream.wait_event(ev)
+                        waited.add(id(ev))
                     p._eth_ready_event = None
 
     def share_tied_copy(self, root, copy):
@@ -483,6 +488,7 @@ class MegatronOptimizer:
                 launch = functools.partial(self.launch_update_part, k) if k >= eager else None
                 for p in part:
                     p._eth_ready_event = ev
+                    p._eth_ready_part = part
                     p._eth_update_launch = launch
             if scaler is None:
                 # no overflow to wait for: the step counters advance now
