@@ -142,15 +142,19 @@ class MegatronOptimizer:
         self.optimizer.set_partition(parts)
         self._overlap = (torch.cuda.Stream(device=dev), [list(part) for part in model_param_parts])
 
-    def launch_update_part(self, k):
+    def launch_update_part(self, k, wait=True):
         """Issue part k of a deferred overlapped update (once) on the side
-        stream, behind everything queued on the current stream so far."""
+        stream, behind everything queued on the current stream so far (with
+        wait=False, behind what the side stream already waited for: the
+        step's own launches, issued right after that wait, skip a second
+        one, which would cost the side stream a few microseconds)."""
         side, model_parts = self._overlap
         if k not in self._unlaunched_parts:
             return
         self._unlaunched_parts.discard(k)
         # (the parameters keep their launch hook: a second call returns above)
-        side.wait_stream(torch.cuda.current_stream(self._device()))
+        if wait:
+            side.wait_stream(torch.cuda.current_stream(self._device()))
         with torch.cuda.stream(side):
             self.optimizer.launch_part(k)
 
@@ -482,8 +486,11 @@ class MegatronOptimizer:
             # the eager parts go out before the per-parameter bookkeeping,
             # which the GPU would otherwise wait for at the step boundary
             eager = min(self.eager_update_parts, len(model_parts))
+            # (the side stream waited for the current one above; since then
+            # only the statistics read-back is queued there, which the update
+            # does not touch)
             for k in range(eager):
-                self.launch_update_part(k)
+                self.launch_update_part(k, wait=False)
             for k, (part, ev) in enumerate(zip(model_parts, self.optimizer.part_events)):
                 launch = functools.partial(self.launch_update_part, k) if k >= eager else None
                 for p in part:
