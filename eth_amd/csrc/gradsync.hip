@@ -268,11 +268,11 @@ __global__ void __launch_bounds__(kThreads) stats_kernel(const eth_chunk_t* __re
     const bool cvec = !TIED || aligned16(g + copy_off);
     const int64_t nv = n / 4;
     float4* gv = reinterpret_cast<float4*>(g);
-    for (int64_t i = threadIdx.x; i < nv; i += kThreads) {
-      float4 x = gv[i];
+    // one vector of the walk: vector i of the gradient, x its value (y the
+    // copy's, for the tied sum)
+    auto step = [&](int64_t i, float4 x, float4 y) __attribute__((always_inline)) {
       if (TIED) {
         float* cp = g + copy_off + 4 * i;
-        const float4 y = cvec ? *reinterpret_cast<const float4*>(cp) : make_float4(cp[0], cp[1], cp[2], cp[3]);
         x.x = x.x + y.x; x.y = x.y + y.y; x.z = x.z + y.z; x.w = x.w + y.w;
         gv[i] = x;
         if (cvec) {
@@ -287,7 +287,25 @@ __global__ void __launch_bounds__(kThreads) stats_kernel(const eth_chunk_t* __re
         gv[i] = x;
       }
       sq += x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w;
+    };
+    auto copy_at = [&](int64_t i) __attribute__((always_inline)) {
+      const float* cp = g + copy_off + 4 * i;
+      return cvec ? *reinterpret_cast<const float4*>(cp) : make_float4(cp[0], cp[1], cp[2], cp[3]);
+    };
+    int64_t i = threadIdx.x;
+    // four vectors per operand in flight per trip, taken in the order of
+    // the one-vector walk below (the same sums, rounded alike)
+    for (; i + 3 * kThreads < nv; i += 4 * kThreads) {
+      float4 x[4], y[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        x[u] = gv[i + u * kThreads];
+        y[u] = TIED ? copy_at(i + u * kThreads) : x[u];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) step(i + u * kThreads, x[u], y[u]);
     }
+    for (; i < nv; i += kThreads) step(i, gv[i], TIED ? copy_at(i) : gv[i]);
     for (int64_t i = nv * 4 + threadIdx.x; i < n; i += kThreads) {
       float x = g[i];
       if (TIED) g[i] = g[i + copy_off] = x = x + g[i + copy_off];
