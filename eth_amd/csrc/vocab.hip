@@ -173,8 +173,8 @@ __global__ void __launch_bounds__(kXentThreads) xent_fwd_kernel(const uint16_t* 
   const uint16_t* z = logits + row * ld;
   float m = -INFINITY, s = 0.f;
   const int64_t nv = V / 8;
-  for (int64_t i = threadIdx.x; i < nv; i += kXentThreads) {
-    uint4 a = *reinterpret_cast<const uint4*>(z + i * 8);
+  // one 8-element vector of the online max / sum-exp
+  auto fold = [&](const uint4& a) __attribute__((always_inline)) {
     const uint16_t* e = reinterpret_cast<const uint16_t*>(&a);
     float x[8], mx = m;
 #pragma unroll
@@ -186,7 +186,17 @@ __global__ void __launch_bounds__(kXentThreads) xent_fwd_kernel(const uint16_t* 
 #pragma unroll
     for (int j = 0; j < 8; ++j) s += __expf(x[j] - mx);
     m = mx;
+  };
+  int64_t i = threadIdx.x;
+  // four vectors in flight per trip, folded in the order of the walk below
+  for (; i + 3 * kXentThreads < nv; i += 4 * kXentThreads) {
+    uint4 a[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) a[u] = *reinterpret_cast<const uint4*>(z + (i + u * kXentThreads) * 8);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) fold(a[u]);
   }
+  for (; i < nv; i += kXentThreads) fold(*reinterpret_cast<const uint4*>(z + i * 8));
   for (int64_t i = nv * 8 + threadIdx.x; i < V; i += kXentThreads) {
     const float x = vin<FP16>(z[i]);
     const float mx = fmaxf(m, x);
