@@ -585,8 +585,9 @@ def main():
                          "FETCH_SIZE / WRITE_SIZE counter runs behind roofline.traffic)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: every GPU box of this build has a single MI355X and no "
-              "collective is exercised (see DESIGN.md for how the stage shards)", file=sys.stderr)
+        print("bench.py measures one GPU: every GPU box of this build has a single MI355X, so no "
+              "collective is exercised and the stage's data-, tensor- and pipeline-parallel "
+              "sharding is design only", file=sys.stderr)
         sys.exit(2)
 
     import torch
