@@ -464,3 +464,29 @@ def test_update_overlapped_with_the_next_forward_is_bit_identical(cuda):
     torch.cuda.synchronize()
     for (n1, p1), (n2, p2) in zip(plain.model.named_parameters(), over.model.named_parameters()):
         assert torch.equal(p1, p2), n1
+
+
+def test_forward_waits_once_per_update_part(cuda, monkeypatch):
+    """The next forward waits for each overlapped update part once, at the
+    first op that reads one of its parameters (every later op of the part is
+    behind that wait on the same stream), and for every part."""
+    announce("forward waits once per overlapped update part")
+    gen = torch.Generator().manual_seed(43)
+    over = MiddleStageTrainer(_cfg(layers=3), overlap_optimizer=True)
+    _randomize(over, gen)
+    x, dy = _inputs(gen)
+    over.train_step(x, dy)  # leaves its parts' events on the parameters
+    part_events = {id(e) for e in over.optimizer.optimizer.part_events}
+    assert len(part_events) == len(over.optimizer._overlap[1]) > 1
+    waits = []
+    wait_event = torch.cuda.Stream.wait_event
+
+    def counting(self, event):
+        if id(event) in part_events:
+            waits.append(id(event))
+        return wait_event(self, event)
+
+    monkeypatch.setattr(torch.cuda.Stream, "wait_event", counting)
+    over.train_step(x, dy)
+    torch.cuda.synchronize()
+    assert sorted(waits) == sorted(part_events)
