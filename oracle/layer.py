@@ -13,7 +13,7 @@ Follows eth/runtime/megatron/model/flex_ops.py:
   * fc1 + GELU: F.gelu(x + b, approximate="tanh") (flex_ops.py:60-63,1897)
   * LM head + cross entropy: logits = h @ E^T, max-subtracted
     loss = log sum exp(z - max) - (z[label] - max)
-    (model/language_model.py:126-141, mpu/cross_entropy.py:36-92)
+    (model/language_model.py:24-38, mpu/cross_entropy.py:36-92)
 """
 
 import math
