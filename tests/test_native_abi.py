@@ -31,6 +31,14 @@ def test_library_exports_every_declared_symbol():
     assert lib.eth_abi_version() >= 1
 
 
+def test_integration_guide_names_every_declared_symbol():
+    """The binding guide's export table keeps up with the header: a
+    maintainer binding the reference finds every function there."""
+    guide = (HEADER.parents[1] / "INTEGRATION.md").read_text()
+    missing = [name for name in declared_functions() if f"`{name}`" not in guide]
+    assert not missing, f"not in the integration guide: {missing}"
+
+
 def test_invalid_arguments_raise_value_error_without_gpu():
     with pytest.raises(ValueError, match="unsupported dtype"):
         nat.call("eth_bucket_pack", None, 1, None, 9, None)
